@@ -1,0 +1,108 @@
+"""exactattention_amd: certified split-KV ExactAttention on AMD Instinct MI355X (gfx950).
+
+The public names mirror the reference package (src/exactattn/__init__.py:3-14): `attention`,
+`attention_row`, `default_alpha`, `float_to_bf16_bits`, `bf16_bits_to_float32`,
+`ExactAttentionDomainError`, with the same signatures and bf16-bit-pattern dtypes. Here the rows
+are computed on the GPU by hand-written HIP kernels (libexactattn_hip.so); every returned bit
+equals the ExactAttention definition. `attention_hip` mirrors the reference's attention_triton /
+attention_cpu backends (returns (out, flags)), and `launch_hip` the device-level launcher.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import problem
+from .formats import (
+    ExactAttentionDomainError,
+    ExactAttentionUncertifiedError,
+    bf16_bits_to_float32,
+    default_alpha,
+    default_alpha_bits,
+    float_to_bf16_bits,
+    fp32_bits,
+)
+
+__all__ = [
+    "ExactAttentionDomainError",
+    "ExactAttentionUncertifiedError",
+    "attention",
+    "attention_row",
+    "attention_hip",
+    "attention_geom",
+    "bf16_bits_to_float32",
+    "default_alpha",
+    "float_to_bf16_bits",
+    "launch_hip",
+]
+
+
+def _alpha_bits(alpha) -> int:
+    return int(alpha) if isinstance(alpha, (int, np.integer)) and not isinstance(alpha, np.floating) \
+        else fp32_bits(alpha)
+
+
+def _finish(res: np.ndarray, out: str) -> np.ndarray:
+    return res.view(np.float32) if out == "fp32" else res
+
+
+def attention_hip(q_bits, k_bits, v_bits, alpha, kv_len=None, row_ptr=None, key_idx=None, out: str = "bf16",
+                  splits: int = 0, merge_order=None, fallback: bool = True, device: str = "cuda"):
+    """numpy-level GPU backend (mirrors src/exactattn/triton_kernels.py:1522-1560 and
+    src/exactattn/cpu.py:70-109). q (R, d), k (n, d), v (n, dv) bf16 bits. Row r attends keys
+    [0, kv_len[r]) (causal, decode, prefill), or key_idx[row_ptr[r]:row_ptr[r+1]] (any mask), or
+    all keys. Returns (out, flags): out uint16 bf16 bits, or float32 for out="fp32"."""
+    from .hip import attention_problem
+    q = np.asarray(q_bits, dtype=np.uint16)
+    k = np.asarray(k_bits, dtype=np.uint16)
+    v = np.asarray(v_bits, dtype=np.uint16)
+    R, n = q.shape[0], k.shape[0]
+    if row_ptr is None:
+        if kv_len is None:
+            kv_len = np.full(R, n)
+        kv_len = np.asarray(kv_len, dtype=np.int64)
+        row_ptr = np.concatenate([[0], np.cumsum(kv_len)]).astype(np.int64)
+        key_idx = np.concatenate([np.arange(x) for x in kv_len]).astype(np.int64) if R else np.zeros(0, np.int64)
+    prob = problem.csr(q, k, v, row_ptr, key_idx)
+    res, flags, _ = attention_problem(prob, _alpha_bits(alpha), out, splits, merge_order, True, fallback, device)
+    return _finish(res.reshape(R, -1), out), flags
+
+
+def attention_geom(prob: dict, alpha, out: str = "bf16", splits: int = 0, merge_order=None, fallback: bool = True,
+                   device: str = "cuda"):
+    """Serving-geometry problem (exactattention_amd.problem) on the GPU -> (out (B,T,Hq,dv), flags, stats)."""
+    from .hip import attention_problem
+    res, flags, st = attention_problem(prob, _alpha_bits(alpha), out, splits, merge_order, True, fallback, device)
+    return _finish(res, out), flags, st
+
+
+def attention(q_bits, k_bits, v_bits, alpha, mask=None, out: str = "bf16") -> np.ndarray:
+    """Batched attention (src/exactattn/reference.py:150-161): q (r, d), k (n, d), v (n, dv),
+    mask (r, n) bool or None. Returns (r, dv) uint16 bf16 bits, or float32 for out="fp32"."""
+    q = np.asarray(q_bits, dtype=np.uint16)
+    if out not in ("bf16", "fp32"):
+        raise ValueError("out must be 'bf16' or 'fp32'")
+    if mask is None:
+        res, _ = attention_hip(q, k_bits, v_bits, alpha, out=out)
+        return res
+    mask = np.asarray(mask, dtype=bool)
+    counts = mask.sum(axis=1)
+    row_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    key_idx = np.concatenate([np.flatnonzero(m) for m in mask]).astype(np.int64) if mask.size else np.zeros(0, np.int64)
+    res, _ = attention_hip(q, k_bits, v_bits, alpha, row_ptr=row_ptr, key_idx=key_idx, out=out)
+    return res
+
+
+def attention_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> np.ndarray:
+    """One query row over all given keys (src/exactattn/reference.py:146-147)."""
+    q = np.asarray(q_bits, dtype=np.uint16).reshape(1, -1)
+    k = np.asarray(k_bits, dtype=np.uint16).reshape(-1, q.shape[1])
+    v = np.asarray(v_bits, dtype=np.uint16)
+    v = v.reshape(k.shape[0], -1) if v.size else np.zeros((k.shape[0], v.shape[-1] if v.ndim else 0), np.uint16)
+    return attention(q, k, v, alpha, out=out)[0]
+
+
+def launch_hip(*args, **kwargs):
+    """Device-level launch on torch tensors (see exactattention_amd.hip.launch_hip)."""
+    from .hip import launch_hip as _l
+    return _l(*args, **kwargs)

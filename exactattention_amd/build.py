@@ -1,0 +1,37 @@
+"""Builds libexactattn_hip.so in-tree with hipcc for gfx950 (python -m exactattention_amd.build)."""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libexactattn_hip.so")
+
+# -packed-fp32-ops: never emit packed fp32 VALU ops (their forms have misbehaved on this pool).
+# -fno-gpu-flush-denormals-to-zero: bf16 subnormals convert exactly through fp32.
+HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+               "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-Wall", "-Wno-unused-function"]
+
+
+def build(verbose: bool = False) -> str:
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    gen = os.path.join(CSRC, "gen_tables.py")
+    subprocess.run([sys.executable, gen], check=True, stdout=subprocess.DEVNULL)
+    tmp = LIB + ".tmp"
+    cmd = [hipcc, *HIPCC_FLAGS, "-o", tmp, os.path.join(CSRC, "ea_hip.hip")]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed building libexactattn_hip.so")
+    if verbose:
+        sys.stderr.write(r.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,480 @@
+// Device helpers of the certified attention kernels (gfx950). Pure functions on registers.
+//
+// Tier 1 works in fp64, which CDNA4 executes at the full VALU rate:
+//   * a bf16 converts to fp64 exactly; a product of two bf16 is exact in fp64 (16-bit
+//     significands); an FMA chain of such products is exact whenever every partial sum fits
+//     53 bits above the smallest product's lsb (checked per (row, key) from exponent spreads);
+//   * t = RN32(alpha * s) from the exact product split p + e (FMA), with the one double-rounding
+//     case (p exactly an fp32 midpoint) resolved by the sign of e;
+//   * w = RN24(2^t) by a two-level table with a cubic; relative error below 2^-50.9, so the
+//     24-bit rounding is decided unless Y = 2^f * 2^23 lies within 2^-26 of a half-integer;
+//   * o = RN(N/Z) from fp64 N, Z with rigorous error bounds: certified when the whole error
+//     interval lies strictly between two adjacent rounding midpoints.
+// Tier 2 works in 128-bit integers (unsigned __int128 / __int128 compile to 64-bit VALU ops).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ea_tables.h"
+
+namespace ea {
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+__device__ __forceinline__ double u64_as_f64(uint64_t x) { return __longlong_as_double((long long)x); }
+__device__ __forceinline__ uint64_t f64_as_u64(double x) { return (uint64_t)__double_as_longlong(x); }
+
+// bf16 halves of a dword -> fp64 (exact; subnormals need fp32 denormals enabled, which the
+// build does with -fno-gpu-flush-denormals-to-zero)
+__device__ __forceinline__ double bf16lo_f64(uint32_t w) { return (double)__uint_as_float(w << 16); }
+__device__ __forceinline__ double bf16hi_f64(uint32_t w) { return (double)__uint_as_float(w & 0xFFFF0000u); }
+
+// ----------------------------------------------------------------------------------------------
+// t = RN32(alpha * s) for an exact fp64 score s and fp32 alpha (as fp64, exact).
+// Returns the fp32 bits of t in *t_bits. status: 0 ok, 1 tiny (|t| < 2^-25, so w = 1 exactly),
+// 2 overflow (|t| above fp32 max: a domain error).
+// ----------------------------------------------------------------------------------------------
+__device__ __forceinline__ int logit_rn32(double alpha, double s, uint32_t* t_bits) {
+    double p = alpha * s;
+    double e = __fma_rn(alpha, s, -p);  // alpha*s = p + e exactly (|p| >= 2^-969 here or tiny)
+    double ap = fabs(p);
+    if (ap <= 0x1.ffffffcp-26) {  // |alpha s| <= 2^-25 (1 - 2^-29)(1 + 2^-53) < 2^-25
+        *t_bits = 0;
+        return 1;
+    }
+    float t0 = (float)p;  // RN-even
+    uint32_t b0 = __float_as_uint(t0);
+    if ((b0 & 0x7F800000u) == 0x7F800000u) {
+        // RN32(p) overflowed. p == 2^128 - 2^103 (the overflow midpoint) with e pulling toward
+        // zero would round to the largest finite; everything else overflows.
+        if (ap == 0x1.ffffffp127 && (e != 0.0) && ((e < 0.0) == (p > 0.0))) {
+            *t_bits = (p > 0.0) ? 0x7F7FFFFFu : 0xFF7FFFFFu;
+            return 0;
+        }
+        return 2;
+    }
+    double d0 = (double)t0;
+    if (d0 != p && e != 0.0) {
+        // neighbour on p's side of t0
+        bool up_mag = (fabs(p) > fabs(d0));
+        uint32_t b1 = up_mag ? b0 + 1 : b0 - 1;
+        double d1 = (double)__uint_as_float(b1);
+        if (2.0 * p == d0 + d1) {  // p is exactly the midpoint (all terms exact in fp64)
+            // x = p + e: the true value lies on e's side of the midpoint
+            bool toward_d1 = ((d1 > d0) == (e > 0.0));
+            if (toward_d1) b0 = b1;
+        }
+    }
+    *t_bits = b0;
+    return 0;
+}
+
+// ----------------------------------------------------------------------------------------------
+// w = RN24(2^t) = M * 2^E, M in [2^23, 2^24). fp64 path. Returns 0 certified, 1 undecided
+// (|Y - round| too close to a half), 2 out of range (|t| >= 2^30).
+// T1/T2 point at the fp64 tables (LDS copies).
+// Error analysis (relative, |delta| <= 2^-53 per rounding): T1, T2 entries (2 roundings), their
+// product (1), the final FMA (1), the cubic including its truncation (< 2^-67 absolute on a
+// value near 1): |y - 2^f| <= 4.01 * 2^-53 * 2^f < 2^-49.9, hence |Y - 2^(f+23)| < 2^-26.9.
+// ----------------------------------------------------------------------------------------------
+__device__ __forceinline__ int weight_f64(uint32_t t_bits, const double* T1, const double* T2, int32_t* M,
+                                          int32_t* E) {
+    float tf = __uint_as_float(t_bits);
+    uint32_t field = (t_bits >> 23) & 0xFF;
+    if (field < 102) {  // |t| < 2^-25: 2^t rounds to 1
+        *M = 1 << 23;
+        *E = -23;
+        return 0;
+    }
+    if (field >= 127 + 30) return 2;
+    double td = (double)tf;
+    double n = floor(td);
+    double f = td - n;  // exact
+    int ni = (int)n;
+    if (f == 0.0) {
+        *M = 1 << 23;
+        *E = ni - 23;
+        return 0;
+    }
+    int i = (int)(f * 65536.0);  // floor, f < 1
+    double r = __fma_rn(-(double)i, 0x1p-16, f);  // exact: clears f's top 16 fraction bits
+    const double c1 = u64_as_f64(EA_C_BITS[0]), c2 = u64_as_f64(EA_C_BITS[1]), c3 = u64_as_f64(EA_C_BITS[2]);
+    double poly = r * __fma_rn(r, __fma_rn(r, c3, c2), c1);
+    double a = T1[i >> 8] * T2[i & 255];
+    double y = __fma_rn(a, poly, a);
+    double Y = y * 8388608.0;  // 2^23, exact
+    double fl = floor(Y);
+    double fr = Y - fl;  // exact
+    if (fabs(fr - 0.5) <= 0x1p-26) return 1;
+    int m = (int)fl + (fr > 0.5 ? 1 : 0);
+    int e = ni - 23;
+    if (m == (1 << 24)) {
+        m = 1 << 23;
+        ++e;
+    }
+    *M = m;
+    *E = e;
+    return 0;
+}
+
+// ----------------------------------------------------------------------------------------------
+// Certified rounding of a real known to lie in [x - r, x + r] (x, r fp64, r >= 0) to bf16 or
+// fp32 (RN-even, gradual underflow, +0 for every zero). Returns true and the bits when every
+// point of the interval rounds to the same value.
+// ----------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool certify_round(double x, double r, int fp32, uint32_t* bits) {
+    const int p = fp32 ? 24 : 8;
+    const int qmin = fp32 ? -149 : -133;
+    // zero region: |v| <= 2^(qmin-1) rounds to +0 (the boundary is a tie to even zero)
+    const double zlim = fp32 ? 0x1p-150 : 0x1p-134;
+    double ax = fabs(x);
+    if (ax + r <= zlim * (1.0 - 0x1p-40)) {
+        *bits = 0;
+        return true;
+    }
+    if (!(ax < 0x1p200) || !(r < 0x1p200)) return false;  // NaN/inf or absurd: not certified
+    // RN of x to p bits with the format's subnormal quantum
+    uint64_t xb = f64_as_u64(x);
+    uint32_t sign = (uint32_t)(xb >> 63);
+    int ex = (int)((xb >> 52) & 0x7FF);
+    if (ex == 0) return false;  // |x| < 2^-1022: cannot be certified away from zero here
+    int k = ex - 1023;  // floor(log2 |x|)
+    int qe = k - (p - 1);
+    if (qe < qmin) qe = qmin;
+    // q = RN(|x| / 2^qe) exactly from the 53-bit significand
+    uint64_t mant = (xb & ((1ull << 52) - 1)) | (1ull << 52);  // |x| = mant * 2^(k-52)
+    int sh = qe - (k - 52);  // >= 52 - 23 = 29 > 0
+    uint64_t q;
+    if (sh >= 64) {
+        q = 0;  // |x| < 2^(qe-11): rounds to zero; handled by the interval test below
+    } else {
+        q = mant >> sh;
+        uint64_t rem = mant & ((1ull << sh) - 1), half = 1ull << (sh - 1);
+        if (rem > half || (rem == half && (q & 1))) ++q;
+    }
+    // value o = q * 2^qe; neighbours' midpoints
+    double o = ldexp((double)q, qe);
+    double ulp_up = ldexp(1.0, qe);
+    if (q == (1ull << p)) {  // carried into the next binade: o = 2^(qe+p)
+        ulp_up = ldexp(1.0, qe + 1);
+    }
+    double ulp_dn = ldexp(1.0, qe);
+    if (q == (1ull << (p - 1)) && qe > qmin) ulp_dn = ldexp(1.0, qe - 1);  // o is a power of two
+    if (q == 0) {
+        // the interval straddles the zero region boundary
+        return false;
+    }
+    double m_lo = o - 0.5 * ulp_dn, m_hi = o + 0.5 * ulp_up;  // exact
+    double dlo = ax - m_lo, dhi = m_hi - ax;  // relative error <= 2^-53 each
+    double need = 2.0 * r + 0x1p-1060;
+    if (!(dlo > need && dhi > need)) return false;
+    // encode |o| in the format
+    uint64_t qq = q;
+    int e = qe;
+    if (qq == (1ull << p)) {
+        qq >>= 1;
+        ++e;
+    }
+    if (e + (63 - __clzll(qq)) > 127) return false;  // overflow: never certified
+    uint32_t field, frac;
+    if (qq < (1ull << (p - 1))) {
+        field = 0;
+        frac = (uint32_t)qq;
+    } else {
+        field = (uint32_t)(e - qmin + 1);
+        frac = (uint32_t)(qq - (1ull << (p - 1)));
+    }
+    *bits = (sign << (p - 1 + 8)) | (field << (p - 1)) | frac;
+    return true;
+}
+
+// ----------------------------------------------------------------------------------------------
+// 128-bit helpers (tier 2)
+// ----------------------------------------------------------------------------------------------
+__device__ __forceinline__ int clz64(uint64_t x) { return x ? __clzll(x) : 64; }
+__device__ __forceinline__ int bitlen128(u128 x) {
+    uint64_t hi = (uint64_t)(x >> 64), lo = (uint64_t)x;
+    return hi ? 128 - clz64(hi) : (lo ? 64 - clz64(lo) : 0);
+}
+
+// floor / ceil of (a * b) >> 126 for a, b < 2^127
+__device__ __forceinline__ u128 mulshr126(u128 a, u128 b, bool up) {
+    uint64_t a1 = (uint64_t)(a >> 64), a0 = (uint64_t)a, b1 = (uint64_t)(b >> 64), b0 = (uint64_t)b;
+    u128 p00 = (u128)a0 * b0, p01 = (u128)a0 * b1, p10 = (u128)a1 * b0, p11 = (u128)a1 * b1;
+    u128 mid = p01 + p10;
+    u128 mid_c = mid < p01 ? 1 : 0;
+    u128 lo = p00 + (mid << 64);
+    u128 lo_c = lo < p00 ? 1 : 0;
+    u128 hi = p11 + (mid >> 64) + (mid_c << 64) + lo_c;
+    u128 res = (hi << 2) | (lo >> 126);
+    if (up && (lo & (((u128)1 << 126) - 1))) ++res;
+    return res;
+}
+
+__device__ __forceinline__ u128 div_small(u128 a, uint32_t n, bool up) {
+    // long division by a 32-bit divisor, 32 bits at a time
+    uint64_t r = 0;
+    u128 q = 0;
+    for (int s = 96; s >= 0; s -= 32) {
+        uint64_t cur = (r << 32) | (uint32_t)(a >> s);
+        uint64_t qd = cur / n;
+        r = cur - qd * n;
+        q |= (u128)qd << s;
+    }
+    if (up && r) ++q;
+    return q;
+}
+
+// exp(x) * 2^126 enclosure for x in [xl, xh] * 2^-126 with 0 <= x < 2^-8
+__device__ __forceinline__ void exp_encl126(u128 xl, u128 xh, u128* lo, u128* hi) {
+    const u128 one = (u128)1 << 126;
+    u128 s = 0, t = one;
+    for (uint32_t n = 1; t != 0 && n < 40; ++n) {
+        s += t;
+        t = div_small(mulshr126(t, xl, false), n, false);
+    }
+    *lo = s;
+    s = 0;
+    t = one;
+    for (uint32_t n = 1;; ++n) {
+        s += t;
+        t = div_small(mulshr126(t, xh, true), n, true);
+        if ((t <= 1 && n > 3) || n >= 40) {
+            s += 2 * t + 2;
+            break;
+        }
+    }
+    *hi = s;
+}
+
+// w = RN24(2^t) from a 128-bit fixed-point enclosure (tier 2). 0 certified, 1 undecided,
+// 2 out of range (|t| >= 2^62).
+__device__ inline int weight_wide(uint32_t t_bits, int32_t* M, int64_t* E) {
+    uint32_t field = (t_bits >> 23) & 0xFF;
+    if (field < 102) {
+        *M = 1 << 23;
+        *E = -23;
+        return 0;
+    }
+    if (field >= 127 + 62) return 2;
+    int32_t mag = (int32_t)((t_bits & 0x7FFFFF) | 0x800000);
+    int32_t tm = (t_bits >> 31) ? -mag : mag;
+    int te = (int)field - 150;
+    int64_t n;
+    uint64_t F;  // f = F * 2^-48
+    if (te >= 0) {
+        n = (int64_t)tm << te;
+        F = 0;
+    } else {
+        int s = -te;
+        n = (int64_t)tm >> s;
+        int64_t a = (int64_t)tm - (n << s);
+        F = (uint64_t)a << (48 - s);
+    }
+    if (F == 0) {
+        *M = 1 << 23;
+        *E = n - 23;
+        return 0;
+    }
+    // 2^f = 2^(j1/256) * 2^(j2/65536) * exp(r ln2), r = R * 2^-48 < 2^-16
+    int j1 = (int)(F >> 40), j2 = (int)((F >> 32) & 255);
+    uint64_t R = F & 0xFFFFFFFFull;
+    const u128 ln2lo = ((u128)EA_LN2W[0] << 64) | EA_LN2W[1];  // floor(ln2 * 2^126)
+    const u128 ln2hi = ln2lo + 1;
+    u128 xl = mulshr126((u128)R << 78, ln2lo, false);
+    u128 xh = mulshr126((u128)R << 78, ln2hi, true);
+    u128 el, eh;
+    exp_encl126(xl, xh, &el, &eh);
+    u128 t1l = ((u128)EA_T1W[2 * j1] << 64) | EA_T1W[2 * j1 + 1], t1h = t1l + 1;
+    u128 t2l = ((u128)EA_T2W[2 * j2] << 64) | EA_T2W[2 * j2 + 1], t2h = t2l + 1;
+    u128 yl = mulshr126(mulshr126(t1l, t2l, false), el, false);
+    u128 yh = mulshr126(mulshr126(t1h, t2h, true), eh, true);
+    const int sh = 126 - 23;
+    u128 half = (u128)1 << (sh - 1);
+    u128 ql = (yl + half) >> sh, qh = (yh + half) >> sh;
+    if (ql != qh) return 1;
+    int64_t e = n - 23;
+    if (ql == ((u128)1 << 24)) {
+        ql >>= 1;
+        ++e;
+    }
+    *M = (int32_t)ql;
+    *E = e;
+    return 0;
+}
+
+// Multiword unsigned, 32-bit limbs (tier 2 final rounding and logit rounding)
+#define EA_MW 12
+struct mw {
+    uint32_t w[EA_MW];
+};
+__device__ inline void mw_zero(mw& a) {
+#pragma unroll
+    for (int i = 0; i < EA_MW; ++i) a.w[i] = 0;
+}
+__device__ inline void mw_from_u128(mw& a, u128 x) {
+    mw_zero(a);
+    for (int i = 0; i < 4; ++i) a.w[i] = (uint32_t)(x >> (32 * i));
+}
+__device__ inline int mw_bitlen(const mw& a) {
+    for (int i = EA_MW - 1; i >= 0; --i)
+        if (a.w[i]) return 32 * i + (32 - __clz(a.w[i]));
+    return 0;
+}
+__device__ inline void mw_shl(mw& r, const mw& a, int s) {
+    mw t;
+    mw_zero(t);
+    int L = s >> 5, b = s & 31;
+    for (int i = EA_MW - 1; i >= 0; --i) {
+        int src = i - L;
+        if (src < 0) continue;
+        uint64_t v = (uint64_t)a.w[src] << b;
+        if (b && src - 1 >= 0) v |= (uint64_t)a.w[src - 1] >> (32 - b);
+        t.w[i] = (uint32_t)v;
+    }
+    r = t;
+}
+__device__ inline int mw_cmp(const mw& a, const mw& b) {
+    for (int i = EA_MW - 1; i >= 0; --i)
+        if (a.w[i] != b.w[i]) return a.w[i] < b.w[i] ? -1 : 1;
+    return 0;
+}
+__device__ inline void mw_sub(mw& a, const mw& b) {
+    int64_t br = 0;
+    for (int i = 0; i < EA_MW; ++i) {
+        int64_t x = (int64_t)a.w[i] - (int64_t)b.w[i] - br;
+        br = x < 0;
+        a.w[i] = (uint32_t)(x + (br ? ((int64_t)1 << 32) : 0));
+    }
+}
+
+struct rnd {
+    int sign;
+    uint64_t m;
+    int e;
+    int overflow;
+};
+__device__ inline bool rnd_eq(const rnd& a, const rnd& b) {
+    if (a.overflow || b.overflow) return false;
+    if (a.m == 0 && b.m == 0) return true;
+    return a.sign == b.sign && a.m == b.m && a.e == b.e;
+}
+
+// RN-even of (a / b) * 2^E into (p, qmin, emax=127); a, b < 2^128, b > 0.
+__device__ inline rnd round_ratio(u128 a_, u128 b_, int E, int sign, int p, int qmin) {
+    rnd r = {sign, 0, 0, 0};
+    if (a_ == 0) return r;
+    mw a, b, t;
+    mw_from_u128(a, a_);
+    mw_from_u128(b, b_);
+    int k = mw_bitlen(a) - mw_bitlen(b);
+    if (k >= 0) {
+        mw_shl(t, b, k);
+        if (mw_cmp(a, t) < 0) --k;
+    } else {
+        mw_shl(t, a, -k);
+        if (mw_cmp(t, b) < 0) --k;
+    }
+    long K = (long)k + E;
+    if (K < (long)qmin - 1) return r;
+    long qe = K - (p - 1);
+    if (qe < qmin) qe = qmin;
+    long s = (long)E - qe;
+    if (s > 200 || s < -200) {  // outside what 12 limbs hold; K range makes this unreachable
+        r.overflow = 1;
+        return r;
+    }
+    mw n = a, d = b;
+    if (s >= 0) mw_shl(n, a, (int)s);
+    else mw_shl(d, b, (int)-s);
+    uint64_t q = 0;
+    for (int i = p + 1; i >= 0; --i) {
+        mw_shl(t, d, i);
+        if (mw_cmp(n, t) >= 0) {
+            mw_sub(n, t);
+            q |= 1ull << i;
+        }
+    }
+    mw_shl(t, n, 1);
+    int c = mw_cmp(t, d);
+    if (c > 0 || (c == 0 && (q & 1))) ++q;
+    if (q == (1ull << p)) {
+        q >>= 1;
+        ++qe;
+    }
+    if (qe + (63 - __clzll(q)) > 127) r.overflow = 1;
+    r.m = q;
+    r.e = (int)qe;
+    return r;
+}
+
+__device__ inline uint32_t rnd_bits(const rnd& r, int fp32) {
+    if (r.m == 0) return 0;
+    int p = fp32 ? 24 : 8, qmin = fp32 ? -149 : -133;
+    uint64_t m = r.m;
+    int e = r.e;
+    while (m < (1ull << (p - 1)) && e > qmin) {
+        m <<= 1;
+        --e;
+    }
+    uint32_t field, frac;
+    if (m < (1ull << (p - 1))) {
+        field = 0;
+        frac = (uint32_t)m;
+    } else {
+        field = (uint32_t)(e - qmin + 1);
+        frac = (uint32_t)(m - (1ull << (p - 1)));
+    }
+    uint32_t sg = r.sign < 0 ? 1u : 0u;
+    return (sg << (p - 1 + 8)) | (field << (p - 1)) | frac;
+}
+
+// RN32 of (am * X) * 2^E with X a signed 128-bit integer and |am| < 2^24: the tier-2 logit.
+// status 0 ok, 2 overflow. Zero gives bits 0.
+__device__ inline int rn32_prod(int32_t am, i128 X, int E, uint32_t* bits) {
+    if (X == 0 || am == 0) {
+        *bits = 0;
+        return 0;
+    }
+    int sign = ((X < 0) != (am < 0)) ? -1 : 1;
+    u128 ax = X < 0 ? (u128)(-X) : (u128)X;
+    uint64_t aa = (uint64_t)(am < 0 ? -(int64_t)am : am);
+    // 152-bit product in three 64-bit words: ax * aa
+    u128 lo = (u128)(uint64_t)ax * aa;
+    u128 hi = (u128)(uint64_t)(ax >> 64) * aa + (lo >> 64);
+    uint64_t w0 = (uint64_t)lo, w1 = (uint64_t)hi, w2 = (uint64_t)(hi >> 64);
+    mw m;
+    mw_zero(m);
+    m.w[0] = (uint32_t)w0; m.w[1] = (uint32_t)(w0 >> 32);
+    m.w[2] = (uint32_t)w1; m.w[3] = (uint32_t)(w1 >> 32);
+    m.w[4] = (uint32_t)w2; m.w[5] = (uint32_t)(w2 >> 32);
+    int bl = mw_bitlen(m);
+    long k = (long)bl - 1 + E;
+    long qe = k - 23;
+    if (qe < -149) qe = -149;
+    long lo_bit = qe - E;
+    uint64_t q = 0;
+    int rb = 0, st = 0;
+    if (lo_bit <= 0) {
+        // exact: shift left
+        for (int i = bl - 1; i >= 0; --i) q = (q << 1) | ((m.w[i >> 5] >> (i & 31)) & 1);
+        q <<= (-lo_bit);
+    } else {
+        for (int i = bl - 1; i >= (int)lo_bit; --i) q = (q << 1) | ((m.w[i >> 5] >> (i & 31)) & 1);
+        int rbi = (int)lo_bit - 1;
+        rb = (m.w[rbi >> 5] >> (rbi & 31)) & 1;
+        for (int i = 0; i < rbi && !st; ++i) st |= (m.w[i >> 5] >> (i & 31)) & 1;
+    }
+    if (rb && (st || (q & 1))) ++q;
+    if (q == (1ull << 24)) {
+        q >>= 1;
+        ++qe;
+    }
+    if (q && qe + (63 - __clzll(q)) > 127) return 2;
+    rnd r = {sign, q, (int)qe, 0};
+    *bits = rnd_bits(r, 1);
+    return 0;
+}
+
+}  // namespace ea

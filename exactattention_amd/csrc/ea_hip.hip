@@ -1,0 +1,1209 @@
+// Certified split-KV ExactAttention for AMD Instinct MI355X (gfx950): kernels and C ABI.
+//
+// One step is four launches on the caller's stream, with fixed grids and no memsets:
+//   ea_prep      q rows -> fp64 + exponent ranges; clears the tier-2 work counter
+//   ea_split     tier 1: per (segment, row block, KV split) an fp64 pass over 64-key tiles:
+//                exact scores (checked), certified logits and weights, P.V partials with
+//                rigorous error bounds. Writes one partial per (split, row).
+//   ea_combine   merges the split partials in the caller's order and certifies RN(N/Z) per
+//                channel; appends rows it cannot certify to the tier-2 work list
+//   ea_tier2     per listed row: 128-bit windowed scores, 128-bit exp2 enclosure, 128-bit
+//                fixed-point Z and N with counted truncation, exact final rounding
+// Reference behaviour: src/exactattn/triton_kernels.py:1324-1519 (split, combine, tier 2,
+// host fallback) and docs/SPEC.md (the definition the bits must equal).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/exactattn_hip.h"
+#include "ea_device.h"
+
+using namespace ea;
+
+#define EA_TILE 64
+#define EA_THREADS 256
+#define EA_MAXRB 4
+#define EA_MAXD 128
+#define EA_MAXDV 128
+#define EA_T2_BLOCKS 32
+
+// ------------------------------------------------------------------------------------------------
+// Kernel parameters
+// ------------------------------------------------------------------------------------------------
+struct Params {
+    ea_geometry g;
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const int32_t* seq_len;
+    const int32_t* kv_len;
+    const int32_t* bt;
+    const int64_t* bt_off;
+    const uint64_t* tree_mask;
+    const int32_t* tree_base;
+    void* out;
+    uint8_t* flags;
+    int64_t* stats;
+    const int32_t* merge_order;
+    double alpha;
+    int32_t am, ae;
+    int32_t out_fp32;
+    int32_t nsplit, split_len;
+    int32_t grp, r_seg, rb, nrb, nseg;
+    int32_t pshift;
+    int32_t dlog;
+    int64_t rows;
+    // workspace
+    double* q64;      // rows * d
+    int32_t* qinfo;   // rows: (FQmax << 16) | FQmin' ; bit 31 = all zero
+    int32_t* pR;      // nsplit * rows
+    int32_t* pn;      // nsplit * rows (visible keys, or -1 for a tier-1 flag)
+    double* pZ;       // nsplit * rows
+    double* pN;       // nsplit * rows * dv
+    float* pV;        // nsplit * nseg * nrb * dv : max |v| per channel over the block's keys
+    int32_t* wl;      // rows
+    int32_t* wl_cnt;  // 1
+    int32_t* t2M;     // EA_T2_BLOCKS * max_keys
+    int64_t* t2E;     // EA_T2_BLOCKS * max_keys
+    int32_t t2_keys;
+};
+
+__device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
+    return (b * P.g.num_tokens + t) * P.g.num_q_heads + hq;
+}
+
+// global element offset of key n of sequence b, kv head hk (K when isv = 0, V when 1)
+__device__ __forceinline__ int64_t kv_off(const Params& P, int64_t b, int64_t n, int hk, int isv) {
+    int64_t page, slot;
+    if (P.bt) {
+        int64_t off = P.bt_off ? P.bt_off[b] : b * (int64_t)P.g.block_table_stride;
+        page = P.bt[off + (n >> P.pshift)];
+        slot = n & ((1 << P.pshift) - 1);
+    } else {
+        page = b;
+        slot = n;
+    }
+    if (isv) return page * P.g.v_page_stride + slot * P.g.v_slot_stride + (int64_t)hk * P.g.v_head_stride;
+    return page * P.g.k_page_stride + slot * P.g.k_slot_stride + (int64_t)hk * P.g.k_head_stride;
+}
+
+__device__ __forceinline__ bool visible(const Params& P, int64_t tok, int64_t b, int64_t n) {
+    if (n < P.kv_len[tok]) return true;
+    if (P.tree_mask) {
+        int64_t i = n - P.tree_base[b];
+        if (i >= 0 && i < 64) return (P.tree_mask[tok] >> i) & 1;
+    }
+    return false;
+}
+
+// end of the visible key range of a query token
+__device__ __forceinline__ int64_t vis_end(const Params& P, int64_t tok, int64_t b) {
+    int64_t e = P.kv_len[tok];
+    if (P.tree_mask) {
+        uint64_t m = P.tree_mask[tok];
+        if (m) {
+            int64_t te = P.tree_base[b] + 64 - __clzll(m);
+            if (te > e) e = te;
+        }
+    }
+    return e;
+}
+
+__device__ __forceinline__ double wave_sum(double x) {
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+    for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_min_i(int x) {
+    for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_sum_i(int x) {
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Kernel 1: q rows to fp64 and their exponent ranges. One wave per row.
+// qinfo = (FQmax << 16) | FQmin' with FQmin' = max(min nonzero exponent field, 1); 0x80000000 when
+// the row is all zeros; 0x40000000 when it holds a NaN/inf.
+// ------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) ea_prep(Params P) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *P.wl_cnt = 0;
+    int lane = threadIdx.x & 63;
+    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= P.rows) return;
+    int Hq = P.g.num_q_heads, T = P.g.num_tokens, d = P.g.head_dim;
+    int64_t b = row / ((int64_t)T * Hq);
+    int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
+    const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
+    int fmax = 0, fmin = 0x1FF, bad = 0;
+    for (int i = lane; i < d; i += 64) {
+        uint32_t x = qr[i];
+        P.q64[row * d + i] = (double)__uint_as_float(x << 16);
+        int f = (x >> 7) & 0xFF;
+        if (f == 0xFF) bad = 1;
+        if (x & 0x7FFF) {
+            fmax = max(fmax, f);
+            fmin = min(fmin, max(f, 1));
+        }
+    }
+    fmax = wave_max_i(fmax);
+    fmin = wave_min_i(fmin);
+    bad = wave_max_i(bad);
+    if (lane == 0) {
+        int32_t info = (fmax << 16) | (fmin & 0xFFFF);
+        if (fmin == 0x1FF) info = (int32_t)0x80000000;
+        if (bad) info = 0x40000000;
+        P.qinfo[row] = info;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Kernel 2: tier-1 split kernel.
+// Block = 4 waves over one (segment, row block, split). Per 64-key tile:
+//   S: thread (w, l) forms 32-dim partial dots of key l with every row (fp64 FMA chains),
+//      and the key's exponent range over those dims (packed 16-bit max/min on magnitudes);
+//   B: wave r finishes row r: exactness check, t, w = M 2^E, tile max, running rescale;
+//   P: thread (w, l) accumulates channels 2l, 2l+1 over keys 16w..16w+15 for every row.
+// K tiles sit in LDS with an XOR swizzle of their 16-byte chunks (conflict-free per-key reads);
+// the next tile's K and V are loaded into registers while the current one is processed.
+// ------------------------------------------------------------------------------------------------
+struct SplitSmem {
+    uint4 K[2][EA_TILE * (EA_MAXD / 8)];          // 32 KB
+    uint32_t V[2][EA_TILE * (EA_MAXDV / 2)];      // 32 KB
+    double T1[256], T2[256];                      // 4 KB
+    double sc[4][EA_MAXRB][EA_TILE];              // 8 KB partial scores
+    uint32_t kmx[4][EA_TILE], kmn[4][EA_TILE];    // 2 KB packed magnitude max / min-1
+    double w[EA_MAXRB][EA_TILE];                  // 2 KB weights of the tile
+    double scale[EA_MAXRB];
+    int32_t rowflag[EA_MAXRB];
+};
+
+__global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    SplitSmem& S = *reinterpret_cast<SplitSmem*>(smem_raw);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int d = P.g.head_dim, dv = P.g.head_dim_v;
+    const int nchunk = d >> 3;     // 16-byte chunks per key row
+    const int ndw = dv >> 1;       // dwords per value row
+
+    const int item = blockIdx.x;
+    const int seg = item / P.nrb, rbk = item % P.nrb;
+    const int split = blockIdx.y;
+    const int Hkv = P.g.num_kv_heads;
+    const int64_t b = seg / Hkv;
+    const int hk = seg % Hkv;
+    const int row0 = rbk * P.rb;
+    const int nrow = min(P.rb, P.r_seg - row0);
+
+    for (int i = tid; i < 256; i += EA_THREADS) {
+        S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
+        S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
+    }
+    // rows of this block
+    int64_t grow[EA_MAXRB], gtok[EA_MAXRB];
+    int64_t kend = 0;
+#pragma unroll
+    for (int r = 0; r < EA_MAXRB; ++r) {
+        int lr = row0 + min(r, nrow - 1);
+        int t = lr / P.grp, gi = lr % P.grp;
+        int hq = hk * P.grp + gi;
+        grow[r] = row_index(P, b, t, hq);
+        gtok[r] = b * P.g.num_tokens + t;
+        if (r < nrow) kend = max(kend, vis_end(P, gtok[r], b));
+    }
+    int64_t my_grow = 0, my_gtok = 0;
+    if (w < nrow) {
+        int lr = row0 + w;
+        int t = lr / P.grp, gi = lr % P.grp;
+        my_grow = row_index(P, b, t, hk * P.grp + gi);
+        my_gtok = b * P.g.num_tokens + t;
+    }
+    int64_t slen = P.seq_len[b];
+    if (kend > slen) kend = slen;
+    const int64_t k0 = (int64_t)split * P.split_len;
+    const int64_t k1 = min(k0 + (int64_t)P.split_len, kend);
+    const int64_t pbase = (int64_t)split * P.rows;
+
+    // per-row state (meaningful in wave r for row r)
+    int Rrun = INT_MIN;
+    double zacc = 0.0;
+    int nvis = 0;
+    int rflag = 0;
+    int fqmax = 0, fqmin = 0;
+    bool qzero = false;
+    if (w < nrow) {
+        int32_t qi = P.qinfo[my_grow];
+        if (qi == 0x40000000) rflag = 1;
+        qzero = (qi == (int32_t)0x80000000);
+        fqmax = (qi >> 16) & 0x1FF;
+        fqmin = qi & 0xFFFF;
+    }
+    const int spread_lim = 37 - P.dlog;  // exactness: (FQmax-FQmin') + (FKmax-FKmin') <= 37 - ceil(log2 d)
+
+    double acc[EA_MAXRB][2];
+    for (int r = 0; r < EA_MAXRB; ++r) acc[r][0] = acc[r][1] = 0.0;
+    uint32_t vmx = 0;  // packed max |v| magnitude bits for channels 2l, 2l+1
+
+    // register staging of the next tile: 4 K chunks + (up to) 4 V dword-pairs per thread
+    uint4 kst[4];
+    uint32_t vst[EA_TILE * (EA_MAXDV / 2) / EA_THREADS];  // 16 dwords
+    auto load_tile = [&](int64_t n0) {
+        // K: chunk index x = i*256 + tid -> key x/16, LDS chunk slot x%16 holds global chunk
+        // (x%16) ^ (key%16)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int x = i * EA_THREADS + tid;
+            int key = x >> 4, cs = x & 15;
+            int c = cs ^ (key & 15);
+            int64_t n = n0 + key;
+            uint4 val = make_uint4(0, 0, 0, 0);
+            if (c < nchunk && n < k1) {
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4* src = reinterpret_cast<const u32x4*>(P.k + kv_off(P, b, n, hk, 0)) + c;
+                u32x4 t4 = __builtin_nontemporal_load(src);
+                val = make_uint4(t4.x, t4.y, t4.z, t4.w);
+            }
+            kst[i] = val;
+        }
+        // V: dword index x = i*256 + tid -> key x/64, dword x%64
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int x = i * EA_THREADS + tid;
+            int key = x >> 6, dw = x & 63;
+            int64_t n = n0 + key;
+            uint32_t val = 0;
+            if (dw < ndw && n < k1) {
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(P.v + kv_off(P, b, n, hk, 1)) + dw;
+                val = __builtin_nontemporal_load(src);
+            }
+            vst[i] = val;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S.K[buf][i * EA_THREADS + tid] = kst[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S.V[buf][i * EA_THREADS + tid] = vst[i];
+    };
+
+    int ntiles = (k1 > k0) ? (int)((k1 - k0 + EA_TILE - 1) / EA_TILE) : 0;
+    if (ntiles > 0) {
+        load_tile(k0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    const double* q64 = P.q64;
+    for (int it = 0; it < ntiles; ++it) {
+        const int buf = it & 1;
+        const int64_t n0 = k0 + (int64_t)it * EA_TILE;
+        if (it + 1 < ntiles) load_tile(n0 + EA_TILE);
+
+        // ---- S: partial dots over dims [32w, 32w+32) of key `lane`
+        {
+            double sacc[EA_MAXRB];
+#pragma unroll
+            for (int r = 0; r < EA_MAXRB; ++r) sacc[r] = 0.0;
+            typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+            us2 mx = {0, 0}, mn = {0xFFFF, 0xFFFF};
+            for (int cc = 0; cc < 4; ++cc) {
+                int c = 4 * w + cc;
+                if (c >= nchunk) break;
+                uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
+                uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t m2 = wd[j] & 0x7FFF7FFFu;
+                    us2 mv = __builtin_bit_cast(us2, m2);
+                    mx = __builtin_elementwise_max(mx, mv);
+                    mn = __builtin_elementwise_min(mn, mv - (us2){1, 1});
+                    double k_lo = bf16lo_f64(wd[j]), k_hi = bf16hi_f64(wd[j]);
+                    int dim = c * 8 + 2 * j;
+#pragma unroll
+                    for (int r = 0; r < EA_MAXRB; ++r) {
+                        if (r < nrow) {
+                            const double* qr = q64 + grow[r] * d + dim;
+                            sacc[r] = __fma_rn(qr[0], k_lo, sacc[r]);
+                            sacc[r] = __fma_rn(qr[1], k_hi, sacc[r]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < EA_MAXRB; ++r) S.sc[w][r][lane] = sacc[r];
+            S.kmx[w][lane] = __builtin_bit_cast(uint32_t, mx);
+            S.kmn[w][lane] = __builtin_bit_cast(uint32_t, mn);
+        }
+        __syncthreads();
+
+        // ---- B: wave w finishes row w
+        if (w < nrow) {
+            const int r = w;
+            const int64_t n = n0 + lane;
+            bool vis = (n < k1) && visible(P, my_gtok, b, n);
+            double s = 0.0;
+            for (int ww = 0; ww < 4; ++ww) s += S.sc[ww][r][lane];
+            uint32_t kmxa = 0, kmna = 0xFFFFFFFFu;
+            for (int ww = 0; ww < 4; ++ww) {
+                uint32_t a = S.kmx[ww][lane], c2 = S.kmn[ww][lane];
+                kmxa = max(kmxa & 0xFFFF, a & 0xFFFF) | (max(kmxa >> 16, a >> 16) << 16);
+                kmna = min(kmna & 0xFFFF, c2 & 0xFFFF) | (min(kmna >> 16, c2 >> 16) << 16);
+            }
+            uint32_t magmax = max(kmxa & 0xFFFF, kmxa >> 16);
+            uint32_t magmin1 = min(kmna & 0xFFFF, kmna >> 16);  // (min nonzero magnitude) - 1, 0xFFFF if none
+            int32_t M = 1 << 23, E = -23;
+            bool kzero = (magmax == 0);
+            if (vis && !rflag) {
+                bool exact = qzero || kzero;
+                if (!exact) {
+                    int fkmax = (int)(magmax >> 7);
+                    int fkmin = max((int)((magmin1 + 1) >> 7), 1);
+                    exact = (fqmax - fqmin) + (fkmax - fkmin) <= spread_lim;
+                }
+                if (!isfinite(s)) exact = false;
+                if (!exact) {
+                    rflag = 1;  // score not certified here: tier 2
+                } else {
+                    uint32_t tb = 0;
+                    int ls = (s == 0.0) ? 1 : logit_rn32(P.alpha, s, &tb);
+                    if (ls == 2) {
+                        rflag = 1;  // logit overflow: tier 2 confirms and reports the domain error
+                    } else if (ls == 0) {
+                        int ws = weight_f64(tb, S.T1, S.T2, &M, &E);
+                        if (ws) rflag = 1;
+                    }
+                }
+            }
+            // any lane flagged -> the row is flagged
+            rflag = wave_max_i(rflag);
+            int tmax = wave_max_i(vis ? E + 23 : INT_MIN);
+            int Rnew = max(Rrun, tmax);
+            double sc = 1.0;
+            if (Rrun != INT_MIN && Rnew != Rrun) {
+                int dsh = Rrun - Rnew;
+                if (dsh < -900) rflag = 1;
+                sc = ldexp(1.0, max(dsh, -1000));
+                zacc *= sc;
+            }
+            double om = 0.0;
+            if (vis) {
+                int de = E - Rnew;
+                if (de < -1000) rflag = 1;
+                om = ldexp((double)M, max(de, -1000));
+            }
+            if (rflag) om = 0.0;
+            zacc += om;
+            nvis += vis ? 1 : 0;
+            Rrun = Rnew;
+            S.w[r][lane] = om;
+            if (lane == 0) {
+                S.scale[r] = sc;
+                S.rowflag[r] = rflag;
+            }
+        }
+        __syncthreads();
+
+        // ---- P: channels 2*lane, 2*lane+1 over keys 16w .. 16w+15
+        if (lane < ndw) {
+#pragma unroll
+            for (int r = 0; r < EA_MAXRB; ++r) {
+                if (r < nrow) {
+                    double sc = S.scale[r];
+                    if (sc != 1.0) {
+                        acc[r][0] *= sc;
+                        acc[r][1] *= sc;
+                    }
+                }
+            }
+            typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+            us2 vm = __builtin_bit_cast(us2, vmx);
+            for (int kk = 0; kk < 16; ++kk) {
+                int key = 16 * w + kk;
+                uint32_t vd = S.V[buf][key * 64 + lane];
+                vm = __builtin_elementwise_max(vm, __builtin_bit_cast(us2, vd & 0x7FFF7FFFu));
+                double v0 = bf16lo_f64(vd), v1 = bf16hi_f64(vd);
+#pragma unroll
+                for (int r = 0; r < EA_MAXRB; ++r) {
+                    if (r < nrow) {
+                        double om = S.w[r][key];
+                        acc[r][0] = __fma_rn(om, v0, acc[r][0]);
+                        acc[r][1] = __fma_rn(om, v1, acc[r][1]);
+                    }
+                }
+            }
+            vmx = __builtin_bit_cast(uint32_t, vm);
+        }
+        if (it + 1 < ntiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: reduce N over the 4 waves, write the split partial
+    double* red = reinterpret_cast<double*>(&S.K[0][0]);  // reuse: 4 * EA_MAXRB * 128 doubles = 16 KB
+    uint32_t* vred = reinterpret_cast<uint32_t*>(&S.V[0][0]);
+    if (lane < ndw) {
+#pragma unroll
+        for (int r = 0; r < EA_MAXRB; ++r) {
+            red[((w * EA_MAXRB) + r) * 128 + 2 * lane] = acc[r][0];
+            red[((w * EA_MAXRB) + r) * 128 + 2 * lane + 1] = acc[r][1];
+        }
+        vred[w * 64 + lane] = vmx;
+    }
+    // row scalars
+    if (w < nrow) {
+        double z = wave_sum(zacc);
+        int nv = wave_sum_i(nvis);
+        if (lane == 0) {
+            int64_t o = pbase + my_grow;
+            P.pR[o] = Rrun;
+            P.pZ[o] = z;
+            P.pn[o] = rflag ? -1 : nv;
+        }
+    }
+    __syncthreads();
+    for (int x = tid; x < nrow * dv; x += EA_THREADS) {
+        int r = x / dv, c = x % dv;
+        double s = 0.0;
+        for (int ww = 0; ww < 4; ++ww) s += red[((ww * EA_MAXRB) + r) * 128 + c];
+        P.pN[(pbase + grow[r]) * dv + c] = s;
+    }
+    for (int c = tid; c < dv; c += EA_THREADS) {
+        uint32_t m = 0;
+        for (int ww = 0; ww < 4; ++ww) {
+            uint32_t a = vred[ww * 64 + (c >> 1)];
+            m = max(m, (c & 1) ? (a >> 16) : (a & 0xFFFF));
+        }
+        // bf16 magnitude bits -> fp32 value (a NaN pattern keeps the row from certifying)
+        P.pV[(((int64_t)split * P.nseg + seg) * P.nrb + rbk) * dv + c] = __uint_as_float(m << 16);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Kernel 3: combine. One wave per row. Merges the split partials in merge order, then the
+// certified rounding per channel. Rows not certified go to the tier-2 work list.
+// Error bound (u = 2^-53, relative weights w_j 2^-R of the split, n_s visible keys):
+//   |Zhat_s - Z_s| <= (n_s + 4) u' Z_s,  |Nhat_sc - N_sc| <= (n_s + 4) u' Vmax_sc Z_s
+// (any summation tree of FMA-fused exact products, depth <= n_s + 2, u' = u (1 + 2^-28));
+// merging adds depth nsplit, so with A = sum_s 2^(R_s - R) Zhat_s (n_s + nsplit + 4):
+//   eZ = u' A + tiny,  eN_c = u' A max_s Vmax_sc + tiny.
+// ------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) ea_combine(Params P) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= P.rows) return;
+    const int dv = P.g.head_dim_v;
+    const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
+    const int64_t b = row / ((int64_t)T * Hq);
+    const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
+    const int hk = hq / P.grp, gi = hq % P.grp;
+    const int seg = (int)(b * P.g.num_kv_heads + hk);
+    const int lr = t * P.grp + gi;
+    const int rbk = lr / P.rb;
+    const int ns = P.nsplit;
+
+    // the caller's merge order is used only if it is a permutation of [0, ns); any order gives
+    // the same certified bits, so an invalid one falls back to 0..ns-1
+    bool use_mo = P.merge_order != nullptr && ns <= 64;
+    if (use_mo) {
+        uint64_t seen = 0;
+        for (int i = 0; i < ns; ++i) {
+            int s = P.merge_order[i];
+            if (s < 0 || s >= ns) use_mo = false;
+            else seen |= 1ull << s;
+        }
+        if (seen != (ns == 64 ? ~0ull : ((1ull << ns) - 1))) use_mo = false;
+    }
+    int flag = 0;
+    int R = INT_MIN;
+    for (int s = 0; s < ns; ++s) {
+        int64_t o = (int64_t)s * P.rows + row;
+        int n = P.pn[o];
+        if (n < 0) flag = 1;
+        else if (n > 0) R = max(R, P.pR[o]);
+    }
+    if (P.qinfo[row] == 0x40000000) flag = 1;
+    uint16_t* o16 = (uint16_t*)P.out;
+    uint32_t* o32 = (uint32_t*)P.out;
+    int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
+    const double up = 0x1p-53 * (1.0 + 0x1p-28);
+    double Z = 0.0, A = 0.0;
+    int nterm = 0;
+    if (!flag && R != INT_MIN) {
+        for (int i = 0; i < ns; ++i) {
+            int s = use_mo ? P.merge_order[i] : i;
+            int64_t o = (int64_t)s * P.rows + row;
+            int n = P.pn[o];
+            if (n <= 0) continue;
+            int dsh = P.pR[o] - R;
+            if (dsh < -900) flag = 1;
+            double zs = ldexp(P.pZ[o], max(dsh, -1000));
+            Z += zs;
+            A += zs * (double)(n + ns + 4);
+            nterm += n;
+        }
+    }
+    if (!flag && R == INT_MIN) {
+        // no visible key: the output is +0 (docs/SPEC.md step 5, empty set)
+        for (int c = lane; c < dv; c += 64) {
+            if (P.out_fp32) o32[obase + c] = 0;
+            else o16[obase + c] = 0;
+        }
+        if (lane == 0) P.flags[row] = 0;
+        return;
+    }
+    double tiny = (double)(nterm + 64 * ns + 64) * 0x1p-1074;
+    double eZ = A * up + tiny;
+    if (!(Z > 2.0 * eZ) || !isfinite(Z)) flag = 1;
+    bool ok = !flag;
+    for (int c = lane; c < dv; c += 64) {
+        uint32_t bits = 0;
+        if (!flag) {
+            double N = 0.0;
+            float vmaxf = 0.0f;
+            for (int i = 0; i < ns; ++i) {
+                int s = use_mo ? P.merge_order[i] : i;
+                int64_t o = (int64_t)s * P.rows + row;
+                int n = P.pn[o];
+                if (n <= 0) continue;
+                N += ldexp(P.pN[o * dv + c], max(P.pR[o] - R, -1000));
+                float vm = P.pV[(((int64_t)s * P.nseg + seg) * P.nrb + rbk) * dv + c];
+                vmaxf = fmaxf(vmaxf, vm);
+                if (!(vm <= 3.4028235e38f)) vmaxf = __builtin_inff();
+            }
+            double eN = A * up * (double)vmaxf + tiny;
+            double q = N / Z;
+            double aq = fabs(q);
+            double delta = (eN + aq * eZ) / (Z - eZ) * (1.0 + 0x1p-40) + aq * 0x1p-51 + 0x1p-1070;
+            if (!isfinite(q) || !isfinite(delta) || !certify_round(q, delta, P.out_fp32, &bits)) ok = false;
+        }
+        if (P.out_fp32) o32[obase + c] = bits;
+        else o16[obase + c] = (uint16_t)bits;
+    }
+    // all lanes agree
+    int bad = wave_max_i(ok ? 0 : 1);
+    if (lane == 0) {
+        P.flags[row] = bad ? 1 : 0;
+        if (bad) {
+            int slot = atomicAdd(P.wl_cnt, 1);
+            P.wl[slot] = (int32_t)row;
+        }
+        if (P.stats) {
+            atomicAdd((unsigned long long*)&P.stats[0], 1ull);
+            if (bad) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Kernel 4: tier 2. One block per listed row (grid-stride over the work list). 128-bit arithmetic
+// throughout; the same certified structure as the reference's int128 CPU schedule
+// (csrc/exact_attention_cpu.cpp:361-490 with acc_bits = 128), with a single tile per row.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ i128 floor_shift128(i128 m, int64_t sh, int* lost) {
+    if (sh >= 0) {
+        *lost = 0;
+        return m << sh;
+    }
+    int64_t s = -sh;
+    if (s >= 127) {
+        *lost = m != 0;
+        return m < 0 ? (i128)-1 : (i128)0;
+    }
+    i128 v = m >> s;
+    *lost = (v << s) != m;
+    return v;
+}
+
+struct T2Smem {
+    double T1[256], T2[256];
+    int32_t qm[EA_MAXD], qe[EA_MAXD];
+    uint64_t red_hi[EA_THREADS], red_lo[EA_THREADS];
+    int64_t red_i[EA_THREADS];
+    int32_t flag;
+};
+
+__device__ void block_reduce_i128(T2Smem& S, i128* v, uint64_t* err) {
+    int tid = threadIdx.x;
+    S.red_hi[tid] = (uint64_t)((u128)*v >> 64);
+    S.red_lo[tid] = (uint64_t)(u128)*v;
+    S.red_i[tid] = (int64_t)*err;
+    __syncthreads();
+    for (int s = EA_THREADS / 2; s > 0; s >>= 1) {
+        if (tid < s) {
+            u128 a = ((u128)S.red_hi[tid] << 64) | S.red_lo[tid];
+            u128 c = ((u128)S.red_hi[tid + s] << 64) | S.red_lo[tid + s];
+            u128 x = a + c;
+            S.red_hi[tid] = (uint64_t)(x >> 64);
+            S.red_lo[tid] = (uint64_t)x;
+            S.red_i[tid] += S.red_i[tid + s];
+        }
+        __syncthreads();
+    }
+    *v = (i128)(((u128)S.red_hi[0] << 64) | S.red_lo[0]);
+    *err = (uint64_t)S.red_i[0];
+    __syncthreads();
+}
+
+__device__ int block_max_i64(T2Smem& S, int64_t x, int64_t* out) {
+    int tid = threadIdx.x;
+    S.red_i[tid] = x;
+    __syncthreads();
+    for (int s = EA_THREADS / 2; s > 0; s >>= 1) {
+        if (tid < s) S.red_i[tid] = max(S.red_i[tid], S.red_i[tid + s]);
+        __syncthreads();
+    }
+    *out = S.red_i[0];
+    __syncthreads();
+    return 0;
+}
+
+__global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
+    __shared__ T2Smem S;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 256; i += EA_THREADS) {
+        S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
+        S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
+    }
+    __syncthreads();
+    const int cnt = *P.wl_cnt;
+    const int d = P.g.head_dim, dv = P.g.head_dim_v;
+    const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
+    int32_t* Mw = P.t2M + (int64_t)blockIdx.x * P.t2_keys;
+    int64_t* Ew = P.t2E + (int64_t)blockIdx.x * P.t2_keys;
+    for (int item = blockIdx.x; item < cnt; item += gridDim.x) {
+        const int64_t row = P.wl[item];
+        const int64_t b = row / ((int64_t)T * Hq);
+        const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
+        const int hk = hq / P.grp;
+        const int64_t tok = b * T + t;
+        const int64_t L = P.kv_len[tok];
+        const uint64_t mask = P.tree_mask ? P.tree_mask[tok] : 0ull;
+        const int64_t nkeys = L + __popcll(mask);
+        const int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
+        if (tid == 0) S.flag = 0;
+        const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
+        for (int i = tid; i < d; i += EA_THREADS) {
+            uint32_t x = qr[i];
+            int f = (x >> 7) & 0xFF;
+            int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+            S.qm[i] = (x & 0x8000) ? -m : m;
+            S.qe[i] = (f ? f : 1) - 134;
+            if (f == 0xFF) atomicMax(&S.flag, 2);
+        }
+        __syncthreads();
+        int myflag = 0;
+        if (nkeys > P.t2_keys) myflag = 1;  // workspace too small: not certified
+        // ---- scores, logits, weights: threads over keys
+        int64_t emax = INT64_MIN;
+        for (int64_t j = tid; j < nkeys && !myflag && S.flag < 2; j += EA_THREADS) {
+            int64_t n;
+            if (j < L) n = j;
+            else {
+                // (j - L)-th set bit of mask
+                uint64_t m = mask;
+                for (int64_t c = j - L; c > 0; --c) m &= m - 1;
+                n = P.tree_base[b] + (__ffsll((long long)m) - 1);
+            }
+            const uint16_t* kr = P.k + kv_off(P, b, n, hk, 0);
+            const uint16_t* vr = P.v + kv_off(P, b, n, hk, 1);
+            int lmax = INT_MIN;
+            bool bad = false;
+            for (int i = 0; i < d; ++i) {
+                uint32_t x = kr[i];
+                int f = (x >> 7) & 0xFF;
+                if (f == 0xFF) bad = true;
+                int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                int p = S.qm[i] * ((x & 0x8000) ? -m : m);
+                if (p) {
+                    int ap = p < 0 ? -p : p;
+                    int lead = S.qe[i] + (f ? f : 1) - 134 + (31 - __clz(ap));
+                    lmax = max(lmax, lead);
+                }
+            }
+            for (int i = 0; i < dv; ++i)
+                if (((vr[i] >> 7) & 0xFF) == 0xFF) bad = true;
+            if (bad) {
+                atomicMax(&S.flag, 2);
+                break;
+            }
+            int32_t M = 1 << 23;
+            int64_t E = -23;
+            if (lmax != INT_MIN && P.am != 0) {
+                int base = lmax + 1 - 120;
+                i128 acc = 0;
+                uint64_t err = 0;
+                for (int i = 0; i < d; ++i) {
+                    uint32_t x = kr[i];
+                    int f = (x >> 7) & 0xFF;
+                    int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                    int p = S.qm[i] * ((x & 0x8000) ? -m : m);
+                    if (!p) continue;
+                    int lost;
+                    acc += floor_shift128((i128)p, (int64_t)S.qe[i] + (f ? f : 1) - 134 - base, &lost);
+                    err += (uint64_t)lost;
+                }
+                uint32_t tlo = 0, thi = 0;
+                int slo = rn32_prod(P.am, acc, P.ae + base, &tlo);
+                int shi = err ? rn32_prod(P.am, acc + (i128)err, P.ae + base, &thi) : slo;
+                if (!err) thi = tlo;
+                if (slo == 2 && shi == 2) {
+                    atomicMax(&S.flag, 2);  // |alpha s| rounds above fp32 max: domain error
+                    break;
+                }
+                if (slo != 0 || shi != 0 || tlo != thi) {
+                    myflag = 1;
+                    break;
+                }
+                int32_t Mi;
+                int32_t Ei;
+                int ws = weight_f64(tlo, S.T1, S.T2, &Mi, &Ei);
+                if (ws == 0) {
+                    M = Mi;
+                    E = Ei;
+                } else {
+                    int ww = weight_wide(tlo, &M, &E);
+                    if (ww) {
+                        myflag = 1;
+                        break;
+                    }
+                }
+            }
+            Mw[j] = M;
+            Ew[j] = E;
+            emax = max(emax, E + 23);
+        }
+        if (myflag) atomicMax(&S.flag, 1);
+        __syncthreads();
+        int64_t R;
+        block_max_i64(S, emax, &R);
+        int fl = S.flag;
+        if (fl == 0 && nkeys > 0) {
+            int key_log2 = 0;
+            while (((int64_t)1 << key_log2) < nkeys) ++key_log2;
+            const int F = 126 - key_log2;
+            // Z
+            i128 z = 0;
+            uint64_t ze = 0;
+            for (int64_t j = tid; j < nkeys; j += EA_THREADS) {
+                int lost;
+                z += floor_shift128((i128)Mw[j], Ew[j] - (R - F), &lost);
+                ze += (uint64_t)lost;
+            }
+            block_reduce_i128(S, &z, &ze);
+            // N per channel: threads over channels, loop over keys
+            bool ok = true;
+            for (int c = tid; c < dv; c += EA_THREADS) {
+                int64_t NR = INT64_MIN;
+                for (int64_t j = 0; j < nkeys; ++j) {
+                    int64_t n;
+                    if (j < L) n = j;
+                    else {
+                        uint64_t m = mask;
+                        for (int64_t cc = j - L; cc > 0; --cc) m &= m - 1;
+                        n = P.tree_base[b] + (__ffsll((long long)m) - 1);
+                    }
+                    uint32_t x = P.v[kv_off(P, b, n, hk, 1) + c];
+                    if (!(x & 0x7FFF)) continue;
+                    int f = (x >> 7) & 0xFF;
+                    int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                    int64_t Lj = Ew[j] + 24 + (f ? f : 1) - 134 + (31 - __clz(m));
+                    NR = max(NR, Lj);
+                }
+                uint32_t bits = 0;
+                if (NR != INT64_MIN) {
+                    const int64_t base = NR - F;
+                    i128 acc = 0;
+                    uint64_t err = 0;
+                    for (int64_t j = 0; j < nkeys; ++j) {
+                        int64_t n;
+                        if (j < L) n = j;
+                        else {
+                            uint64_t m = mask;
+                            for (int64_t cc = j - L; cc > 0; --cc) m &= m - 1;
+                            n = P.tree_base[b] + (__ffsll((long long)m) - 1);
+                        }
+                        uint32_t x = P.v[kv_off(P, b, n, hk, 1) + c];
+                        if (!(x & 0x7FFF)) continue;
+                        int f = (x >> 7) & 0xFF;
+                        int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                        int64_t vm = (x & 0x8000) ? -m : m;
+                        int lost;
+                        acc += floor_shift128((i128)((int64_t)Mw[j] * vm), Ew[j] + (f ? f : 1) - 134 - base, &lost);
+                        err += (uint64_t)lost;
+                    }
+                    // interval [acc, acc+err] * 2^base over [z, z+ze] * 2^(R-F)
+                    i128 Zlo = z, Zhi = z + (i128)ze;
+                    i128 Nlo = acc, Nhi = acc + (i128)err;
+                    i128 ln, ld, hn, hd;
+                    if (Nlo >= 0) {
+                        ln = Nlo; ld = Zhi; hn = Nhi; hd = Zlo;
+                    } else if (Nhi <= 0) {
+                        ln = Nlo; ld = Zlo; hn = Nhi; hd = Zhi;
+                    } else {
+                        ln = Nlo; ld = Zlo; hn = Nhi; hd = Zlo;
+                    }
+                    int64_t sh = base - (R - F);
+                    int p = P.out_fp32 ? 24 : 8, qmin = P.out_fp32 ? -149 : -133;
+                    if (Zlo <= 0 || sh > 100000 || sh < -100000) {
+                        ok = false;
+                    } else {
+                        rnd rl = round_ratio(ln < 0 ? (u128)(-ln) : (u128)ln, (u128)ld, (int)sh, ln < 0 ? -1 : 1, p, qmin);
+                        rnd rh = round_ratio(hn < 0 ? (u128)(-hn) : (u128)hn, (u128)hd, (int)sh, hn < 0 ? -1 : 1, p, qmin);
+                        if (!rnd_eq(rl, rh)) ok = false;
+                        else bits = rnd_bits(rl, P.out_fp32);
+                    }
+                }
+                if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = bits;
+                else ((uint16_t*)P.out)[obase + c] = (uint16_t)bits;
+            }
+            if (!ok) atomicMax(&S.flag, 1);
+            __syncthreads();
+            fl = S.flag;
+        } else if (fl == 0) {
+            for (int c = tid; c < dv; c += EA_THREADS) {
+                if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
+                else ((uint16_t*)P.out)[obase + c] = 0;
+            }
+        }
+        if (fl != 0) {
+            for (int c = tid; c < dv; c += EA_THREADS) {
+                if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
+                else ((uint16_t*)P.out)[obase + c] = 0;
+            }
+        }
+        if (tid == 0) {
+            P.flags[row] = (uint8_t)fl;
+            if (P.stats) {
+                if (fl == 0) atomicAdd((unsigned long long*)&P.stats[2], 1ull);
+                if (fl == 1) atomicAdd((unsigned long long*)&P.stats[3], 1ull);
+                if (fl == 2) atomicAdd((unsigned long long*)&P.stats[4], 1ull);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Known-answer kernels over the device helpers
+// ------------------------------------------------------------------------------------------------
+__global__ void ea_kat_weight(int64_t n, const uint32_t* t, int32_t* M, int64_t* E, int32_t* st, int32_t* M2,
+                              int64_t* E2, int32_t* st2) {
+    __shared__ double T1[256], T2[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+        T1[i] = u64_as_f64(EA_T1_BITS[i]);
+        T2[i] = u64_as_f64(EA_T2_BITS[i]);
+    }
+    __syncthreads();
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int32_t m = 0, e = 0;
+    st[i] = weight_f64(t[i], T1, T2, &m, &e);
+    M[i] = m;
+    E[i] = e;
+    int32_t m2 = 0;
+    int64_t e2 = 0;
+    st2[i] = weight_wide(t[i], &m2, &e2);
+    M2[i] = m2;
+    E2[i] = e2;
+}
+
+__global__ void ea_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, uint32_t* bits, int32_t* ok) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t bb = 0;
+    ok[i] = certify_round(x[i], r[i], fp32, &bb) ? 1 : 0;
+    bits[i] = bb;
+}
+
+__global__ void ea_kat_round_ratio(int64_t n, const uint64_t* ah, const uint64_t* al, const uint64_t* bh,
+                                   const uint64_t* bl, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
+                                   int32_t* ov) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    u128 a = ((u128)ah[i] << 64) | al[i], b = ((u128)bh[i] << 64) | bl[i];
+    rnd r = round_ratio(a, b, E[i], neg[i] ? -1 : 1, fp32 ? 24 : 8, fp32 ? -149 : -133);
+    ov[i] = r.overflow;
+    bits[i] = r.overflow ? 0u : rnd_bits(r, fp32);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------------
+namespace {
+
+struct Plan {
+    int nsplit, split_len, rb, nrb, r_seg, grp, nseg, pshift, dlog;
+    int64_t rows;
+    size_t off_q64, off_qinfo, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
+    int t2_keys;
+};
+
+size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
+    if (!g || !o) return -1;
+    if (g->num_seqs < 0 || g->num_tokens <= 0 || g->num_q_heads <= 0 || g->num_kv_heads <= 0) return -1;
+    if (g->num_q_heads % g->num_kv_heads) return -1;
+    if (g->head_dim <= 0 || g->head_dim > EA_MAXD || (g->head_dim & 7)) return -1;
+    if (g->head_dim_v <= 0 || g->head_dim_v > EA_MAXDV || (g->head_dim_v & 1)) return -1;
+    if (g->page_size <= 0 || (g->page_size & (g->page_size - 1))) return -1;
+    if (g->max_seq_len < 0) return -1;
+    if (o->splits < 0) return -2;
+    pl->grp = g->num_q_heads / g->num_kv_heads;
+    pl->r_seg = g->num_tokens * pl->grp;
+    pl->rb = pl->r_seg < EA_MAXRB ? pl->r_seg : EA_MAXRB;
+    pl->nrb = (pl->r_seg + pl->rb - 1) / pl->rb;
+    pl->nseg = g->num_seqs * g->num_kv_heads;
+    pl->rows = (int64_t)g->num_seqs * g->num_tokens * g->num_q_heads;
+    int ps = 0;
+    while ((1 << ps) < g->page_size) ++ps;
+    pl->pshift = ps;
+    int dl = 0;
+    while ((1 << dl) < g->head_dim) ++dl;
+    pl->dlog = dl;
+    int maxlen = g->max_seq_len > 0 ? g->max_seq_len : 1;
+    int ns = o->splits;
+    if (ns == 0) {
+        // enough work items for 256 CUs x 2 blocks, splits of at least 256 keys
+        int64_t items = (int64_t)pl->nseg * pl->nrb;
+        ns = 1;
+        while (items * ns < 1024 && (int64_t)maxlen / (ns * 2) >= 256) ns *= 2;
+    }
+    int sl = (maxlen + ns - 1) / ns;
+    sl = (sl + EA_TILE - 1) / EA_TILE * EA_TILE;
+    if (sl < EA_TILE) sl = EA_TILE;
+    pl->split_len = sl;
+    pl->nsplit = (maxlen + sl - 1) / sl;
+    if (pl->nsplit < 1) pl->nsplit = 1;
+    int64_t R = pl->rows;
+    int dv = g->head_dim_v, d = g->head_dim;
+    size_t off = 0;
+    pl->off_q64 = off; off = align_up(off + (size_t)R * d * 8);
+    pl->off_qinfo = off; off = align_up(off + (size_t)R * 4);
+    pl->off_pR = off; off = align_up(off + (size_t)pl->nsplit * R * 4);
+    pl->off_pn = off; off = align_up(off + (size_t)pl->nsplit * R * 4);
+    pl->off_pZ = off; off = align_up(off + (size_t)pl->nsplit * R * 8);
+    pl->off_pN = off; off = align_up(off + (size_t)pl->nsplit * R * dv * 8);
+    pl->off_pV = off; off = align_up(off + (size_t)pl->nsplit * pl->nseg * pl->nrb * dv * 4);
+    pl->off_wl = off; off = align_up(off + (size_t)(R > 0 ? R : 1) * 4);
+    pl->off_cnt = off; off = align_up(off + 4);
+    pl->t2_keys = maxlen + 64;
+    pl->off_t2M = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 4);
+    pl->off_t2E = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 8);
+    pl->total = off;
+    return 0;
+}
+
+int herr(hipError_t e) { return e == hipSuccess ? 0 : -100 - (int)e; }
+
+}  // namespace
+
+extern "C" {
+
+const char* ea_hip_version(void) { return "exactattn_hip 0.1 (gfx950, fp64 tier 1, 128-bit tier 2)"; }
+
+int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* bytes, int32_t* nsplit) {
+    Plan pl;
+    int rc = make_plan(g, o, &pl);
+    if (rc) return rc;
+    if (bytes) *bytes = pl.total;
+    if (nsplit) *nsplit = pl.nsplit;
+    return 0;
+}
+
+int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, void* workspace,
+                     size_t workspace_bytes, ea_stream_t stream) {
+    Plan pl;
+    int rc = make_plan(g, o, &pl);
+    if (rc) return rc;
+    if (!bf || !bf->q || !bf->k || !bf->v || !bf->seq_len || !bf->kv_len || !bf->out || !bf->flags) return -1;
+    if (bf->tree_mask && !bf->tree_base) return -1;
+    if (workspace_bytes < pl.total || (!workspace && pl.total)) return -2;
+    uint32_t ab = o->alpha_bits;
+    if (((ab >> 23) & 0xFF) == 0xFF) return -3;
+    if (pl.rows == 0) return 0;
+    Params P;
+    memset(&P, 0, sizeof(P));
+    P.g = *g;
+    P.q = bf->q; P.k = bf->k; P.v = bf->v;
+    P.seq_len = bf->seq_len; P.kv_len = bf->kv_len; P.bt = bf->block_table; P.bt_off = bf->block_table_offset;
+    P.tree_mask = bf->tree_mask; P.tree_base = bf->tree_base;
+    P.out = bf->out; P.flags = bf->flags; P.stats = o->stats; P.merge_order = o->merge_order;
+    float af;
+    memcpy(&af, &ab, 4);
+    P.alpha = (double)af;
+    {
+        int ex = (ab >> 23) & 0xFF;
+        int32_t fr = ab & 0x7FFFFF;
+        int32_t m = ex ? (fr | 0x800000) : fr;
+        P.am = (ab >> 31) ? -m : m;
+        P.ae = ex ? ex - 150 : -149;
+    }
+    P.out_fp32 = o->out_fp32 ? 1 : 0;
+    P.nsplit = pl.nsplit; P.split_len = pl.split_len;
+    P.grp = pl.grp; P.r_seg = pl.r_seg; P.rb = pl.rb; P.nrb = pl.nrb; P.nseg = pl.nseg;
+    P.pshift = pl.pshift; P.dlog = pl.dlog; P.rows = pl.rows;
+    char* ws = (char*)workspace;
+    P.q64 = (double*)(ws + pl.off_q64);
+    P.qinfo = (int32_t*)(ws + pl.off_qinfo);
+    P.pR = (int32_t*)(ws + pl.off_pR);
+    P.pn = (int32_t*)(ws + pl.off_pn);
+    P.pZ = (double*)(ws + pl.off_pZ);
+    P.pN = (double*)(ws + pl.off_pN);
+    P.pV = (float*)(ws + pl.off_pV);
+    P.wl = (int32_t*)(ws + pl.off_wl);
+    P.wl_cnt = (int32_t*)(ws + pl.off_cnt);
+    P.t2M = (int32_t*)(ws + pl.off_t2M);
+    P.t2E = (int64_t*)(ws + pl.off_t2E);
+    P.t2_keys = pl.t2_keys;
+    hipStream_t st = (hipStream_t)stream;
+    unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
+    hipLaunchKernelGGL(ea_prep, dim3(rb4), dim3(256), 0, st, P);
+    rc = herr(hipGetLastError());
+    if (rc) return rc;
+    if (pl.nseg > 0) {
+        static std::once_flag once;
+        static hipError_t attr_err = hipSuccess;
+        std::call_once(once, [] {
+            attr_err = hipFuncSetAttribute((const void*)ea_split, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)sizeof(SplitSmem));
+        });
+        rc = herr(attr_err);
+        if (rc) return rc;
+        dim3 grid((unsigned)(pl.nseg * pl.nrb), (unsigned)pl.nsplit);
+        hipLaunchKernelGGL(ea_split, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
+        rc = herr(hipGetLastError());
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(ea_combine, dim3(rb4), dim3(256), 0, st, P);
+    rc = herr(hipGetLastError());
+    if (rc) return rc;
+    if (o->tier2) {
+        hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_THREADS), 0, st, P);
+        rc = herr(hipGetLastError());
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
+                     int dv, uint32_t alpha_bits, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
+                     int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
+                     uint8_t* flags, int64_t* stats) {
+    (void)acc_bits; (void)tile; (void)order_seed; (void)nthreads;
+    if (d <= 0 || d > EA_MAXD || dv <= 0 || dv > EA_MAXDV || splits <= 0 || rows < 0 || nkeys < 0) return -1;
+    if ((d & 7) || (dv & 1)) return -1;
+    if (((alpha_bits >> 23) & 0xFF) == 0xFF) return -3;
+    if (rows == 0) return 0;
+    // Each CSR row is one sequence whose page table is its key list (page size 1).
+    int64_t maxn = 0, nnz = row_ptr[rows];
+    for (int64_t r = 0; r < rows; ++r) maxn = row_ptr[r + 1] - row_ptr[r] > maxn ? row_ptr[r + 1] - row_ptr[r] : maxn;
+    if (maxn > INT32_MAX / 2 || nkeys > INT32_MAX) return -1;
+    ea_geometry g;
+    memset(&g, 0, sizeof(g));
+    g.num_seqs = (int32_t)rows; g.num_tokens = 1; g.num_q_heads = 1; g.num_kv_heads = 1;
+    g.head_dim = d; g.head_dim_v = dv;
+    g.q_seq_stride = d; g.q_tok_stride = 0; g.q_head_stride = 0;
+    g.o_seq_stride = dv; g.o_tok_stride = 0; g.o_head_stride = 0;
+    g.k_page_stride = d; g.k_slot_stride = 0; g.k_head_stride = 0;
+    g.v_page_stride = dv; g.v_slot_stride = 0; g.v_head_stride = 0;
+    g.page_size = 1; g.block_table_stride = 0; g.max_seq_len = (int32_t)maxn;
+    ea_options o;
+    memset(&o, 0, sizeof(o));
+    o.alpha_bits = alpha_bits; o.out_fp32 = fp32_out; o.splits = splits; o.tier2 = 1;
+    size_t ws_bytes = 0;
+    int32_t ns = 0;
+    int rc = ea_hip_workspace_size(&g, &o, &ws_bytes, &ns);
+    if (rc) return rc;
+    std::vector<int32_t> bt((size_t)(nnz > 0 ? nnz : 1)), sl((size_t)rows);
+    std::vector<int64_t> bo((size_t)rows);
+    for (int64_t r = 0; r < rows; ++r) {
+        sl[r] = (int32_t)(row_ptr[r + 1] - row_ptr[r]);
+        bo[r] = row_ptr[r];
+    }
+    for (int64_t j = 0; j < nnz; ++j) bt[j] = (int32_t)key_idx[j];
+    size_t osz = fp32_out ? 4 : 2;
+    void *dq = 0, *dk = 0, *dv_ = 0, *dbt = 0, *dbo = 0, *dsl = 0, *dout = 0, *dfl = 0, *dws = 0, *dst = 0;
+    hipError_t e = hipSuccess;
+#define EA_TRY(x) do { e = (x); if (e != hipSuccess) goto done; } while (0)
+    EA_TRY(hipMalloc(&dq, (size_t)rows * d * 2));
+    EA_TRY(hipMalloc(&dk, (size_t)(nkeys > 0 ? nkeys : 1) * d * 2));
+    EA_TRY(hipMalloc(&dv_, (size_t)(nkeys > 0 ? nkeys : 1) * dv * 2));
+    EA_TRY(hipMalloc(&dbt, bt.size() * 4));
+    EA_TRY(hipMalloc(&dbo, (size_t)rows * 8));
+    EA_TRY(hipMalloc(&dsl, (size_t)rows * 4));
+    EA_TRY(hipMalloc(&dout, (size_t)rows * dv * osz));
+    EA_TRY(hipMalloc(&dfl, (size_t)rows));
+    EA_TRY(hipMalloc(&dws, ws_bytes > 0 ? ws_bytes : 256));
+    EA_TRY(hipMalloc(&dst, 8 * sizeof(int64_t)));
+    EA_TRY(hipMemcpy(dq, q, (size_t)rows * d * 2, hipMemcpyHostToDevice));
+    if (nkeys > 0) {
+        EA_TRY(hipMemcpy(dk, k, (size_t)nkeys * d * 2, hipMemcpyHostToDevice));
+        EA_TRY(hipMemcpy(dv_, v, (size_t)nkeys * dv * 2, hipMemcpyHostToDevice));
+    }
+    EA_TRY(hipMemcpy(dbt, bt.data(), bt.size() * 4, hipMemcpyHostToDevice));
+    EA_TRY(hipMemcpy(dbo, bo.data(), (size_t)rows * 8, hipMemcpyHostToDevice));
+    EA_TRY(hipMemcpy(dsl, sl.data(), (size_t)rows * 4, hipMemcpyHostToDevice));
+    EA_TRY(hipMemset(dst, 0, 8 * sizeof(int64_t)));
+    {
+        ea_buffers b;
+        memset(&b, 0, sizeof(b));
+        b.q = (const uint16_t*)dq; b.k = (const uint16_t*)dk; b.v = (const uint16_t*)dv_;
+        b.seq_len = (const int32_t*)dsl; b.kv_len = (const int32_t*)dsl;
+        b.block_table = (const int32_t*)dbt; b.block_table_offset = (const int64_t*)dbo;
+        b.out = dout; b.flags = (uint8_t*)dfl;
+        o.stats = (int64_t*)dst;
+        rc = ea_hip_attention(&g, &b, &o, dws, ws_bytes, 0);
+        if (rc) goto done;
+    }
+    EA_TRY(hipDeviceSynchronize());
+    EA_TRY(hipMemcpy(out, dout, (size_t)rows * dv * osz, hipMemcpyDeviceToHost));
+    EA_TRY(hipMemcpy(flags, dfl, (size_t)rows, hipMemcpyDeviceToHost));
+    {
+        int64_t hs[8];
+        EA_TRY(hipMemcpy(hs, dst, sizeof(hs), hipMemcpyDeviceToHost));
+        if (stats) stats[2] += hs[1];
+    }
+done:
+    (void)hipFree(dq); (void)hipFree(dk); (void)hipFree(dv_); (void)hipFree(dbt); (void)hipFree(dbo);
+    (void)hipFree(dsl); (void)hipFree(dout); (void)hipFree(dfl); (void)hipFree(dws); (void)hipFree(dst);
+#undef EA_TRY
+    if (rc) return rc;
+    return herr(e);
+}
+
+int ea_hip_kat_weight(int64_t n, const uint32_t* t_bits, int32_t* M, int64_t* E, int32_t* status, int32_t* M2,
+                      int64_t* E2, int32_t* status2, ea_stream_t stream) {
+    if (n <= 0) return n < 0 ? -1 : 0;
+    hipLaunchKernelGGL(ea_kat_weight, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n, t_bits,
+                       M, E, status, M2, E2, status2);
+    return herr(hipGetLastError());
+}
+
+int ea_hip_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, uint32_t* bits, int32_t* ok,
+                     ea_stream_t stream) {
+    if (n <= 0) return n < 0 ? -1 : 0;
+    hipLaunchKernelGGL(ea_kat_round, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n, x, r,
+                       fp32, bits, ok);
+    return herr(hipGetLastError());
+}
+
+int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo, const uint64_t* b_hi,
+                           const uint64_t* b_lo, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
+                           int32_t* overflow, ea_stream_t stream) {
+    if (n <= 0) return n < 0 ? -1 : 0;
+    hipLaunchKernelGGL(ea_kat_round_ratio, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n,
+                       a_hi, a_lo, b_hi, b_lo, E, neg, fp32, bits, overflow);
+    return herr(hipGetLastError());
+}
+
+}  // extern "C"

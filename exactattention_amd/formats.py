@@ -1,0 +1,92 @@
+"""bf16/fp32 bit-pattern helpers of the public API (src/exactattn/formats.py:16-17,160-181 and
+src/exactattn/reference.py:164-173 of the reference): input generation and the default scale.
+None of these sits on the attention path itself."""
+
+from __future__ import annotations
+
+import math
+from functools import lru_cache
+
+import numpy as np
+
+
+class ExactAttentionDomainError(ValueError):
+    """An input is outside the definition's domain: NaN/inf, or an fp32-overflowing logit
+    (mirrors src/exactattn/formats.py:16-17)."""
+
+
+class ExactAttentionUncertifiedError(RuntimeError):
+    """A row that no device tier could certify. The library never substitutes a CPU result."""
+
+
+def float_to_bf16_bits(x) -> np.ndarray:
+    """RN-even conversion of float32-castable values to bf16 bit patterns (uint16), through float32
+    (src/exactattn/formats.py:160-176). For generating inputs only."""
+    f = np.asarray(x, dtype=np.float32)
+    if not np.all(np.isfinite(f)):
+        raise ExactAttentionDomainError("non-finite value")
+    u = f.view(np.uint32).astype(np.uint64)
+    out = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    if np.any((out & 0x7F80) == 0x7F80):
+        raise ExactAttentionDomainError("bf16 overflow when generating input")
+    return out
+
+
+def bf16_bits_to_float32(bits) -> np.ndarray:
+    """src/exactattn/formats.py:179-181."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def fp32_bits(x) -> int:
+    return int(np.asarray(x, dtype=np.float32).view(np.uint32))
+
+
+def _ln2_interval(W: int) -> tuple[int, int]:
+    # ln 2 = 2 atanh(1/3) = sum_k 2 / ((2k+1) 3^(2k+1)), both ends enclosed at scale 2^W
+    lo = hi = 0
+    k = 0
+    one = 1 << W
+    while True:
+        den = (2 * k + 1) * 3 ** (2 * k + 1)
+        t = (2 * one) // den
+        lo += t
+        hi += -((-2 * one) // den)
+        k += 1
+        if t == 0:
+            return lo, hi + 2
+
+
+def _rn32_ratio(num: int, den: int) -> int:
+    """fp32 bits of RN-even(num/den) for num, den > 0 (normal range)."""
+    k = num.bit_length() - den.bit_length()
+    if (num << max(0, -k)) < (den << max(0, k)):
+        k -= 1
+    qe = k - 23
+    n, d = (num, den << qe) if qe >= 0 else (num << -qe, den)
+    q, r = divmod(n, d)
+    if 2 * r > d or (2 * r == d and q & 1):
+        q += 1
+    if q == 1 << 24:
+        q >>= 1
+        qe += 1
+    return ((qe + 23 + 127) << 23) | (q - (1 << 23))
+
+
+@lru_cache(maxsize=None)
+def default_alpha_bits(d: int) -> int:
+    """fp32 bits of RN_fp32(log2(e) / sqrt(d)) = RN(1 / (ln 2 sqrt d)), decided by integer
+    enclosures with doubling precision (src/exactattn/reference.py:164-173 uses mpmath)."""
+    W = 80
+    while True:
+        L_lo, L_hi = _ln2_interval(W)
+        s = math.isqrt(d << (2 * W))
+        s_hi = s if s * s == (d << (2 * W)) else s + 1
+        lo = _rn32_ratio(1 << (2 * W), L_hi * s_hi)
+        hi = _rn32_ratio(1 << (2 * W), L_lo * s)
+        if lo == hi:
+            return lo
+        W *= 2
+
+
+def default_alpha(d: int) -> np.float32:
+    return np.array([default_alpha_bits(d)], dtype=np.uint32).view(np.float32)[0]

@@ -1,0 +1,214 @@
+"""ctypes binding of libexactattn_hip.so and the device-level launcher.
+
+`launch_hip` mirrors launch() of src/exactattn/triton_kernels.py:1324-1519: device tensors in,
+work enqueued on torch's current stream, no host transfer and no synchronisation, flags left on
+the device. `attention_problem` is the numpy-level round trip used by the public API.
+
+There is no CPU fallback: if the library is missing the calls raise, and a row that no device
+tier certifies is reported, never replaced by a host computation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from .formats import ExactAttentionDomainError, ExactAttentionUncertifiedError, fp32_bits
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libexactattn_hip.so")
+P = ctypes.c_void_p
+_lib = None
+
+GEOM_FIELDS = (["num_seqs", "num_tokens", "num_q_heads", "num_kv_heads", "head_dim", "head_dim_v"],
+               ["q_seq_stride", "q_tok_stride", "q_head_stride", "o_seq_stride", "o_tok_stride", "o_head_stride",
+                "k_page_stride", "k_slot_stride", "k_head_stride", "v_page_stride", "v_slot_stride", "v_head_stride"],
+               ["page_size", "block_table_stride", "max_seq_len", "pad0"])
+
+
+class Geometry(ctypes.Structure):
+    _fields_ = ([(n, ctypes.c_int32) for n in GEOM_FIELDS[0]] + [(n, ctypes.c_int64) for n in GEOM_FIELDS[1]]
+                + [(n, ctypes.c_int32) for n in GEOM_FIELDS[2]])
+
+
+class Buffers(ctypes.Structure):
+    _fields_ = [(n, P) for n in ("q", "k", "v", "seq_len", "kv_len", "block_table", "block_table_offset",
+                                 "tree_mask", "tree_base", "out", "flags")]
+
+
+class Options(ctypes.Structure):
+    _fields_ = [("alpha_bits", ctypes.c_uint32), ("out_fp32", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("reserved", ctypes.c_int32 * 4)]
+
+
+STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
+         "undecided_weights", "uncertified_final"]
+
+
+def available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def load():
+    """Load the in-tree library; raises if it was not built (no silent fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python -m exactattention_amd.build` (or "
+                               "__graft_entry__.build()) first; there is no CPU fallback")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.ea_hip_workspace_size.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Options),
+                                              ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_int32)]
+        lib.ea_hip_workspace_size.restype = ctypes.c_int
+        lib.ea_hip_attention.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), ctypes.POINTER(Options),
+                                         P, ctypes.c_size_t, P]
+        lib.ea_hip_attention.restype = ctypes.c_int
+        lib.ea_attention_hip.argtypes = [P, ctypes.c_int64, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int,
+                                         ctypes.c_uint32, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_uint64, ctypes.c_int, P, P, P]
+        lib.ea_attention_hip.restype = ctypes.c_int
+        lib.ea_hip_kat_weight.argtypes = [ctypes.c_int64] + [P] * 7 + [P]
+        lib.ea_hip_kat_weight.restype = ctypes.c_int
+        lib.ea_hip_kat_round.argtypes = [ctypes.c_int64, P, P, ctypes.c_int32, P, P, P]
+        lib.ea_hip_kat_round.restype = ctypes.c_int
+        lib.ea_hip_kat_round_ratio.argtypes = [ctypes.c_int64] + [P] * 6 + [ctypes.c_int32, P, P, P]
+        lib.ea_hip_kat_round_ratio.restype = ctypes.c_int
+        lib.ea_hip_version.restype = ctypes.c_char_p
+        _lib = lib
+    return _lib
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise ValueError(f"{what}: error code {rc}")
+
+
+def geometry(g: dict) -> Geometry:
+    return Geometry(**{f: int(g.get(f, 0)) for f, _ in Geometry._fields_})
+
+
+def _stream_ptr(torch):
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def workspace_size(g: dict, splits: int = 0, out_fp32: bool = False) -> tuple[int, int]:
+    lib = load()
+    o = Options(splits=splits, out_fp32=int(out_fp32), tier2=1)
+    nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
+    _check(lib.ea_hip_workspace_size(ctypes.byref(geometry(g)), ctypes.byref(o), ctypes.byref(nb), ctypes.byref(ns)),
+           "ea_hip_workspace_size")
+    return int(nb.value), int(ns.value)
+
+
+class DeviceProblem:
+    """A problem's arrays resident on the GPU, plus output, flags, workspace and stats buffers.
+    Built once; `launch_hip` then runs steps on it with no allocation."""
+
+    def __init__(self, prob: dict, out: str = "bf16", splits: int = 0, device: str = "cuda"):
+        import torch
+        self.torch = torch
+        self.prob = prob
+        self.geom = dict(prob["geom"])
+        self.out_fp32 = out == "fp32"
+        self.splits = splits
+        dev = torch.device(device)
+
+        def t(a, dt=None):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            if a.dtype == np.uint16:
+                a = a.view(np.int16)
+            elif a.dtype == np.uint64:
+                a = a.view(np.int64)
+            return torch.from_numpy(a).to(dev)
+
+        self.t = {k: t(prob.get(k)) for k in ("q", "k", "v", "seq_len", "kv_len", "block_table",
+                                               "block_table_offset", "tree_mask", "tree_base")}
+        rows = int(np.prod(prob["out_shape"][:3]))
+        self.rows = rows
+        self.out = torch.empty(prob["out_shape"], dtype=torch.int32 if self.out_fp32 else torch.int16, device=dev)
+        self.flags = torch.empty(rows, dtype=torch.uint8, device=dev)
+        nb, self.nsplit = workspace_size(self.geom, splits, self.out_fp32)
+        self.workspace = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
+        self.ws_bytes = nb
+        self.stats = torch.zeros(8, dtype=torch.int64, device=dev)
+        self._geom_c = geometry(self.geom)
+
+    def buffers(self) -> Buffers:
+        ptr = {k: (None if v is None else v.data_ptr()) for k, v in self.t.items()}
+        return Buffers(**ptr, out=self.out.data_ptr(), flags=self.flags.data_ptr())
+
+
+def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True) -> None:
+    """Enqueue one step on torch's current stream (no sync, no host copies, no allocation)."""
+    lib = load()
+    mo = None
+    if merge_order is not None:
+        mo = merge_order if hasattr(merge_order, "data_ptr") else None
+    o = Options(alpha_bits=alpha_bits, out_fp32=int(dp.out_fp32), splits=dp.splits, tier2=int(tier2),
+                merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr())
+    b = dp.buffers()
+    _check(lib.ea_hip_attention(ctypes.byref(dp._geom_c), ctypes.byref(b), ctypes.byref(o), dp.workspace.data_ptr(),
+                                dp.ws_bytes, _stream_ptr(dp.torch)), "ea_hip_attention")
+
+
+def merge_order_tensor(order, nsplit: int, device="cuda"):
+    """Keep the caller's order for splits that exist, append the rest (as the reference launcher
+    does, src/exactattn/triton_kernels.py:1471-1479)."""
+    import torch
+    given = [int(i) for i in order if 0 <= int(i) < nsplit]
+    seen = set()
+    given = [i for i in given if not (i in seen or seen.add(i))]
+    full = given + [i for i in range(nsplit) if i not in given]
+    return torch.tensor(full, dtype=torch.int32, device=device)
+
+
+def attention_problem(prob: dict, alpha, out: str = "bf16", splits: int = 0, merge_order=None, tier2: bool = True,
+                      fallback: bool = True, device: str = "cuda"):
+    """Run a problem on the GPU. Returns (out bits shaped (B, T, Hq, dv): uint16 for bf16, uint32
+    for fp32; flags (rows,) uint8; stats dict). With fallback=True, flag 2 raises
+    ExactAttentionDomainError and flag 1 raises ExactAttentionUncertifiedError."""
+    import torch
+    alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
+    dp = DeviceProblem(prob, out, splits, device)
+    mo = merge_order_tensor(merge_order, dp.nsplit, device) if merge_order is not None else None
+    launch_hip(dp, int(alpha_bits), mo, tier2)
+    torch.cuda.synchronize()
+    res = dp.out.cpu().numpy()
+    res = res.view(np.uint32) if dp.out_fp32 else res.view(np.uint16)
+    flags = dp.flags.cpu().numpy()
+    st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    st["nsplit"] = dp.nsplit
+    if fallback:
+        if np.any(flags == 2):
+            raise ExactAttentionDomainError(f"non-finite input or fp32 logit overflow in rows "
+                                            f"{np.flatnonzero(flags == 2)[:8].tolist()}")
+        if np.any(flags == 1):
+            raise ExactAttentionUncertifiedError(f"rows {np.flatnonzero(flags == 1)[:8].tolist()} not certified "
+                                                 "by any device tier")
+    return res, flags, st
+
+
+def ea_attention_hip(q, k, v, alpha_bits, row_ptr, key_idx, out="bf16", splits=8):
+    """The drop-in C entry point (host pointers, same arguments as the reference's
+    ea_attention_cpu). Returns (out bits, flags, stats[3])."""
+    lib = load()
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    rows, d = q.shape
+    n, dv = v.shape
+    rp = np.ascontiguousarray(row_ptr, dtype=np.int64)
+    ki = np.ascontiguousarray(key_idx, dtype=np.int64)
+    fp32 = out == "fp32"
+    res = np.zeros((rows, dv), dtype=np.uint32 if fp32 else np.uint16)
+    flags = np.zeros(rows, dtype=np.uint8)
+    st = np.zeros(3, dtype=np.int64)
+    rc = lib.ea_attention_hip(q.ctypes.data, rows, d, k.ctypes.data, v.ctypes.data, n, dv, int(alpha_bits),
+                              rp.ctypes.data, ki.ctypes.data, int(fp32), 64, 64, splits, 0, 1, res.ctypes.data,
+                              flags.ctypes.data, st.ctypes.data)
+    _check(rc, "ea_attention_hip")
+    return res, flags, st

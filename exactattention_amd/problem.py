@@ -1,0 +1,131 @@
+"""Serving-geometry problems: one description of queries, a (paged) KV cache and per-row key sets.
+
+A problem is a plain dict of numpy arrays and integers, the host-side image of the C ABI's
+ea_geometry + ea_buffers (include/exactattn_hip.h):
+
+    geom            dict of the ea_geometry fields
+    q               (B, T, Hq, d) uint16 bf16 bits (any strides are expressed through geom)
+    k, v            KV cache storage (contiguous (B, Hkv, S, d) or a page pool)
+    seq_len         (B,) int32 keys stored per sequence
+    kv_len          (B*T,) int32 visible prefix per query token
+    block_table     optional int32 page table, block_table_offset optional int64 per sequence
+    tree_mask       optional (B*T,) uint64, tree_base (B,) int32
+    out_shape       (B, T, Hq, dv)
+
+Rows are (sequence, token, query head) in that order. The same dict drives the device library
+and, in tests, the CPU oracle, so both see exactly the same inputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def _geom(B, T, Hq, Hkv, d, dv, q_strides, o_strides, k_strides, v_strides, page_size, bt_stride, max_seq_len):
+    g = dict(num_seqs=B, num_tokens=T, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=d, head_dim_v=dv,
+             q_seq_stride=q_strides[0], q_tok_stride=q_strides[1], q_head_stride=q_strides[2],
+             o_seq_stride=o_strides[0], o_tok_stride=o_strides[1], o_head_stride=o_strides[2],
+             k_page_stride=k_strides[0], k_slot_stride=k_strides[1], k_head_stride=k_strides[2],
+             v_page_stride=v_strides[0], v_slot_stride=v_strides[1], v_head_stride=v_strides[2],
+             page_size=page_size, block_table_stride=bt_stride, max_seq_len=max_seq_len)
+    return {k: int(x) for k, x in g.items()}
+
+
+def contiguous(q, k, v, kv_len, seq_len=None, tree_mask=None, tree_base=None):
+    """q (B, T, Hq, d); k (B, Hkv, S, d); v (B, Hkv, S, dv); kv_len (B, T)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    B, T, Hq, d = q.shape
+    _, Hkv, S, dv = v.shape
+    kv_len = np.ascontiguousarray(np.asarray(kv_len, dtype=np.int32).reshape(B * T))
+    seq_len = np.full(B, S, np.int32) if seq_len is None else np.ascontiguousarray(seq_len, dtype=np.int32)
+    g = _geom(B, T, Hq, Hkv, d, dv, (T * Hq * d, Hq * d, d), (T * Hq * dv, Hq * dv, dv),
+              (Hkv * S * d, d, S * d), (Hkv * S * dv, dv, S * dv), 1, 0, S)
+    return dict(geom=g, q=q, k=k, v=v, seq_len=seq_len, kv_len=kv_len, block_table=None, block_table_offset=None,
+                tree_mask=None if tree_mask is None else np.ascontiguousarray(tree_mask, dtype=np.uint64).reshape(-1),
+                tree_base=None if tree_base is None else np.ascontiguousarray(tree_base, dtype=np.int32),
+                out_shape=(B, T, Hq, dv))
+
+
+def paged(q, k_pages, v_pages, block_table, kv_len, seq_len, layout="NHD", tree_mask=None, tree_base=None):
+    """Paged cache. NHD pages: (num_pages, page_size, Hkv, d); HND: (num_pages, Hkv, page_size, d).
+    block_table (B, max_pages) int32."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k_pages = np.ascontiguousarray(k_pages, dtype=np.uint16)
+    v_pages = np.ascontiguousarray(v_pages, dtype=np.uint16)
+    B, T, Hq, d = q.shape
+    dv = v_pages.shape[-1]
+    if layout == "NHD":
+        _, P, Hkv, _ = k_pages.shape
+        ks = (P * Hkv * d, Hkv * d, d)
+        vs = (P * Hkv * dv, Hkv * dv, dv)
+    elif layout == "HND":
+        _, Hkv, P, _ = k_pages.shape
+        ks = (Hkv * P * d, d, P * d)
+        vs = (Hkv * P * dv, dv, P * dv)
+    else:
+        raise ValueError(layout)
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    seq_len = np.ascontiguousarray(seq_len, dtype=np.int32)
+    g = _geom(B, T, Hq, Hkv, d, dv, (T * Hq * d, Hq * d, d), (T * Hq * dv, Hq * dv, dv), ks, vs, P, bt.shape[1],
+              int(seq_len.max(initial=0)))
+    return dict(geom=g, q=q, k=k_pages, v=v_pages, seq_len=seq_len,
+                kv_len=np.ascontiguousarray(np.asarray(kv_len, dtype=np.int32).reshape(B * T)),
+                block_table=bt, block_table_offset=None,
+                tree_mask=None if tree_mask is None else np.ascontiguousarray(tree_mask, dtype=np.uint64).reshape(-1),
+                tree_base=None if tree_base is None else np.ascontiguousarray(tree_base, dtype=np.int32),
+                out_shape=(B, T, Hq, dv))
+
+
+def csr(q, k, v, row_ptr, key_idx):
+    """The reference CPU ABI's form (csrc/exact_attention_cpu.cpp:585-588): q (R, d), k (n, d),
+    v (n, dv), row r attends key_idx[row_ptr[r]:row_ptr[r+1]]. Each row becomes a sequence whose
+    page table is its key list (page size 1)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    R, d = q.shape
+    dv = v.shape[1]
+    row_ptr = np.asarray(row_ptr, dtype=np.int64)
+    lens = (row_ptr[1:] - row_ptr[:-1]).astype(np.int32)
+    bt = np.ascontiguousarray(np.asarray(key_idx, dtype=np.int32).reshape(-1))
+    if bt.size == 0:
+        bt = np.zeros(1, np.int32)
+    g = _geom(R, 1, 1, 1, d, dv, (d, 0, 0), (dv, 0, 0), (d, 0, 0), (dv, 0, 0), 1, 0, int(lens.max(initial=0)))
+    return dict(geom=g, q=q.reshape(R, 1, 1, d), k=k, v=v, seq_len=lens, kv_len=lens.copy(), block_table=bt,
+                block_table_offset=np.ascontiguousarray(row_ptr[:-1]), tree_mask=None, tree_base=None,
+                out_shape=(R, 1, 1, dv))
+
+
+def to_paged(prob: dict, page_size: int, rng: np.random.Generator, layout: str = "NHD", extra_pages: int = 3) -> dict:
+    """The same problem (same keys per sequence) stored in a shuffled page pool."""
+    g = prob["geom"]
+    assert prob["block_table"] is None
+    B, Hkv, d, dv = g["num_seqs"], g["num_kv_heads"], g["head_dim"], g["head_dim_v"]
+    S = prob["k"].shape[2]
+    k, v = prob["k"], prob["v"]
+    npp = -(-S // page_size)
+    n_pages = B * npp + extra_pages
+    perm = rng.permutation(n_pages)
+    bt = perm[:B * npp].reshape(B, npp).astype(np.int32)
+    shape_k = (n_pages, page_size, Hkv, d) if layout == "NHD" else (n_pages, Hkv, page_size, d)
+    shape_v = (n_pages, page_size, Hkv, dv) if layout == "NHD" else (n_pages, Hkv, page_size, dv)
+    kp = rng.integers(0, 1 << 14, size=shape_k, dtype=np.uint16)  # finite junk in unused slots
+    vp = rng.integers(0, 1 << 14, size=shape_v, dtype=np.uint16)
+    for b in range(B):
+        for p in range(npp):
+            s0, s1 = p * page_size, min(S, (p + 1) * page_size)
+            if layout == "NHD":
+                kp[bt[b, p], :s1 - s0] = k[b, :, s0:s1].transpose(1, 0, 2)
+                vp[bt[b, p], :s1 - s0] = v[b, :, s0:s1].transpose(1, 0, 2)
+            else:
+                kp[bt[b, p], :, :s1 - s0] = k[b, :, s0:s1]
+                vp[bt[b, p], :, :s1 - s0] = v[b, :, s0:s1]
+    kv_len = prob["kv_len"].reshape(B, -1)
+    return paged(prob["q"], kp, vp, bt, kv_len, prob["seq_len"], layout, prob["tree_mask"], prob["tree_base"])
+
+
+def flat_rows(prob: dict, out: np.ndarray) -> np.ndarray:
+    """(rows, dv) view of an output array in row order (sequence, token, query head)."""
+    return np.asarray(out).reshape(-1, prob["geom"]["head_dim_v"])

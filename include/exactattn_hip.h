@@ -1,0 +1,132 @@
+/*
+ * exactattn_hip: certified split-KV ExactAttention on AMD Instinct MI355X (gfx950).
+ *
+ * C ABI of libexactattn_hip.so. Plain pointers, sizes and a hipStream_t; no torch types.
+ * Every returned bf16/fp32 bit pattern equals the ExactAttention definition (the reference's
+ * docs/SPEC.md): o_c = RN(N_c / Z) with exact scores, t = RN32(alpha*s), w = RN24(2^t).
+ *
+ * Return codes: 0 = success; -1 invalid shape/geometry, -2 invalid option, -3 non-finite alpha
+ * (the same convention as the reference's ea_attention_cpu, csrc/exact_attention_cpu.cpp:589-592);
+ * -100 - e for a HIP runtime error e. Nothing throws across this ABI.
+ *
+ * Per-row flags (uint8), the reference's meaning (csrc/exact_attention_cpu.cpp:580-584):
+ *   0 = certified (bits equal the definition)
+ *   1 = not certified by any device tier (the row's output is +0 and must not be used)
+ *   2 = domain error: a NaN/inf input in the row's visible set, or an fp32 logit overflow
+ */
+#ifndef EXACTATTN_HIP_H
+#define EXACTATTN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ea_stream_t; /* = hipStream_t */
+
+/*
+ * Serving geometry. Rows are (sequence b, token t, query head h), enumerated in that order
+ * (flags and stats index them so). Sequence b's keys 0 .. seq_len[b]-1 live in a paged or
+ * contiguous cache; query head h reads KV head h / (num_q_heads / num_kv_heads) (GQA).
+ *
+ * Element addresses, in uint16 elements:
+ *   q[b, t, h, i]     = q + b*q_seq_stride + t*q_tok_stride + h*q_head_stride + i
+ *   out[b, t, h, c]   = out + b*o_seq_stride + t*o_tok_stride + h*o_head_stride + c (bf16 or fp32 units)
+ *   key n of seq b:   page = block_table ? block_table[off_b + n / page_size] : b,
+ *                     slot = block_table ? n % page_size : n,
+ *                     off_b = block_table_offset ? block_table_offset[b] : b*block_table_stride
+ *   K[b, n, hk, i]    = k + page*k_page_stride + slot*k_slot_stride + hk*k_head_stride + i  (V alike)
+ * Row (b, t, h) attends keys n < kv_len[b*T + t], plus, with tree_mask, keys tree_base[b] + i for
+ * every set bit i of tree_mask[b*T + t] (speculative tree verification). Causal prefill, chunked
+ * prefill, decode and verification chains are all kv_len prefixes.
+ */
+typedef struct ea_geometry {
+    int32_t num_seqs, num_tokens, num_q_heads, num_kv_heads, head_dim, head_dim_v;
+    int64_t q_seq_stride, q_tok_stride, q_head_stride;
+    int64_t o_seq_stride, o_tok_stride, o_head_stride;
+    int64_t k_page_stride, k_slot_stride, k_head_stride;
+    int64_t v_page_stride, v_slot_stride, v_head_stride;
+    int32_t page_size;          /* power of two; ignored without a block table */
+    int32_t block_table_stride; /* entries per sequence when block_table_offset is NULL */
+    int32_t max_seq_len;        /* >= every seq_len[b] (sizes the split grid) */
+    int32_t pad0;
+} ea_geometry;
+
+/* Device pointers. seq_len, kv_len required; block_table, block_table_offset, tree_mask,
+ * tree_base optional (NULL). out: bf16 bits (uint16) or fp32; flags: one uint8 per row. */
+typedef struct ea_buffers {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const int32_t* seq_len;
+    const int32_t* kv_len;
+    const int32_t* block_table;
+    const int64_t* block_table_offset;
+    const uint64_t* tree_mask;
+    const int32_t* tree_base;
+    void* out;
+    uint8_t* flags;
+} ea_buffers;
+
+typedef struct ea_options {
+    uint32_t alpha_bits;    /* fp32 bit pattern of the base-2 logit scale */
+    int32_t out_fp32;       /* 0 = bf16 output, 1 = fp32 output */
+    int32_t splits;         /* KV splits per segment; 0 = choose for the device */
+    int32_t tier2;          /* 1 = run the device tier 2 on rows tier 1 leaves uncertified */
+    const int32_t* merge_order; /* optional device permutation of [0, nsplit): combine order */
+    int64_t* stats;         /* optional device int64[8], accumulated (+=):
+                               [0] rows, [1] rows flagged by tier 1, [2] rows certified by tier 2,
+                               [3] rows left flag 1, [4] rows flag 2, [5] uncertified scores,
+                               [6] undecided weights, [7] uncertified final roundings */
+    int32_t reserved[4];
+} ea_options;
+
+/* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
+ * the split count it will use. Reference counterpart: none (the Triton launcher allocates its
+ * partial buffers itself, src/exactattn/triton_kernels.py:1411-1448). */
+int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* bytes, int32_t* nsplit);
+
+/* Enqueue one certified attention step on `stream`: q prep, tier-1 split kernel, combine with
+ * certified rounding, device tier 2 for rows tier 1 could not certify. No host transfer, no
+ * synchronisation, fixed grids: capturable in a hipGraph. The caller owns every buffer; the
+ * library retains nothing after the work completes.
+ * Replaces launch() of src/exactattn/triton_kernels.py:1324-1519 (split kernel + combine +
+ * tier 2), extended with paged KV, GQA segments and tree masks. */
+int ea_hip_attention(const ea_geometry* g, const ea_buffers* b, const ea_options* o, void* workspace,
+                     size_t workspace_bytes, ea_stream_t stream);
+
+/* Drop-in for the reference CPU ABI ea_attention_cpu (csrc/exact_attention_cpu.cpp:585-588),
+ * same arguments and meaning, host pointers; computes on the current HIP device and returns when
+ * done. `acc_bits`, `tile`, `nthreads` and `order_seed` are accepted and ignored (they cannot
+ * change certified bits). `alpha` is passed as its fp32 bits. Flags 1 mean "not certified on the
+ * device"; stats[0..2] += score, weight and final-rounding fallbacks of tier 1. */
+int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
+                     int dv, uint32_t alpha_bits, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
+                     int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
+                     uint8_t* flags, int64_t* stats);
+
+/* Known-answer entry points over the device helper routines (device arrays, n elements).
+ * ea_hip_kat_weight: w = RN24(2^t) for fp32 t bits -> M, E, status (0 certified by the fp64
+ *   tier-1 path, 1 undecided there; wide tier-2 value in M2/E2 with status2 0/1).
+ *   Reference counterpart: exp2.exp2_weight_int_np (src/exactattn/exp2.py:187-195).
+ * ea_hip_kat_round: RN of the fp64 interval [x - r, x + r] into bf16/fp32 -> bits, certified.
+ *   Reference counterpart: the combine's _ratio_round (src/exactattn/triton_kernels.py:150-195).
+ * ea_hip_kat_round_ratio: RN-even of (a/b)*2^E, a,b 128-bit -> bits, overflow.
+ *   Reference counterpart: ea_round_ratio (csrc/exact_attention_cpu.cpp:632-638). */
+int ea_hip_kat_weight(int64_t n, const uint32_t* t_bits, int32_t* M, int64_t* E, int32_t* status, int32_t* M2,
+                      int64_t* E2, int32_t* status2, ea_stream_t stream);
+int ea_hip_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, uint32_t* bits, int32_t* ok,
+                     ea_stream_t stream);
+int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo, const uint64_t* b_hi,
+                           const uint64_t* b_lo, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
+                           int32_t* overflow, ea_stream_t stream);
+
+/* Library version string. */
+const char* ea_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

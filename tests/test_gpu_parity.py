@@ -1,0 +1,247 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle, bit for bit.
+
+Every comparison is exact equality of bf16/fp32 bit patterns. The oracle is the C restatement of
+the reference's certified CPU kernel plus the Python exact definition for the rows it flags.
+"""
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from exactattention_amd import configs, problem
+from exactattention_amd.formats import default_alpha_bits
+from gen import KINDS, bf16
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _run(prob, alpha_bits, out="bf16", splits=0, merge_order=None):
+    from exactattention_amd.hip import attention_problem
+    return attention_problem(prob, alpha_bits, out, splits, merge_order, True, False)
+
+
+def _oracle(prob, alpha_bits, out="bf16"):
+    from oracle import oracle
+    return oracle.attention_geom(prob, alpha_bits, out)
+
+
+def _rand_problem(rng, kind, vkind, B, T, Hq, Hkv, S, d, dv, causal=True):
+    q = bf16(rng, (B, T, Hq, d), kind)
+    k = bf16(rng, (B, Hkv, S, d), kind)
+    v = bf16(rng, (B, Hkv, S, dv), vkind)
+    seq = rng.integers(max(1, S // 2), S + 1, size=B)
+    if causal:
+        kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    else:
+        kv = np.repeat(seq[:, None], T, axis=1)
+    return problem.contiguous(q, k, v, kv, seq_len=seq)
+
+
+# ---------------------------------------------------------------------------------------------
+# helper known-answer tests
+# ---------------------------------------------------------------------------------------------
+
+def test_weight_kat_matches_oracle(gpu):
+    import torch
+    from exactattention_amd import hip
+    from oracle import exact
+    rng = np.random.default_rng(5)
+    ts = np.concatenate([rng.uniform(-60, 60, 20000), rng.uniform(-1e-6, 1e-6, 500),
+                         np.arange(-40, 40) + rng.uniform(-1e-7, 1e-7, 80), rng.uniform(-1e4, 1e4, 2000),
+                         np.float32(2.0) ** rng.uniform(-40, -20, 500) * rng.choice([-1, 1], 500),
+                         [0.0, -0.0, 1.0, -1.0, 2.0 ** -25, -(2.0 ** -25), 2.0 ** -26, 0.99999994, 1e9, -1e9]])
+    tb = np.float32(ts).view(np.uint32)
+    n = tb.size
+    dev = {k: torch.zeros(n, dtype=dt, device="cuda") for k, dt in
+           (("M", torch.int32), ("E", torch.int64), ("st", torch.int32), ("M2", torch.int32), ("E2", torch.int64),
+            ("st2", torch.int32))}
+    tt = torch.from_numpy(tb.view(np.int32)).cuda()
+    rc = hip.load().ea_hip_kat_weight(n, tt.data_ptr(), *[dev[k].data_ptr() for k in ("M", "E", "st", "M2", "E2", "st2")],
+                                      torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    h = {k: v.cpu().numpy() for k, v in dev.items()}
+    undecided = 0
+    for i in range(n):
+        tm, te = exact.decode_fp32_bits(int(tb[i]))
+        big = abs(float(np.float32(ts[i]))) >= 2 ** 30
+        want = exact.exp2_rn(tm, te) if not big else None
+        if h["st"][i] == 0:
+            assert (int(h["M"][i]), int(h["E"][i])) == want, ts[i]
+        else:
+            undecided += 1
+            assert big or h["st"][i] == 1
+        if not big:
+            assert h["st2"][i] == 0 and (int(h["M2"][i]), int(h["E2"][i])) == want, ts[i]
+    assert undecided <= 12, undecided  # fp64 path leaves ~2^-25 of weights (+ the 2 out-of-range)
+
+
+def test_round_ratio_kat_matches_oracle(gpu):
+    import torch
+    from exactattention_amd import hip
+    from oracle import oracle
+    rng = np.random.default_rng(9)
+    cases = []
+    for _ in range(4000):
+        ab, bb = int(rng.integers(1, 127)), int(rng.integers(1, 127))
+        a = int(rng.integers(1, 1 << min(ab, 62))) << max(0, ab - 62)
+        b = int(rng.integers(1, 1 << min(bb, 62))) << max(0, bb - 62)
+        cases.append((a | int(rng.integers(0, 2)), b, int(rng.integers(-300, 200)), int(rng.integers(0, 2))))
+    for fp32 in (0, 1):
+        n = len(cases)
+        arr = lambda f, dt: torch.from_numpy(np.array([f(c) for c in cases], dtype=dt)).cuda()
+        ah = arr(lambda c: c[0] >> 64, np.uint64).view(torch.int64)
+        al = arr(lambda c: c[0] & ((1 << 64) - 1), np.uint64).view(torch.int64)
+        bh = arr(lambda c: c[1] >> 64, np.uint64).view(torch.int64)
+        bl = arr(lambda c: c[1] & ((1 << 64) - 1), np.uint64).view(torch.int64)
+        E = arr(lambda c: c[2], np.int32)
+        ng = arr(lambda c: c[3], np.int32)
+        bits = torch.zeros(n, dtype=torch.int32, device="cuda")
+        ov = torch.zeros(n, dtype=torch.int32, device="cuda")
+        rc = hip.load().ea_hip_kat_round_ratio(n, ah.data_ptr(), al.data_ptr(), bh.data_ptr(), bl.data_ptr(),
+                                               E.data_ptr(), ng.data_ptr(), fp32, bits.data_ptr(), ov.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        gb, go = bits.cpu().numpy().view(np.uint32), ov.cpu().numpy()
+        for i, (a, b, e, neg) in enumerate(cases):
+            wb, wo = oracle.round_ratio_bits(a, b, e, bool(neg), bool(fp32))
+            assert bool(go[i]) == wo, (a, b, e, neg, fp32)
+            if not wo:
+                assert int(gb[i]) == wb, (a, b, e, neg, fp32)
+
+
+def test_certify_round_kat(gpu):
+    """certify_round on exact points (r = 0) equals RN of the point; with r > 0 it never certifies
+    an interval that holds a rounding midpoint."""
+    import torch
+    from exactattention_amd import hip
+    from oracle import exact
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(3000) * np.exp2(rng.uniform(-140, 120, 3000)),
+                        np.float32(rng.standard_normal(500)).astype(np.float64)])
+    for fp32 in (0, 1):
+        p = 24 if fp32 else 8
+        # exact midpoints between adjacent values: never certified with r > 0
+        r0 = np.zeros_like(x)
+        xs = torch.from_numpy(x).cuda()
+        rs = torch.from_numpy(r0).cuda()
+        bits = torch.zeros(x.size, dtype=torch.int32, device="cuda")
+        ok = torch.zeros(x.size, dtype=torch.int32, device="cuda")
+        assert hip.load().ea_hip_kat_round(x.size, xs.data_ptr(), rs.data_ptr(), fp32, bits.data_ptr(), ok.data_ptr(),
+                                           torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        gb, gk = bits.cpu().numpy().view(np.uint32), ok.cpu().numpy()
+        fmt = exact.FP32 if fp32 else exact.BF16
+        enc = exact.encode_fp32 if fp32 else exact.encode_bf16
+        n_ok = 0
+        for i, xv in enumerate(x.tolist()):
+            num, den = float(xv).as_integer_ratio()
+            m, e = exact.round_rational(num, den, fmt)
+            want = 0 if m == 0 else enc(m, e)
+            if gk[i]:
+                n_ok += 1
+                assert int(gb[i]) == want, (xv, fp32)
+        assert n_ok > 0.9 * x.size
+
+
+# ---------------------------------------------------------------------------------------------
+# rows against the oracle
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("vkind", ["normal", "wide", "dupes"])
+def test_random_rows_match_oracle(gpu, kind, vkind):
+    rng = np.random.default_rng(hash((kind, vkind)) % (1 << 32))
+    prob = _rand_problem(rng, kind, vkind, B=2, T=3, Hq=4, Hkv=2, S=150, d=64, dv=64)
+    ab = default_alpha_bits(64)
+    want, _ = _oracle(prob, ab)
+    got, flags, st = _run(prob, ab, splits=3)
+    assert not np.any(flags == 1), (flags, st)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("out", ["bf16", "fp32"])
+def test_d128_rows_match_oracle_and_split_invariance(gpu, out):
+    rng = np.random.default_rng(11)
+    prob = _rand_problem(rng, "normal", "normal", B=3, T=2, Hq=4, Hkv=2, S=700, d=128, dv=128)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab, out)
+    for splits in (1, 2, 3, 7, 11):
+        got, flags, st = _run(prob, ab, out, splits=splits, merge_order=list(range(64))[::-1])
+        assert not np.any(flags), (splits, st)
+        assert np.array_equal(got, want), splits
+
+
+def test_paged_layouts_and_page_sizes_same_bits(gpu):
+    rng = np.random.default_rng(12)
+    base = _rand_problem(rng, "outlier", "normal", B=3, T=1, Hq=8, Hkv=4, S=333, d=128, dv=128, causal=False)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(base, ab)
+    for ps in (1, 16, 64):
+        for layout in ("NHD", "HND"):
+            p = problem.to_paged(base, ps, np.random.default_rng(ps), layout)
+            got, flags, _ = _run(p, ab, splits=4)
+            assert not np.any(flags)
+            assert np.array_equal(got, want), (ps, layout)
+
+
+def test_tree_rows_equal_sequential_decode(gpu):
+    """Each draft node's row equals decoding its root-to-node path after the prefix."""
+    rng = np.random.default_rng(21)
+    B, P, N, Hq, Hkv, d = 2, 300, 9, 4, 2, 128
+    parents = [configs.draft_tree(rng, N) for _ in range(B)]
+    q = bf16(rng, (B, N, Hq, d))
+    k = bf16(rng, (B, Hkv, P + N, d))
+    v = bf16(rng, (B, Hkv, P + N, d))
+    mask = np.array([[sum(1 << a for a in configs.path_of(parents[b], i)) for i in range(N)] for b in range(B)],
+                    dtype=np.uint64)
+    tree = problem.contiguous(q, k, v, np.full((B, N), P), tree_mask=mask, tree_base=np.full(B, P))
+    ab = default_alpha_bits(d)
+    got, flags, _ = _run(tree, ab, splits=3)
+    assert not np.any(flags)
+    for b in range(B):
+        for i in range(N):
+            path = configs.path_of(parents[b], i)
+            idx = np.concatenate([np.arange(P), P + np.array(path)])
+            seq = problem.contiguous(q[b:b + 1, i:i + 1], k[b:b + 1][:, :, idx], v[b:b + 1][:, :, idx],
+                                     np.array([[len(idx)]]))
+            s_out, s_fl, _ = _run(seq, ab, splits=2)
+            assert not np.any(s_fl)
+            assert np.array_equal(got[b, i], s_out[0, 0]), (b, i)
+
+
+def test_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
+    rng = np.random.default_rng(4)
+    prob = _rand_problem(rng, "normal", "normal", B=1, T=8, Hq=2, Hkv=1, S=64, d=64, dv=64)
+    prob["seq_len"][:] = 64
+    prob["kv_len"][:] = 57 + np.arange(8)
+    prob["k"][0, 0, 60, 3] = 0x7FC0   # NaN key at position 60
+    prob["v"][0, 0, 62, 1] = 0x7F80   # inf value at position 62
+    ab = default_alpha_bits(64)
+    got, flags, _ = _run(prob, ab)
+    kvl = prob["kv_len"]
+    for t in range(8):
+        for h in range(2):
+            r = t * 2 + h
+            assert flags[r] == (2 if kvl[t] > 60 else 0), (t, h, flags)
+
+
+def test_fixture_sha256(gpu):
+    """The reference's published SHA-256 of all 2x2048 causal rows of two real Qwen3-0.6B heads
+    (fixtures/expected_sha256.json), computed by the HIP path."""
+    z = np.load(os.path.join(GOLD, "qwen3_0.6b_heads.npz"))
+    exp = json.load(open(os.path.join(GOLD, "expected_sha256.json")))
+    for key, info in exp["heads"].items():
+        q, k, v = z[f"q_{key}"], z[f"k_{key}"], z[f"v_{key}"]
+        ab = int(np.asarray(z[f"alpha_{key}"], dtype=np.float32).view(np.uint32))
+        L = q.shape[0]
+        prob = problem.contiguous(q.reshape(1, L, 1, -1), k.reshape(1, 1, L, -1), v.reshape(1, 1, L, -1),
+                                  (np.arange(L) + 1).reshape(1, L))
+        got, flags, st = _run(prob, ab, splits=8)
+        assert not np.any(flags), st
+        assert hashlib.sha256(got.reshape(L, -1).tobytes()).hexdigest() == info["sha256"], key
