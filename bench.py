@@ -1,0 +1,191 @@
+#!/usr/bin/env python
+"""Benchmark of the certified split-KV attention path on one MI355X.
+
+Workload: BASELINE config C2 (batched paged decode: B=32, 16 query / 8 KV heads, d=128, 4096 keys
+per sequence, NHD pages of 16, one query token per sequence), inputs resident in HBM. One step =
+one ea_hip_attention call (q prep, tier-1 split kernel, combine with certified rounding, tier 2).
+
+Prints one JSON line: whole-step decode throughput in GB/s over the algorithmic bytes (bf16 K+V,
+q, out, block table), the split kernel's roofline fraction timed with HIP events on the launch
+stream, bit-exactness against the committed golden hash, the tier-1 fallback-row rate, and the
+reference's own C++ certified CPU kernel (oracle/_ref, built from the reference source) timed on
+this host's cores as the CPU baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode KV GB/s & prefill int8-MFMA TOPS (% roofline), bit-exact, fallback-row %"
+HBM_PEAK_GBS = 8000.0
+GOLDEN = os.path.join(ROOT, "tests", "golden", "baseline_sha256.json")
+TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def algorithmic_bytes(prob: dict) -> int:
+    """bf16 K+V of every visible key, q, out and the block table (per step)."""
+    g = prob["geom"]
+    B, Hkv, d, dv, Hq, T = (g[x] for x in ("num_seqs", "num_kv_heads", "head_dim", "head_dim_v", "num_q_heads",
+                                          "num_tokens"))
+    keys = int(prob["seq_len"].astype(np.int64).sum())
+    kv = keys * Hkv * (d + dv) * 2
+    q = B * T * Hq * d * 2
+    out = B * T * Hq * dv * 2
+    bt = 0 if prob.get("block_table") is None else int(prob["block_table"].size) * 4
+    return kv + q + out + bt
+
+
+class HipEvents:
+    """Raw hipEvent_t handles (libamdhip64) so the library can record them on its launch stream."""
+
+    def __init__(self, n: int):
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.ev = (ctypes.c_void_p * n)()
+        for i in range(n):
+            e = ctypes.c_void_p()
+            assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+            self.ev[i] = e
+        self.n = n
+
+    def slot(self, i: int):
+        return ctypes.cast(ctypes.byref(self.ev, i * ctypes.sizeof(ctypes.c_void_p)), ctypes.c_void_p)
+
+    def ms(self, a: int, b: int) -> float:
+        assert self.h.hipEventSynchronize(self.ev[b]) == 0
+        t = ctypes.c_float(0)
+        assert self.h.hipEventElapsedTime(ctypes.byref(t), self.ev[a], self.ev[b]) == 0
+        return float(t.value)
+
+    def close(self):
+        for i in range(self.n):
+            self.h.hipEventDestroy(self.ev[i])
+
+
+def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
+    """The reference's certified CPU kernel (oracle/_ref, compiled from its csrc) on the full
+    C2 workload in its CSR form; the oracle's C restatement when that build is absent."""
+    from oracle import oracle
+    g = prob["geom"]
+    B, Hkv, Hq, d, dv = g["num_seqs"], g["num_kv_heads"], g["num_q_heads"], g["head_dim"], g["head_dim_v"]
+    P = g["page_size"]
+    S = int(prob["seq_len"].max())
+    n = np.arange(S)
+    pages = prob["block_table"][:, n // P]                   # (B, S)
+    K = prob["k"][pages, (n % P)[None, :]]                  # (B, S, Hkv, d)
+    V = prob["v"][pages, (n % P)[None, :]]
+    Kf = np.ascontiguousarray(K.transpose(0, 2, 1, 3).reshape(-1, d))
+    Vf = np.ascontiguousarray(V.transpose(0, 2, 1, 3).reshape(-1, dv))
+    q = prob["q"].reshape(B * Hq, d)
+    grp = Hq // Hkv
+    seg = (np.arange(B)[:, None] * Hkv + np.arange(Hq)[None, :] // grp).reshape(-1)
+    L = prob["seq_len"].repeat(Hq).astype(np.int64)
+    row_ptr = np.concatenate([[0], np.cumsum(L)]).astype(np.int64)
+    key_idx = np.concatenate([s * S + np.arange(l) for s, l in zip(seg, L)]).astype(np.int64)
+    ref = oracle.ref_available()
+    kind = "reference" if ref else "port"
+    run = lambda: oracle.raw_csr(q, Kf, Vf, alpha_bits, row_ptr, key_idx, "bf16", 64, 64, 8, 0, threads,
+                                 reference=ref)
+    run()  # warm-up
+    times = []
+    res = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        res, flags, _ = run()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    pairs = int(L.sum())
+    return {"value": round(algorithmic_bytes(prob) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"full C2 step ({pairs} query-key pairs, splits=8, 64-key tiles, int64), median of 3 "
+                      f"after 1 warm-up; {pairs / t / 1e6:.2f} M pairs/s; {int((flags != 0).sum())} rows flagged",
+            "wall_s": round(t, 3)}, res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by sequence x KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from exactattention_amd import configs
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+
+    t0 = time.time()
+    prob = configs.c2()
+    ab = configs.alpha_bits()
+    gen_s = time.time() - t0
+    dp = DeviceProblem(prob, "bf16", args.splits, "cuda:0")
+    nbytes = algorithmic_bytes(prob)
+    ev = HipEvents(5 * args.steps)
+    for _ in range(args.warmup):
+        launch_hip(dp, ab)
+    torch.cuda.synchronize()
+    out = dp.out.cpu().numpy().view(np.uint16)
+    golden = json.load(open(GOLDEN)).get("C2", {}).get("sha256") if os.path.exists(GOLDEN) else None
+    bit_exact = (hashlib.sha256(out.tobytes()).hexdigest() == golden) if golden else None
+    dp.stats.zero_()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        launch_hip(dp, ab, events=ctypes.cast(ev.slot(5 * i), ctypes.POINTER(ctypes.c_void_p)))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    phases = np.array([[ev.ms(5 * i + j, 5 * i + j + 1) for j in range(4)] for i in range(args.steps)])
+    ev.close()
+    split_ms = float(phases[:, 1].mean())
+    st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    flagged_pct = 100.0 * st["tier1_flagged"] / max(1, st["rows"])
+    traffic = None
+    if os.path.exists(TRAFFIC):
+        traffic = json.load(open(TRAFFIC)).get("ea_split_C2", {}).get("bytes_per_launch")
+    achieved = nbytes / (split_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(nbytes / (ms_step * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f64", "data": "synthetic",
+        "config": {"workload": "C2 batched paged decode", "batch": 32, "q_heads": 16, "kv_heads": 8,
+                   "head_dim": 128, "kv_len": 4096, "page_size": 16, "layout": "NHD", "nsplit": dp.nsplit,
+                   "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "ea_split",
+                     "kernel_ms": round(split_ms, 5)},
+        "kernels_ms": {k: round(float(phases[:, j].mean()), 5) for j, k in enumerate(("prep", "split", "combine",
+                                                                                      "tier2"))},
+        "bit_exact": bit_exact, "fallback_rows_pct": round(flagged_pct, 4),
+        "tier2_certified_rows": st["tier2_certified"], "uncertified_rows": st["uncertified"],
+        "tier1_causes": {k: st[k] for k in ("uncertified_scores", "undecided_weights", "uncertified_final", "slow_path_scores")},
+        "input_gen_s": round(gen_s, 1),
+    }
+    if not args.no_cpu:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        cb, cres = cpu_baseline(prob, ab, threads)
+        line["cpu_baseline"] = cb
+        line["cpu_bits_equal"] = bool(np.array_equal(cres.reshape(out.shape), out)) if cres is not None else None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

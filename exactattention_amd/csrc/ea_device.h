@@ -70,6 +70,69 @@ __device__ __forceinline__ int logit_rn32(double alpha, double s, uint32_t* t_bi
     return 0;
 }
 
+// Error-free sum: a + b = s + e exactly (Knuth's TwoSum; any fp64 a, b without overflow).
+__device__ __forceinline__ double two_sum(double a, double b, double* e) {
+    double s = a + b;
+    double bb = s - a;
+    *e = (a - (s - bb)) + (b - bb);
+    return s;
+}
+
+// t = RN32(alpha * x) for a real x known to lie in [s + sig - del, s + sig + del] (fp64 s, sig,
+// del >= 0; sig a small correction, |sig| <= 2^-52 |s| or so). Returns 0 and the fp32 bits of t
+// when every point of that interval rounds to the same fp32 value, 1 when that value is below
+// 2^-25 in magnitude (so w = RN24(2^t) = 1 exactly), 2 when the whole interval overflows fp32
+// (a domain error), 3 when undecided.
+// alpha*x = p + c with p = RN(alpha s), pe = alpha s - p exact (FMA), c = RN(alpha sig + pe):
+// the uncertainty is |c| u + alpha del (+ tiny). RN32 is constant on the open interval between
+// the midpoints around t0 = RN32(p); the midpoints are exact in fp64 and p - m is exact there.
+__device__ __forceinline__ int logit_cert(double alpha, double s, double sig, double del, uint32_t* t_bits) {
+    double p = alpha * s;
+    double pe = __fma_rn(alpha, s, -p);
+    double c = __fma_rn(alpha, sig, pe);
+    double eps = fabs(c) * 0x1p-52 + fabs(alpha) * del * (1.0 + 0x1p-50) + 0x1p-1070;
+    double ap = fabs(p);
+    if (ap + fabs(c) + eps <= 0x1p-25) {
+        *t_bits = 0;
+        return 1;
+    }
+    if (!(ap < 0x1p129)) return (ap >= 0x1p129 && isfinite(p)) ? 2 : 3;
+    float t0 = (float)p;  // RN-even
+    uint32_t b0 = __float_as_uint(t0);
+    if ((b0 & 0x7F800000u) == 0x7F800000u) {
+        // |p| rounds past the largest finite: certain overflow unless x could lie below the
+        // overflow threshold 2^128 - 2^103
+        double thr = 0x1.ffffffp127;
+        if (ap - fabs(c) - eps > thr) return 2;
+        return 3;
+    }
+    if (pe == 0.0 && sig == 0.0 && del == 0.0) {  // x = p exactly: RN-even of p (ties included)
+        *t_bits = b0;
+        return 0;
+    }
+    // neighbours toward +inf and -inf
+    uint32_t mag = b0 & 0x7FFFFFFFu, sg = b0 & 0x80000000u;
+    uint32_t up_b = (t0 >= 0.0f) ? ((mag + 1) | sg) : (mag == 0 ? 0x00000001u : ((mag - 1) | sg));
+    uint32_t dn_b = (t0 > 0.0f) ? ((mag - 1) | sg) : ((mag + 1) | 0x80000000u);
+    if (mag == 0) {
+        up_b = 0x00000001u;
+        dn_b = 0x80000001u;
+    }
+    double d0 = (double)t0;
+    double m_hi = 0.5 * (d0 + (double)__uint_as_float(up_b));
+    double m_lo = 0.5 * (d0 + (double)__uint_as_float(dn_b));
+    if (!isfinite(m_hi)) m_hi = 0x1.ffffffp127;  // above the largest finite: the overflow threshold
+    if (!isfinite(m_lo)) m_lo = -0x1.ffffffp127;
+    double dl = (p - m_lo) + c;  // p - m_lo exact; one rounding
+    double dh = (m_hi - p) - c;
+    double need = eps + 0x1p-51 * (fabs(dl) + fabs(dh));
+    if (dl > need && dh > need) {
+        *t_bits = b0;
+        return 0;
+    }
+    return 3;
+}
+
 // ----------------------------------------------------------------------------------------------
 // w = RN24(2^t) = M * 2^E, M in [2^23, 2^24). fp64 path. Returns 0 certified, 1 undecided
 // (|Y - round| too close to a half), 2 out of range (|t| >= 2^30).

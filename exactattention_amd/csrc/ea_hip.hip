@@ -57,8 +57,8 @@ struct Params {
     int32_t dlog;
     int64_t rows;
     // workspace
-    double* q64;      // rows * d
-    int32_t* qinfo;   // rows: (FQmax << 16) | FQmin' ; bit 31 = all zero
+    double* q64;      // rows * EA_MAXD
+    int32_t* qinfo;   // rows * 5: per 32-dim block (FQmax << 16) | FQmin', then a NaN/inf flag
     int32_t* pR;      // nsplit * rows
     int32_t* pn;      // nsplit * rows (visible keys, or -1 for a tier-1 flag)
     double* pZ;       // nsplit * rows
@@ -130,9 +130,10 @@ __device__ __forceinline__ int wave_sum_i(int x) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Kernel 1: q rows to fp64 and their exponent ranges. One wave per row.
-// qinfo = (FQmax << 16) | FQmin' with FQmin' = max(min nonzero exponent field, 1); 0x80000000 when
-// the row is all zeros; 0x40000000 when it holds a NaN/inf.
+// Kernel 1: q rows to fp64 plus per-32-dim-block exponent ranges. One wave per row.
+// qinfo[row*5 + blk] = (FQmax << 16) | FQmin' over the nonzero elements of dims [32 blk, 32 blk+32)
+// (FQmin' = max(field, 1): a subnormal's lsb is that of field 1), 0x80000000 for an all-zero block;
+// qinfo[row*5 + 4] = 1 when the row holds a NaN/inf.
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) ea_prep(Params P) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *P.wl_cnt = 0;
@@ -143,49 +144,62 @@ __global__ void __launch_bounds__(256) ea_prep(Params P) {
     int64_t b = row / ((int64_t)T * Hq);
     int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
     const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
-    int fmax = 0, fmin = 0x1FF, bad = 0;
-    for (int i = lane; i < d; i += 64) {
-        uint32_t x = qr[i];
-        P.q64[row * d + i] = (double)__uint_as_float(x << 16);
-        int f = (x >> 7) & 0xFF;
-        if (f == 0xFF) bad = 1;
-        if (x & 0x7FFF) {
-            fmax = max(fmax, f);
-            fmin = min(fmin, max(f, 1));
+    int bad = 0;
+    for (int blk = 0; blk < 4; ++blk) {
+        int i = blk * 32 + (lane & 31);
+        int fmax = 0, fmin = 0x1FF;
+        if (lane < 32 && i < d) {
+            uint32_t x = qr[i];
+            P.q64[row * EA_MAXD + i] = (double)__uint_as_float(x << 16);
+            int f = (x >> 7) & 0xFF;
+            if (f == 0xFF) bad = 1;
+            if (x & 0x7FFF) {
+                fmax = f;
+                fmin = max(f, 1);
+            }
+        } else if (lane < 32 && i < EA_MAXD) {
+            P.q64[row * EA_MAXD + i] = 0.0;
         }
+        fmax = wave_max_i(fmax);
+        fmin = wave_min_i(fmin);
+        if (lane == 0) P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
     }
-    fmax = wave_max_i(fmax);
-    fmin = wave_min_i(fmin);
     bad = wave_max_i(bad);
-    if (lane == 0) {
-        int32_t info = (fmax << 16) | (fmin & 0xFFFF);
-        if (fmin == 0x1FF) info = (int32_t)0x80000000;
-        if (bad) info = 0x40000000;
-        P.qinfo[row] = info;
-    }
+    if (lane == 0) P.qinfo[row * 5 + 4] = bad;
 }
 
 // ------------------------------------------------------------------------------------------------
-// Kernel 2: tier-1 split kernel.
-// Block = 4 waves over one (segment, row block, split). Per 64-key tile:
-//   S: thread (w, l) forms 32-dim partial dots of key l with every row (fp64 FMA chains),
-//      and the key's exponent range over those dims (packed 16-bit max/min on magnitudes);
-//   B: wave r finishes row r: exactness check, t, w = M 2^E, tile max, running rescale;
-//   P: thread (w, l) accumulates channels 2l, 2l+1 over keys 16w..16w+15 for every row.
-// K tiles sit in LDS with an XOR swizzle of their 16-byte chunks (conflict-free per-key reads);
-// the next tile's K and V are loaded into registers while the current one is processed.
+// Kernel 2: tier-1 split kernel, templated on the rows per block (1, 2 or 4).
+// Block = 4 waves over one (segment, row block, KV split); 64-key tiles. Per tile:
+//   load  thread t fetches 64 contiguous bytes of K and of V of key t/4 (one page lookup), into
+//         registers one tile ahead; they land in LDS (K with an XOR swizzle of its 16-byte
+//         chunks so per-key reads are conflict-free, V row-major);
+//   S     wave w, lane = key: fp64 FMA chains over dims [32w, 32w+32) for each row, q read
+//         through the constant address space (scalar loads, SGPR operands). The block's sum is
+//         exact when the exponent ranges of q and k over those dims satisfy
+//         (FQmax-FQmin') + (FKmax-FKmin') <= 32: every partial sum is then a multiple of the
+//         smallest product lsb and below 2^53 of it. Failing pairs are recomputed in B.
+//   B     wave r finishes row r: the 4 exact block sums are added with TwoSum (error-free), so
+//         s lies in [S + sig - 3u E, S + sig + 3u E] (E = sum of the TwoSum errors, 0 when the
+//         fp64 sum is exact); certified t = RN32(alpha s); w = RN24(2^t) (fp64 tables, 128-bit
+//         enclosure when undecided); running reference exponent and exact power-of-two rescale.
+//   P     wave w: channels 2l, 2l+1 over keys 16w..16w+15, FMA-fused exact products w*v.
 // ------------------------------------------------------------------------------------------------
 struct SplitSmem {
-    uint4 K[2][EA_TILE * (EA_MAXD / 8)];          // 32 KB
-    uint32_t V[2][EA_TILE * (EA_MAXDV / 2)];      // 32 KB
-    double T1[256], T2[256];                      // 4 KB
-    double sc[4][EA_MAXRB][EA_TILE];              // 8 KB partial scores
-    uint32_t kmx[4][EA_TILE], kmn[4][EA_TILE];    // 2 KB packed magnitude max / min-1
-    double w[EA_MAXRB][EA_TILE];                  // 2 KB weights of the tile
+    uint4 K[EA_TILE * 16];               // 16 KB, swizzled chunks
+    uint4 V[EA_TILE * 16];               // 16 KB, row-major
+    double T1[256], T2[256];             // 4 KB
+    double sc[4][EA_MAXRB][EA_TILE];     // 8 KB block sums
+    uint32_t fm[4][EA_TILE];             // 1 KB: bit r = block sum of row r not certified exact
+    uint32_t kmx[4][EA_TILE];            // 1 KB: packed max magnitude of the block (for the slow path)
+    double w[EA_MAXRB][EA_TILE];         // 2 KB weights of the tile
     double scale[EA_MAXRB];
-    int32_t rowflag[EA_MAXRB];
 };
 
+typedef const double __attribute__((address_space(4))) cdouble_t;
+typedef const int32_t __attribute__((address_space(4))) cint_t;
+
+template <int RB>
 __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     SplitSmem& S = *reinterpret_cast<SplitSmem*>(smem_raw);
@@ -193,8 +207,9 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int d = P.g.head_dim, dv = P.g.head_dim_v;
-    const int nchunk = d >> 3;     // 16-byte chunks per key row
-    const int ndw = dv >> 1;       // dwords per value row
+    const int nchunk = d >> 3;   // 16-byte chunks per key row
+    const int nvch = dv >> 3;    // 16-byte chunks per value row
+    const int ndw = dv >> 1;
 
     const int item = blockIdx.x;
     const int seg = item / P.nrb, rbk = item % P.nrb;
@@ -203,23 +218,21 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
     const int64_t b = seg / Hkv;
     const int hk = seg % Hkv;
     const int row0 = rbk * P.rb;
-    const int nrow = min(P.rb, P.r_seg - row0);
+    const int nrow = min(RB, P.r_seg - row0);
 
     for (int i = tid; i < 256; i += EA_THREADS) {
         S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
         S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
     }
-    // rows of this block
-    int64_t grow[EA_MAXRB], gtok[EA_MAXRB];
+    // rows of the block (a short block repeats its last row; repeats are never written)
+    int64_t grow[RB];
     int64_t kend = 0;
 #pragma unroll
-    for (int r = 0; r < EA_MAXRB; ++r) {
+    for (int r = 0; r < RB; ++r) {
         int lr = row0 + min(r, nrow - 1);
         int t = lr / P.grp, gi = lr % P.grp;
-        int hq = hk * P.grp + gi;
-        grow[r] = row_index(P, b, t, hq);
-        gtok[r] = b * P.g.num_tokens + t;
-        if (r < nrow) kend = max(kend, vis_end(P, gtok[r], b));
+        grow[r] = row_index(P, b, t, hk * P.grp + gi);
+        kend = max(kend, vis_end(P, b * P.g.num_tokens + t, b));
     }
     int64_t my_grow = 0, my_gtok = 0;
     if (w < nrow) {
@@ -228,121 +241,125 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
         my_grow = row_index(P, b, t, hk * P.grp + gi);
         my_gtok = b * P.g.num_tokens + t;
     }
-    int64_t slen = P.seq_len[b];
+    const int64_t slen = P.seq_len[b];
     if (kend > slen) kend = slen;
     const int64_t k0 = (int64_t)split * P.split_len;
     const int64_t k1 = min(k0 + (int64_t)P.split_len, kend);
     const int64_t pbase = (int64_t)split * P.rows;
 
-    // per-row state (meaningful in wave r for row r)
+    // exponent ranges of this wave's q block for each row (scalar loads)
+    cint_t* qinfo4 = (cint_t*)P.qinfo;
+    int qspread[RB];
+    bool qzero[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        int32_t qi = qinfo4[grow[r] * 5 + w];
+        qzero[r] = (qi == (int32_t)0x80000000);
+        qspread[r] = ((qi >> 16) & 0x1FF) - (qi & 0xFFFF);
+    }
+    int rflag = 0;
+    if (w < nrow && qinfo4[my_grow * 5 + 4]) rflag = 1;
     int Rrun = INT_MIN;
     double zacc = 0.0;
     int nvis = 0;
-    int rflag = 0;
-    int fqmax = 0, fqmin = 0;
-    bool qzero = false;
-    if (w < nrow) {
-        int32_t qi = P.qinfo[my_grow];
-        if (qi == 0x40000000) rflag = 1;
-        qzero = (qi == (int32_t)0x80000000);
-        fqmax = (qi >> 16) & 0x1FF;
-        fqmin = qi & 0xFFFF;
-    }
-    const int spread_lim = 37 - P.dlog;  // exactness: (FQmax-FQmin') + (FKmax-FKmin') <= 37 - ceil(log2 d)
 
-    double acc[EA_MAXRB][2];
-    for (int r = 0; r < EA_MAXRB; ++r) acc[r][0] = acc[r][1] = 0.0;
-    uint32_t vmx = 0;  // packed max |v| magnitude bits for channels 2l, 2l+1
+    double acc[RB][2];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r][0] = acc[r][1] = 0.0;
+    uint32_t vmx = 0;  // packed max |v| magnitude bits, channels 2*lane, 2*lane+1
 
-    // register staging of the next tile: 4 K chunks + (up to) 4 V dword-pairs per thread
-    uint4 kst[4];
-    uint32_t vst[EA_TILE * (EA_MAXDV / 2) / EA_THREADS];  // 16 dwords
+    // loader role: key kt = tid/4, 64-byte quarter qq = tid%4 (chunks 4j + qq, j = 0..3)
+    const int kt = tid >> 2, qq = tid & 3;
+    uint4 kst[4], vst[4];
     auto load_tile = [&](int64_t n0) {
-        // K: chunk index x = i*256 + tid -> key x/16, LDS chunk slot x%16 holds global chunk
-        // (x%16) ^ (key%16)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int x = i * EA_THREADS + tid;
-            int key = x >> 4, cs = x & 15;
-            int c = cs ^ (key & 15);
-            int64_t n = n0 + key;
-            uint4 val = make_uint4(0, 0, 0, 0);
-            if (c < nchunk && n < k1) {
-                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-                const u32x4* src = reinterpret_cast<const u32x4*>(P.k + kv_off(P, b, n, hk, 0)) + c;
-                u32x4 t4 = __builtin_nontemporal_load(src);
-                val = make_uint4(t4.x, t4.y, t4.z, t4.w);
-            }
-            kst[i] = val;
+        int64_t n = n0 + kt;
+        bool ok = n < k1;
+        int64_t page = b, slot = n;
+        if (ok && P.bt) {
+            int64_t off = P.bt_off ? P.bt_off[b] : b * (int64_t)P.g.block_table_stride;
+            page = P.bt[off + (n >> P.pshift)];
+            slot = n & ((1 << P.pshift) - 1);
         }
-        // V: dword index x = i*256 + tid -> key x/64, dword x%64
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4* kp = reinterpret_cast<const u32x4*>(P.k + page * P.g.k_page_stride + slot * P.g.k_slot_stride +
+                                                         (int64_t)hk * P.g.k_head_stride);
+        const u32x4* vp = reinterpret_cast<const u32x4*>(P.v + page * P.g.v_page_stride + slot * P.g.v_slot_stride +
+                                                         (int64_t)hk * P.g.v_head_stride);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            int x = i * EA_THREADS + tid;
-            int key = x >> 6, dw = x & 63;
-            int64_t n = n0 + key;
-            uint32_t val = 0;
-            if (dw < ndw && n < k1) {
-                const uint32_t* src = reinterpret_cast<const uint32_t*>(P.v + kv_off(P, b, n, hk, 1)) + dw;
-                val = __builtin_nontemporal_load(src);
-            }
-            vst[i] = val;
+        for (int j = 0; j < 4; ++j) {
+            int c = 4 * j + qq;
+            u32x4 a = {0, 0, 0, 0}, v4 = {0, 0, 0, 0};
+            if (ok && c < nchunk) a = __builtin_nontemporal_load(kp + c);
+            if (ok && c < nvch) v4 = __builtin_nontemporal_load(vp + c);
+            kst[j] = make_uint4(a.x, a.y, a.z, a.w);
+            vst[j] = make_uint4(v4.x, v4.y, v4.z, v4.w);
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S.K[buf][i * EA_THREADS + tid] = kst[i];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) S.V[buf][i * EA_THREADS + tid] = vst[i];
+        for (int j = 0; j < 4; ++j) {
+            int c = 4 * j + qq;
+            S.K[kt * 16 + (c ^ (kt & 15))] = kst[j];
+            S.V[kt * 16 + c] = vst[j];
+        }
     };
 
-    int ntiles = (k1 > k0) ? (int)((k1 - k0 + EA_TILE - 1) / EA_TILE) : 0;
-    if (ntiles > 0) {
-        load_tile(k0);
-        store_tile(0);
-    }
-    __syncthreads();
+    if (tid < RB) S.scale[tid] = 1.0;  // rows past nrow never rescale
+    const int ntiles = (k1 > k0) ? (int)((k1 - k0 + EA_TILE - 1) / EA_TILE) : 0;
+    if (ntiles > 0) load_tile(k0);
+    cdouble_t* q4 = (cdouble_t*)P.q64;
+    const int spread_lim = 32;
 
-    const double* q64 = P.q64;
     for (int it = 0; it < ntiles; ++it) {
-        const int buf = it & 1;
         const int64_t n0 = k0 + (int64_t)it * EA_TILE;
+        __syncthreads();  // previous tile's readers are done with S.K / S.V
+        store_tile();
         if (it + 1 < ntiles) load_tile(n0 + EA_TILE);
+        __syncthreads();
 
-        // ---- S: partial dots over dims [32w, 32w+32) of key `lane`
+        // ---- S: dims [32w, 32w+32) of key `lane`, every row
         {
-            double sacc[EA_MAXRB];
+            uint32_t kd[16];
 #pragma unroll
-            for (int r = 0; r < EA_MAXRB; ++r) sacc[r] = 0.0;
-            typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-            us2 mx = {0, 0}, mn = {0xFFFF, 0xFFFF};
             for (int cc = 0; cc < 4; ++cc) {
                 int c = 4 * w + cc;
-                if (c >= nchunk) break;
-                uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
-                uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t m2 = wd[j] & 0x7FFF7FFFu;
-                    us2 mv = __builtin_bit_cast(us2, m2);
-                    mx = __builtin_elementwise_max(mx, mv);
-                    mn = __builtin_elementwise_min(mn, mv - (us2){1, 1});
-                    double k_lo = bf16lo_f64(wd[j]), k_hi = bf16hi_f64(wd[j]);
-                    int dim = c * 8 + 2 * j;
-#pragma unroll
-                    for (int r = 0; r < EA_MAXRB; ++r) {
-                        if (r < nrow) {
-                            const double* qr = q64 + grow[r] * d + dim;
-                            sacc[r] = __fma_rn(qr[0], k_lo, sacc[r]);
-                            sacc[r] = __fma_rn(qr[1], k_hi, sacc[r]);
-                        }
-                    }
-                }
+                uint4 kv = (c < nchunk) ? S.K[lane * 16 + (c ^ (lane & 15))] : make_uint4(0, 0, 0, 0);
+                kd[4 * cc] = kv.x;
+                kd[4 * cc + 1] = kv.y;
+                kd[4 * cc + 2] = kv.z;
+                kd[4 * cc + 3] = kv.w;
             }
+            typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+            us2 mx = {0, 0}, mn = {0xFFFF, 0xFFFF};
+            double kf[32];
 #pragma unroll
-            for (int r = 0; r < EA_MAXRB; ++r) S.sc[w][r][lane] = sacc[r];
-            S.kmx[w][lane] = __builtin_bit_cast(uint32_t, mx);
-            S.kmn[w][lane] = __builtin_bit_cast(uint32_t, mn);
+            for (int j = 0; j < 16; ++j) {
+                us2 mv = __builtin_bit_cast(us2, kd[j] & 0x7FFF7FFFu);
+                mx = __builtin_elementwise_max(mx, mv);
+                mn = __builtin_elementwise_min(mn, mv - (us2){1, 1});
+                kf[2 * j] = bf16lo_f64(kd[j]);
+                kf[2 * j + 1] = bf16hi_f64(kd[j]);
+            }
+            uint32_t magmax = max((uint32_t)mx.x, (uint32_t)mx.y);
+            uint32_t magmin1 = min((uint32_t)mn.x, (uint32_t)mn.y);
+            bool kzero = (magmax == 0);
+            int kspread = (int)(magmax >> 7) - max((int)((magmin1 + 1) >> 7), 1);
+            uint32_t fmask = 0;
+            const int dbase = 32 * w;
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                cdouble_t* qr = q4 + grow[r] * EA_MAXD + dbase;
+                double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) {
+                    a0 = __fma_rn(qr[i], kf[i], a0);
+                    a1 = __fma_rn(qr[i + 1], kf[i + 1], a1);
+                }
+                S.sc[w][r][lane] = a0 + a1;
+                bool exact = qzero[r] || kzero || (qspread[r] + kspread <= spread_lim);
+                if (!exact) fmask |= 1u << r;
+            }
+            S.fm[w][lane] = fmask;
         }
         __syncthreads();
 
@@ -350,41 +367,68 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
         if (w < nrow) {
             const int r = w;
             const int64_t n = n0 + lane;
-            bool vis = (n < k1) && visible(P, my_gtok, b, n);
-            double s = 0.0;
-            for (int ww = 0; ww < 4; ++ww) s += S.sc[ww][r][lane];
-            uint32_t kmxa = 0, kmna = 0xFFFFFFFFu;
-            for (int ww = 0; ww < 4; ++ww) {
-                uint32_t a = S.kmx[ww][lane], c2 = S.kmn[ww][lane];
-                kmxa = max(kmxa & 0xFFFF, a & 0xFFFF) | (max(kmxa >> 16, a >> 16) << 16);
-                kmna = min(kmna & 0xFFFF, c2 & 0xFFFF) | (min(kmna >> 16, c2 >> 16) << 16);
-            }
-            uint32_t magmax = max(kmxa & 0xFFFF, kmxa >> 16);
-            uint32_t magmin1 = min(kmna & 0xFFFF, kmna >> 16);  // (min nonzero magnitude) - 1, 0xFFFF if none
-            int32_t M = 1 << 23, E = -23;
-            bool kzero = (magmax == 0);
-            if (vis && !rflag) {
-                bool exact = qzero || kzero;
-                if (!exact) {
-                    int fkmax = (int)(magmax >> 7);
-                    int fkmin = max((int)((magmin1 + 1) >> 7), 1);
-                    exact = (fqmax - fqmin) + (fkmax - fkmin) <= spread_lim;
+            const bool vis = (n < k1) && visible(P, my_gtok, b, n);
+            double x0 = S.sc[0][r][lane], x1 = S.sc[1][r][lane], x2 = S.sc[2][r][lane], x3 = S.sc[3][r][lane];
+            bool slow = ((S.fm[0][lane] | S.fm[1][lane] | S.fm[2][lane] | S.fm[3][lane]) >> r) & 1;
+            double ssum, sig, del;
+            if (vis && slow) {
+                // every product separately, TwoSum-accumulated: exact up to the rounding of the
+                // error sum, bounded by 130 u E (E = sum of |TwoSum errors|)
+                cdouble_t* qr = q4 + my_grow * EA_MAXD;
+                double s = 0.0, es = 0.0, ea = 0.0;
+                for (int c = 0; c < nchunk; ++c) {
+                    uint4 kv = S.K[lane * 16 + (c ^ (lane & 15))];
+                    uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        double e0, e1;
+                        s = two_sum(s, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
+                        s = two_sum(s, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
+                        es += e0 + e1;
+                        ea += fabs(e0) + fabs(e1);
+                    }
                 }
-                if (!isfinite(s)) exact = false;
-                if (!exact) {
-                    rflag = 1;  // score not certified here: tier 2
-                } else {
-                    uint32_t tb = 0;
-                    int ls = (s == 0.0) ? 1 : logit_rn32(P.alpha, s, &tb);
-                    if (ls == 2) {
-                        rflag = 1;  // logit overflow: tier 2 confirms and reports the domain error
-                    } else if (ls == 0) {
-                        int ws = weight_f64(tb, S.T1, S.T2, &M, &E);
-                        if (ws) rflag = 1;
+                ssum = s;
+                sig = es;
+                del = ea * 0x1p-44;  // >= 2 u per accumulation of the error sum
+            } else {
+                double e1, e2, e3;
+                double s = two_sum(x0, x1, &e1);
+                s = two_sum(s, x2, &e2);
+                s = two_sum(s, x3, &e3);
+                ssum = s;
+                sig = (e1 + e2) + e3;
+                del = (fabs(e1) + fabs(e2) + fabs(e3)) * 0x1p-51;
+            }
+            int32_t M = 1 << 23, E = -23;
+            int why = 0;  // 1 score not certified, 2 weight not certified
+            if (vis && !rflag) {
+                uint32_t tb = 0;
+                int ls = (ssum == 0.0 && sig == 0.0 && del == 0.0) ? 1
+                         : (isfinite(ssum) ? logit_cert(P.alpha, ssum, sig, del, &tb) : 3);
+                if (ls == 2 || ls == 3) {
+                    why = 1;  // overflow (tier 2 reports the domain error) or undecided
+                } else if (ls == 0) {
+                    int ws = weight_f64(tb, S.T1, S.T2, &M, &E);
+                    if (ws) {
+                        int32_t M2 = 0;
+                        int64_t E2 = 0;
+                        if (weight_wide(tb, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
+                            M = M2;
+                            E = (int32_t)E2;
+                        } else {
+                            why = 2;
+                        }
                     }
                 }
             }
-            // any lane flagged -> the row is flagged
+            if (P.stats) {
+                uint64_t b1 = __ballot(why == 1), b2 = __ballot(why == 2), b3 = __ballot(vis && slow);
+                if (lane == 0 && b1) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)__popcll(b1));
+                if (lane == 0 && b2) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)__popcll(b2));
+                if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
+            }
+            if (why) rflag = 1;
             rflag = wave_max_i(rflag);
             int tmax = wave_max_i(vis ? E + 23 : INT_MIN);
             int Rnew = max(Rrun, tmax);
@@ -406,59 +450,52 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
             nvis += vis ? 1 : 0;
             Rrun = Rnew;
             S.w[r][lane] = om;
-            if (lane == 0) {
-                S.scale[r] = sc;
-                S.rowflag[r] = rflag;
-            }
+            if (lane == 0) S.scale[r] = sc;
         }
         __syncthreads();
 
         // ---- P: channels 2*lane, 2*lane+1 over keys 16w .. 16w+15
         if (lane < ndw) {
 #pragma unroll
-            for (int r = 0; r < EA_MAXRB; ++r) {
-                if (r < nrow) {
-                    double sc = S.scale[r];
-                    if (sc != 1.0) {
-                        acc[r][0] *= sc;
-                        acc[r][1] *= sc;
-                    }
+            for (int r = 0; r < RB; ++r) {
+                double sc = S.scale[r];
+                if (sc != 1.0) {
+                    acc[r][0] *= sc;
+                    acc[r][1] *= sc;
                 }
             }
             typedef unsigned short us2 __attribute__((ext_vector_type(2)));
             us2 vm = __builtin_bit_cast(us2, vmx);
+            const uint32_t* Vd = reinterpret_cast<const uint32_t*>(S.V);
+#pragma unroll 4
             for (int kk = 0; kk < 16; ++kk) {
                 int key = 16 * w + kk;
-                uint32_t vd = S.V[buf][key * 64 + lane];
+                uint32_t vd = Vd[key * 64 + lane];
                 vm = __builtin_elementwise_max(vm, __builtin_bit_cast(us2, vd & 0x7FFF7FFFu));
                 double v0 = bf16lo_f64(vd), v1 = bf16hi_f64(vd);
 #pragma unroll
-                for (int r = 0; r < EA_MAXRB; ++r) {
-                    if (r < nrow) {
-                        double om = S.w[r][key];
-                        acc[r][0] = __fma_rn(om, v0, acc[r][0]);
-                        acc[r][1] = __fma_rn(om, v1, acc[r][1]);
-                    }
+                for (int r = 0; r < RB; ++r) {
+                    double om = S.w[r][key];
+                    acc[r][0] = __fma_rn(om, v0, acc[r][0]);
+                    acc[r][1] = __fma_rn(om, v1, acc[r][1]);
                 }
             }
             vmx = __builtin_bit_cast(uint32_t, vm);
         }
-        if (it + 1 < ntiles) store_tile(buf ^ 1);
-        __syncthreads();
     }
+    __syncthreads();
 
     // ---- epilogue: reduce N over the 4 waves, write the split partial
-    double* red = reinterpret_cast<double*>(&S.K[0][0]);  // reuse: 4 * EA_MAXRB * 128 doubles = 16 KB
-    uint32_t* vred = reinterpret_cast<uint32_t*>(&S.V[0][0]);
+    double* red = reinterpret_cast<double*>(&S.K[0]);  // 4 * EA_MAXRB * 128 doubles = 16 KB
+    uint32_t* vred = reinterpret_cast<uint32_t*>(&S.V[0]);
     if (lane < ndw) {
 #pragma unroll
-        for (int r = 0; r < EA_MAXRB; ++r) {
+        for (int r = 0; r < RB; ++r) {
             red[((w * EA_MAXRB) + r) * 128 + 2 * lane] = acc[r][0];
             red[((w * EA_MAXRB) + r) * 128 + 2 * lane + 1] = acc[r][1];
         }
         vred[w * 64 + lane] = vmx;
     }
-    // row scalars
     if (w < nrow) {
         double z = wave_sum(zacc);
         int nv = wave_sum_i(nvis);
@@ -474,7 +511,9 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
         int r = x / dv, c = x % dv;
         double s = 0.0;
         for (int ww = 0; ww < 4; ++ww) s += red[((ww * EA_MAXRB) + r) * 128 + c];
-        P.pN[(pbase + grow[r]) * dv + c] = s;
+        int lr = row0 + r;
+        int t = lr / P.grp, gi = lr % P.grp;
+        P.pN[(pbase + row_index(P, b, t, hk * P.grp + gi)) * dv + c] = s;
     }
     for (int c = tid; c < dv; c += EA_THREADS) {
         uint32_t m = 0;
@@ -530,7 +569,7 @@ __global__ void __launch_bounds__(256) ea_combine(Params P) {
         if (n < 0) flag = 1;
         else if (n > 0) R = max(R, P.pR[o]);
     }
-    if (P.qinfo[row] == 0x40000000) flag = 1;
+    if (P.qinfo[row * 5 + 4]) flag = 1;
     uint16_t* o16 = (uint16_t*)P.out;
     uint32_t* o32 = (uint32_t*)P.out;
     int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
@@ -592,6 +631,7 @@ __global__ void __launch_bounds__(256) ea_combine(Params P) {
     int bad = wave_max_i(ok ? 0 : 1);
     if (lane == 0) {
         P.flags[row] = bad ? 1 : 0;
+        if (P.stats && bad && !flag) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
         if (bad) {
             int slot = atomicAdd(P.wl_cnt, 1);
             P.wl[slot] = (int32_t)row;
@@ -960,7 +1000,7 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     if (o->splits < 0) return -2;
     pl->grp = g->num_q_heads / g->num_kv_heads;
     pl->r_seg = g->num_tokens * pl->grp;
-    pl->rb = pl->r_seg < EA_MAXRB ? pl->r_seg : EA_MAXRB;
+    pl->rb = pl->r_seg >= 3 ? 4 : pl->r_seg;  // kernels exist for 1, 2 and 4 rows per block
     pl->nrb = (pl->r_seg + pl->rb - 1) / pl->rb;
     pl->nseg = g->num_seqs * g->num_kv_heads;
     pl->rows = (int64_t)g->num_seqs * g->num_tokens * g->num_q_heads;
@@ -987,8 +1027,8 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     int64_t R = pl->rows;
     int dv = g->head_dim_v, d = g->head_dim;
     size_t off = 0;
-    pl->off_q64 = off; off = align_up(off + (size_t)R * d * 8);
-    pl->off_qinfo = off; off = align_up(off + (size_t)R * 4);
+    pl->off_q64 = off; off = align_up(off + (size_t)R * EA_MAXD * 8);
+    pl->off_qinfo = off; off = align_up(off + (size_t)R * 5 * 4);
     pl->off_pR = off; off = align_up(off + (size_t)pl->nsplit * R * 4);
     pl->off_pn = off; off = align_up(off + (size_t)pl->nsplit * R * 4);
     pl->off_pZ = off; off = align_up(off + (size_t)pl->nsplit * R * 8);
@@ -1067,6 +1107,10 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.t2_keys = pl.t2_keys;
     hipStream_t st = (hipStream_t)stream;
     unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
+    auto mark = [&](int i) -> int {
+        return o->events ? herr(hipEventRecord((hipEvent_t)o->events[i], st)) : 0;
+    };
+    if ((rc = mark(0))) return rc;
     hipLaunchKernelGGL(ea_prep, dim3(rb4), dim3(256), 0, st, P);
     rc = herr(hipGetLastError());
     if (rc) return rc;
@@ -1074,25 +1118,36 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         static std::once_flag once;
         static hipError_t attr_err = hipSuccess;
         std::call_once(once, [] {
-            attr_err = hipFuncSetAttribute((const void*)ea_split, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)sizeof(SplitSmem));
+            const void* fns[3] = {(const void*)ea_split<1>, (const void*)ea_split<2>, (const void*)ea_split<4>};
+            for (const void* f : fns) {
+                hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)sizeof(SplitSmem));
+                if (e != hipSuccess) attr_err = e;
+            }
         });
         rc = herr(attr_err);
         if (rc) return rc;
         dim3 grid((unsigned)(pl.nseg * pl.nrb), (unsigned)pl.nsplit);
-        hipLaunchKernelGGL(ea_split, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
+        if ((rc = mark(1))) return rc;
+        if (pl.rb == 1) hipLaunchKernelGGL(ea_split<1>, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
+        else if (pl.rb == 2) hipLaunchKernelGGL(ea_split<2>, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
+        else hipLaunchKernelGGL(ea_split<4>, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
         rc = herr(hipGetLastError());
         if (rc) return rc;
+    } else if ((rc = mark(1))) {
+        return rc;
     }
+    if ((rc = mark(2))) return rc;
     hipLaunchKernelGGL(ea_combine, dim3(rb4), dim3(256), 0, st, P);
     rc = herr(hipGetLastError());
     if (rc) return rc;
+    if ((rc = mark(3))) return rc;
     if (o->tier2) {
         hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_THREADS), 0, st, P);
         rc = herr(hipGetLastError());
         if (rc) return rc;
     }
-    return 0;
+    return mark(4);
 }
 
 int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
@@ -1144,7 +1199,7 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
     EA_TRY(hipMalloc(&dout, (size_t)rows * dv * osz));
     EA_TRY(hipMalloc(&dfl, (size_t)rows));
     EA_TRY(hipMalloc(&dws, ws_bytes > 0 ? ws_bytes : 256));
-    EA_TRY(hipMalloc(&dst, 8 * sizeof(int64_t)));
+    EA_TRY(hipMalloc(&dst, 16 * sizeof(int64_t)));
     EA_TRY(hipMemcpy(dq, q, (size_t)rows * d * 2, hipMemcpyHostToDevice));
     if (nkeys > 0) {
         EA_TRY(hipMemcpy(dk, k, (size_t)nkeys * d * 2, hipMemcpyHostToDevice));
@@ -1153,7 +1208,7 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
     EA_TRY(hipMemcpy(dbt, bt.data(), bt.size() * 4, hipMemcpyHostToDevice));
     EA_TRY(hipMemcpy(dbo, bo.data(), (size_t)rows * 8, hipMemcpyHostToDevice));
     EA_TRY(hipMemcpy(dsl, sl.data(), (size_t)rows * 4, hipMemcpyHostToDevice));
-    EA_TRY(hipMemset(dst, 0, 8 * sizeof(int64_t)));
+    EA_TRY(hipMemset(dst, 0, 16 * sizeof(int64_t)));
     {
         ea_buffers b;
         memset(&b, 0, sizeof(b));
@@ -1169,7 +1224,7 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
     EA_TRY(hipMemcpy(out, dout, (size_t)rows * dv * osz, hipMemcpyDeviceToHost));
     EA_TRY(hipMemcpy(flags, dfl, (size_t)rows, hipMemcpyDeviceToHost));
     {
-        int64_t hs[8];
+        int64_t hs[16];
         EA_TRY(hipMemcpy(hs, dst, sizeof(hs), hipMemcpyDeviceToHost));
         if (stats) stats[2] += hs[1];
     }

@@ -25,8 +25,9 @@ def float_to_bf16_bits(x) -> np.ndarray:
     f = np.asarray(x, dtype=np.float32)
     if not np.all(np.isfinite(f)):
         raise ExactAttentionDomainError("non-finite value")
-    u = f.view(np.uint32).astype(np.uint64)
-    out = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    u = f.view(np.uint32)
+    # finite patterns are <= 0xFF7FFFFF, so adding at most 0x8000 cannot wrap 32 bits
+    out = ((u + (np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1)))) >> np.uint32(16)).astype(np.uint16)
     if np.any((out & 0x7F80) == 0x7F80):
         raise ExactAttentionDomainError("bf16 overflow when generating input")
     return out

@@ -40,11 +40,12 @@ class Buffers(ctypes.Structure):
 
 class Options(ctypes.Structure):
     _fields_ = [("alpha_bits", ctypes.c_uint32), ("out_fp32", ctypes.c_int32), ("splits", ctypes.c_int32),
-                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("reserved", ctypes.c_int32 * 4)]
+                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P),
+                ("reserved", ctypes.c_int32 * 2)]
 
 
 STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
-         "undecided_weights", "uncertified_final"]
+         "undecided_weights", "uncertified_final", "slow_path_scores"]
 
 
 def available() -> bool:
@@ -134,7 +135,7 @@ class DeviceProblem:
         nb, self.nsplit = workspace_size(self.geom, splits, self.out_fp32)
         self.workspace = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
         self.ws_bytes = nb
-        self.stats = torch.zeros(8, dtype=torch.int64, device=dev)
+        self.stats = torch.zeros(16, dtype=torch.int64, device=dev)
         self._geom_c = geometry(self.geom)
 
     def buffers(self) -> Buffers:
@@ -142,14 +143,16 @@ class DeviceProblem:
         return Buffers(**ptr, out=self.out.data_ptr(), flags=self.flags.data_ptr())
 
 
-def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True) -> None:
-    """Enqueue one step on torch's current stream (no sync, no host copies, no allocation)."""
+def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True, events=None) -> None:
+    """Enqueue one step on torch's current stream (no sync, no host copies, no allocation).
+    `events`: optional ctypes array of 5 hipEvent_t handles recorded between the kernels."""
     lib = load()
     mo = None
     if merge_order is not None:
         mo = merge_order if hasattr(merge_order, "data_ptr") else None
     o = Options(alpha_bits=alpha_bits, out_fp32=int(dp.out_fp32), splits=dp.splits, tier2=int(tier2),
-                merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr())
+                merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr(),
+                events=None if events is None else ctypes.cast(events, P))
     b = dp.buffers()
     _check(lib.ea_hip_attention(ctypes.byref(dp._geom_c), ctypes.byref(b), ctypes.byref(o), dp.workspace.data_ptr(),
                                 dp.ws_bytes, _stream_ptr(dp.torch)), "ea_hip_attention")

@@ -111,17 +111,20 @@ def to_paged(prob: dict, page_size: int, rng: np.random.Generator, layout: str =
     bt = perm[:B * npp].reshape(B, npp).astype(np.int32)
     shape_k = (n_pages, page_size, Hkv, d) if layout == "NHD" else (n_pages, Hkv, page_size, d)
     shape_v = (n_pages, page_size, Hkv, dv) if layout == "NHD" else (n_pages, Hkv, page_size, dv)
-    kp = rng.integers(0, 1 << 14, size=shape_k, dtype=np.uint16)  # finite junk in unused slots
-    vp = rng.integers(0, 1 << 14, size=shape_v, dtype=np.uint16)
-    for b in range(B):
-        for p in range(npp):
-            s0, s1 = p * page_size, min(S, (p + 1) * page_size)
-            if layout == "NHD":
-                kp[bt[b, p], :s1 - s0] = k[b, :, s0:s1].transpose(1, 0, 2)
-                vp[bt[b, p], :s1 - s0] = v[b, :, s0:s1].transpose(1, 0, 2)
-            else:
-                kp[bt[b, p], :, :s1 - s0] = k[b, :, s0:s1]
-                vp[bt[b, p], :, :s1 - s0] = v[b, :, s0:s1]
+    # unused slots and pages hold finite junk (bf16 1.5), which no row may read
+    kp = np.full(shape_k, 0x3FC0, dtype=np.uint16)
+    vp = np.full(shape_v, 0x3FC0, dtype=np.uint16)
+    pad = npp * page_size - S
+    kk = np.pad(k, ((0, 0), (0, 0), (0, pad), (0, 0)), constant_values=0x3FC0)
+    vv = np.pad(v, ((0, 0), (0, 0), (0, pad), (0, 0)), constant_values=0x3FC0)
+    kk = kk.reshape(B, Hkv, npp, page_size, d)
+    vv = vv.reshape(B, Hkv, npp, page_size, dv)
+    if layout == "NHD":
+        kp[bt.reshape(-1)] = kk.transpose(0, 2, 3, 1, 4).reshape(B * npp, page_size, Hkv, d)
+        vp[bt.reshape(-1)] = vv.transpose(0, 2, 3, 1, 4).reshape(B * npp, page_size, Hkv, dv)
+    else:
+        kp[bt.reshape(-1)] = kk.transpose(0, 2, 1, 3, 4).reshape(B * npp, Hkv, page_size, d)
+        vp[bt.reshape(-1)] = vv.transpose(0, 2, 1, 3, 4).reshape(B * npp, Hkv, page_size, dv)
     kv_len = prob["kv_len"].reshape(B, -1)
     return paged(prob["q"], kp, vp, bt, kv_len, prob["seq_len"], layout, prob["tree_mask"], prob["tree_base"])
 

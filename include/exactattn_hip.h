@@ -76,11 +76,15 @@ typedef struct ea_options {
     int32_t splits;         /* KV splits per segment; 0 = choose for the device */
     int32_t tier2;          /* 1 = run the device tier 2 on rows tier 1 leaves uncertified */
     const int32_t* merge_order; /* optional device permutation of [0, nsplit): combine order */
-    int64_t* stats;         /* optional device int64[8], accumulated (+=):
+    int64_t* stats;         /* optional device int64[16], accumulated (+=):
                                [0] rows, [1] rows flagged by tier 1, [2] rows certified by tier 2,
-                               [3] rows left flag 1, [4] rows flag 2, [5] uncertified scores,
-                               [6] undecided weights, [7] uncertified final roundings */
-    int32_t reserved[4];
+                               [3] rows left flag 1, [4] rows flag 2, [5] tier-1 scores not
+                               certified, [6] tier-1 weights not certified, [7] tier-1 final
+                               roundings not certified, [8] scores taken by the per-pair exact
+                               path, [9..15] reserved */
+    void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep, split,
+                               combine and tier 2, and after tier 2 (per-kernel timing) */
+    int32_t reserved[2];
 } ea_options;
 
 /* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
