@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 METRIC = "decode KV GB/s & prefill int8-MFMA TOPS (% roofline), bit-exact, fallback-row %"
 HBM_PEAK_GBS = 8000.0
 GOLDEN = os.path.join(ROOT, "tests", "golden", "baseline_sha256.json")
-TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+TRAFFIC = os.path.join(ROOT, "profiles", "ea_split_C2_traffic.md")
 
 
 def algorithmic_bytes(prob: dict) -> int:
@@ -122,7 +122,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--timers", action="store_true",
+                    help="after the timed steps, run 5 steps of the phase-clock build and report it")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run 5 device-to-device copies of BYTES (scales rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        src = torch.ones(args.copy_calibration // 2, dtype=torch.int16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": args.copy_calibration}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the path shards by sequence x KV head with no exchange; see DESIGN.md)", file=sys.stderr)
@@ -158,9 +171,11 @@ def main():
     split_ms = float(phases[:, 1].mean())
     st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
     flagged_pct = 100.0 * st["tier1_flagged"] / max(1, st["rows"])
-    traffic = None
+    traffic = None  # HBM bytes per split launch, from the committed rocprofv3 PMC summary
     if os.path.exists(TRAFFIC):
-        traffic = json.load(open(TRAFFIC)).get("ea_split_C2", {}).get("bytes_per_launch")
+        for ln in open(TRAFFIC):
+            if ln.startswith("traffic_bytes_per_launch:"):
+                traffic = int(ln.split(":")[1])
     achieved = nbytes / (split_ms * 1e-3) / 1e9
     line = {
         "metric": METRIC, "value": round(nbytes / (ms_step * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
@@ -179,6 +194,17 @@ def main():
         "tier1_causes": {k: st[k] for k in ("uncertified_scores", "undecided_weights", "uncertified_final", "slow_path_scores")},
         "input_gen_s": round(gen_s, 1),
     }
+    if args.timers:
+        from exactattention_amd.hip import TIMER_PHASES
+        tm = torch.zeros(16, dtype=torch.int64, device="cuda:0")
+        for _ in range(5):
+            launch_hip(dp, ab, timers=tm)
+        torch.cuda.synchronize()
+        tv = tm.cpu().numpy()[:8].astype(float)
+        tot = tv[:7].sum()
+        line["phase_clocks"] = {"cycles_per_wave_tile": {k: round(tv[i] / max(1.0, 4 * tv[7]), 1)
+                                                         for i, k in enumerate(TIMER_PHASES[:7])},
+                                "share": {k: round(tv[i] / tot, 4) for i, k in enumerate(TIMER_PHASES[:7])}}
     if not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         cb, cres = cpu_baseline(prob, ab, threads)

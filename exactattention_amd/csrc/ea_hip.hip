@@ -47,6 +47,7 @@ struct Params {
     void* out;
     uint8_t* flags;
     int64_t* stats;
+    int64_t* timers;
     const int32_t* merge_order;
     double alpha;
     int32_t am, ae;
@@ -112,6 +113,29 @@ __device__ __forceinline__ int64_t vis_end(const Params& P, int64_t tok, int64_t
     return e;
 }
 
+// Max over the 64 lanes with DPP row shifts and row broadcasts (no LDS round trip); every lane
+// receives the result. gfx9 DPP controls: row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143; lanes without a source keep their own value (the max identity here).
+__device__ __forceinline__ int wave_max_dpp(int x) {
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xA, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xC, 0xF, false));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Max within each 16-lane DPP row (lanes 16r .. 16r+15); every lane of the row receives it.
+__device__ __forceinline__ int row16_max(int x) {
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0xF, false));
+    // lane 15 of each row now holds the row's max: broadcast it within the row
+    return __shfl(x, (threadIdx.x & 48) | 15, 64);
+}
+
 __device__ __forceinline__ double wave_sum(double x) {
     for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
     return x;
@@ -170,37 +194,50 @@ __global__ void __launch_bounds__(256) ea_prep(Params P) {
 
 // ------------------------------------------------------------------------------------------------
 // Kernel 2: tier-1 split kernel, templated on the rows per block (1, 2 or 4).
-// Block = 4 waves over one (segment, row block, KV split); 64-key tiles. Per tile:
-//   load  thread t fetches 64 contiguous bytes of K and of V of key t/4 (one page lookup), into
-//         registers one tile ahead; they land in LDS (K with an XOR swizzle of its 16-byte
-//         chunks so per-key reads are conflict-free, V row-major);
-//   S     wave w, lane = key: fp64 FMA chains over dims [32w, 32w+32) for each row, q read
-//         through the constant address space (scalar loads, SGPR operands). The block's sum is
-//         exact when the exponent ranges of q and k over those dims satisfy
-//         (FQmax-FQmin') + (FKmax-FKmin') <= 32: every partial sum is then a multiple of the
-//         smallest product lsb and below 2^53 of it. Failing pairs are recomputed in B.
-//   B     wave r finishes row r: the 4 exact block sums are added with TwoSum (error-free), so
-//         s lies in [S + sig - 3u E, S + sig + 3u E] (E = sum of the TwoSum errors, 0 when the
-//         fp64 sum is exact); certified t = RN32(alpha s); w = RN24(2^t) (fp64 tables, 128-bit
-//         enclosure when undecided); running reference exponent and exact power-of-two rescale.
-//   P     wave w: channels 2l, 2l+1 over keys 16w..16w+15, FMA-fused exact products w*v.
+// Block = 4 waves over one (segment, row block, KV split); 64-key tiles, 2 barriers per tile:
+//   [1] K(i) is in LDS (double-buffered, 16-byte chunks XOR-swizzled so per-key reads are
+//       conflict-free).
+//   S   wave w, lane = key: fp64 FMA chains over dims [32w, 32w+32) in 8-dim steps, q read
+//       through the constant address space (scalar loads, SGPR operands). The block's sum is
+//       exact when (FQmax-FQmin') + (FKmax-FKmin') <= 32 over those dims: every partial sum is
+//       then a multiple of the smallest product lsb and below 2^53 of it.
+//   [2] the 4 block sums of every (row, key) are in LDS.
+//   B   wave w, lanes = (row r, key 16w + l): the 4 exact block sums added with TwoSum
+//       (error-free), so s lies in [S + sig - 3u E, S + sig + 3u E], E the sum of the TwoSum errors
+//       (0 when the fp64 sum is exact); pairs whose blocks were not certified exact are redone
+//       product by product. Certified t = RN32(alpha s); w = RN24(2^t) (fp64 tables; 128-bit
+//       enclosure when undecided). Each wave keeps its own running reference exponent per row.
+//   P   wave w: channels 2l, 2l+1 over its 16 keys from registers (the V row of a wave-uniform key:
+//       one 256-byte coalesced load, page lookup on the scalar unit), FMA-fused exact products.
+//       Then V(i+1) is requested and K(i+1) stored to the other LDS buffer.
+// The epilogue merges the 4 wave partials of each row (exact power-of-two rescale, 3 additions).
 // ------------------------------------------------------------------------------------------------
 struct SplitSmem {
-    uint4 K[EA_TILE * 16];               // 16 KB, swizzled chunks
-    uint4 V[EA_TILE * 16];               // 16 KB, row-major
+    uint4 K[2][EA_TILE * 16];            // 32 KB, swizzled chunks; the epilogue reuses it
     double T1[256], T2[256];             // 4 KB
     double sc[4][EA_MAXRB][EA_TILE];     // 8 KB block sums
     uint32_t fm[4][EA_TILE];             // 1 KB: bit r = block sum of row r not certified exact
-    uint32_t kmx[4][EA_TILE];            // 1 KB: packed max magnitude of the block (for the slow path)
-    double w[EA_MAXRB][EA_TILE];         // 2 KB weights of the tile
-    double scale[EA_MAXRB];
+    double w[4][EA_MAXRB][16];           // 2 KB: each wave's weights of its 16 keys
+    int32_t wR[4][EA_MAXRB];             // epilogue: per-wave reference exponents
+    double wZ[4][EA_MAXRB];
+    int32_t wn[4][EA_MAXRB];
+    uint32_t vred[4][64];                // 1 KB
 };
 
 typedef const double __attribute__((address_space(4))) cdouble_t;
 typedef const int32_t __attribute__((address_space(4))) cint_t;
 
-template <int RB>
+template <int RB, bool TIMERS>
 __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
+    uint64_t tclk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t tprev = TIMERS ? __builtin_amdgcn_s_memtime() : 0;
+    auto tick = [&](int ph) {
+        if (TIMERS) {
+            uint64_t t = __builtin_amdgcn_s_memtime();
+            tclk[ph] += t - tprev;
+            tprev = t;
+        }
+    };
     extern __shared__ __align__(16) unsigned char smem_raw[];
     SplitSmem& S = *reinterpret_cast<SplitSmem*>(smem_raw);
     const int tid = threadIdx.x;
@@ -208,8 +245,7 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int d = P.g.head_dim, dv = P.g.head_dim_v;
     const int nchunk = d >> 3;   // 16-byte chunks per key row
-    const int nvch = dv >> 3;    // 16-byte chunks per value row
-    const int ndw = dv >> 1;
+    const int ndw = dv >> 1;     // dwords per value row
 
     const int item = blockIdx.x;
     const int seg = item / P.nrb, rbk = item % P.nrb;
@@ -234,18 +270,31 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
         grow[r] = row_index(P, b, t, hk * P.grp + gi);
         kend = max(kend, vis_end(P, b * P.g.num_tokens + t, b));
     }
-    int64_t my_grow = 0, my_gtok = 0;
-    if (w < nrow) {
-        int lr = row0 + w;
+    // B-phase role: lane -> (row br, key 16w + bk); lanes with br >= nrow only idle
+    const int br = lane >> 4, bk = lane & 15;
+    const bool brow_ok = br < nrow;
+    int64_t my_grow = 0;
+    int64_t my_kvl = 0, my_tb = 0;
+    uint64_t my_tm = 0;
+    if (brow_ok) {
+        int lr = row0 + br;
         int t = lr / P.grp, gi = lr % P.grp;
         my_grow = row_index(P, b, t, hk * P.grp + gi);
-        my_gtok = b * P.g.num_tokens + t;
+        int64_t tok = b * P.g.num_tokens + t;
+        my_kvl = P.kv_len[tok];
+        if (P.tree_mask) {
+            my_tm = P.tree_mask[tok];
+            my_tb = P.tree_base[b];
+        }
     }
     const int64_t slen = P.seq_len[b];
     if (kend > slen) kend = slen;
     const int64_t k0 = (int64_t)split * P.split_len;
     const int64_t k1 = min(k0 + (int64_t)P.split_len, kend);
     const int64_t pbase = (int64_t)split * P.rows;
+    const int64_t bt_off = P.bt ? (P.bt_off ? P.bt_off[b] : b * (int64_t)P.g.block_table_stride) : 0;
+    cint_t* bt4 = (cint_t*)P.bt;
+    const int pmask = (1 << P.pshift) - 1;
 
     // exponent ranges of this wave's q block for each row (scalar loads)
     cint_t* qinfo4 = (cint_t*)P.qinfo;
@@ -257,8 +306,9 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
         qzero[r] = (qi == (int32_t)0x80000000);
         qspread[r] = ((qi >> 16) & 0x1FF) - (qi & 0xFFFF);
     }
-    int rflag = 0;
-    if (w < nrow && qinfo4[my_grow * 5 + 4]) rflag = 1;
+    // per-lane (B role) row state; the flag and running exponent are uniform within a row's
+    // 16 lanes
+    int rflag = (brow_ok && qinfo4[my_grow * 5 + 4]) ? 1 : 0;
     int Rrun = INT_MIN;
     double zacc = 0.0;
     int nvis = 0;
@@ -268,116 +318,144 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
     for (int r = 0; r < RB; ++r) acc[r][0] = acc[r][1] = 0.0;
     uint32_t vmx = 0;  // packed max |v| magnitude bits, channels 2*lane, 2*lane+1
 
-    // loader role: key kt = tid/4, 64-byte quarter qq = tid%4 (chunks 4j + qq, j = 0..3)
+    // K loader role: key kt = tid/4, 64-byte quarter qq = tid%4 (chunks 4j + qq, j = 0..3)
     const int kt = tid >> 2, qq = tid & 3;
-    uint4 kst[4], vst[4];
-    auto load_tile = [&](int64_t n0) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 kst[4];
+    auto load_k = [&](int64_t n0) {
         int64_t n = n0 + kt;
         bool ok = n < k1;
         int64_t page = b, slot = n;
         if (ok && P.bt) {
-            int64_t off = P.bt_off ? P.bt_off[b] : b * (int64_t)P.g.block_table_stride;
-            page = P.bt[off + (n >> P.pshift)];
-            slot = n & ((1 << P.pshift) - 1);
+            page = P.bt[bt_off + (n >> P.pshift)];
+            slot = n & pmask;
         }
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         const u32x4* kp = reinterpret_cast<const u32x4*>(P.k + page * P.g.k_page_stride + slot * P.g.k_slot_stride +
                                                          (int64_t)hk * P.g.k_head_stride);
-        const u32x4* vp = reinterpret_cast<const u32x4*>(P.v + page * P.g.v_page_stride + slot * P.g.v_slot_stride +
-                                                         (int64_t)hk * P.g.v_head_stride);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             int c = 4 * j + qq;
-            u32x4 a = {0, 0, 0, 0}, v4 = {0, 0, 0, 0};
+            u32x4 a = {0, 0, 0, 0};
             if (ok && c < nchunk) a = __builtin_nontemporal_load(kp + c);
-            if (ok && c < nvch) v4 = __builtin_nontemporal_load(vp + c);
-            kst[j] = make_uint4(a.x, a.y, a.z, a.w);
-            vst[j] = make_uint4(v4.x, v4.y, v4.z, v4.w);
+            kst[j] = a;
         }
     };
-    auto store_tile = [&]() {
+    auto store_k = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             int c = 4 * j + qq;
-            S.K[kt * 16 + (c ^ (kt & 15))] = kst[j];
-            S.V[kt * 16 + c] = vst[j];
+            S.K[buf][kt * 16 + (c ^ (kt & 15))] = make_uint4(kst[j].x, kst[j].y, kst[j].z, kst[j].w);
+        }
+    };
+    // V loader role (wave w, keys 16w..16w+15 of the tile, dword `lane` of each row)
+    uint32_t vr[16];
+    auto load_v = [&](int64_t n0) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            int64_t n = n0 + 16 * w + kk;  // wave-uniform
+            uint32_t val = 0;
+            if (n < k1) {
+                int64_t page = b, slot = n;
+                if (P.bt) {
+                    page = bt4[bt_off + (n >> P.pshift)];
+                    slot = n & pmask;
+                }
+                const uint32_t* vp = reinterpret_cast<const uint32_t*>(
+                    P.v + page * P.g.v_page_stride + slot * P.g.v_slot_stride + (int64_t)hk * P.g.v_head_stride);
+                if (lane < ndw) val = __builtin_nontemporal_load(vp + lane);
+            }
+            vr[kk] = val;
         }
     };
 
-    if (tid < RB) S.scale[tid] = 1.0;  // rows past nrow never rescale
     const int ntiles = (k1 > k0) ? (int)((k1 - k0 + EA_TILE - 1) / EA_TILE) : 0;
-    if (ntiles > 0) load_tile(k0);
-    cdouble_t* q4 = (cdouble_t*)P.q64;
+    if (ntiles > 0) {
+        load_k(k0);
+        load_v(k0);
+        store_k(0);
+        if (ntiles > 1) load_k(k0 + EA_TILE);
+    }
     const int spread_lim = 32;
 
+    tick(0);
     for (int it = 0; it < ntiles; ++it) {
+        const int buf = it & 1;
         const int64_t n0 = k0 + (int64_t)it * EA_TILE;
-        __syncthreads();  // previous tile's readers are done with S.K / S.V
-        store_tile();
-        if (it + 1 < ntiles) load_tile(n0 + EA_TILE);
-        __syncthreads();
+        __syncthreads();  // [1] K(i) visible; every wave is past B(i-1)
+        tick(1);
 
         // ---- S: dims [32w, 32w+32) of key `lane`, every row
         {
-            uint32_t kd[16];
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                int c = 4 * w + cc;
-                uint4 kv = (c < nchunk) ? S.K[lane * 16 + (c ^ (lane & 15))] : make_uint4(0, 0, 0, 0);
-                kd[4 * cc] = kv.x;
-                kd[4 * cc + 1] = kv.y;
-                kd[4 * cc + 2] = kv.z;
-                kd[4 * cc + 3] = kv.w;
-            }
+            // re-read q through the scalar cache every tile: hoisting 32*RB doubles out of the
+            // loop would exceed the SGPR file and spill them to VGPR lanes
+            uint64_t qaddr = (uint64_t)P.q64;
+            asm volatile("" : "+s"(qaddr));
+            cdouble_t* q4 = (cdouble_t*)qaddr;
             typedef unsigned short us2 __attribute__((ext_vector_type(2)));
             us2 mx = {0, 0}, mn = {0xFFFF, 0xFFFF};
-            double kf[32];
+            double a0[RB], a1[RB];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                us2 mv = __builtin_bit_cast(us2, kd[j] & 0x7FFF7FFFu);
-                mx = __builtin_elementwise_max(mx, mv);
-                mn = __builtin_elementwise_min(mn, mv - (us2){1, 1});
-                kf[2 * j] = bf16lo_f64(kd[j]);
-                kf[2 * j + 1] = bf16hi_f64(kd[j]);
+            for (int r = 0; r < RB; ++r) a0[r] = a1[r] = 0.0;
+#pragma unroll 1
+            for (int cc = 0; cc < 4; ++cc) {
+                const int c = 4 * w + cc;
+                uint4 kv = (c < nchunk) ? S.K[buf][lane * 16 + (c ^ (lane & 15))] : make_uint4(0, 0, 0, 0);
+                uint32_t kd[4] = {kv.x, kv.y, kv.z, kv.w};
+                double kf[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    us2 mv = __builtin_bit_cast(us2, kd[j] & 0x7FFF7FFFu);
+                    mx = __builtin_elementwise_max(mx, mv);
+                    mn = __builtin_elementwise_min(mn, mv - (us2){1, 1});
+                    kf[2 * j] = bf16lo_f64(kd[j]);
+                    kf[2 * j + 1] = bf16hi_f64(kd[j]);
+                }
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    cdouble_t* qr = q4 + grow[r] * EA_MAXD + 8 * c;
+#pragma unroll
+                    for (int i = 0; i < 8; i += 2) {
+                        a0[r] = __fma_rn(qr[i], kf[i], a0[r]);
+                        a1[r] = __fma_rn(qr[i + 1], kf[i + 1], a1[r]);
+                    }
+                }
             }
             uint32_t magmax = max((uint32_t)mx.x, (uint32_t)mx.y);
             uint32_t magmin1 = min((uint32_t)mn.x, (uint32_t)mn.y);
             bool kzero = (magmax == 0);
             int kspread = (int)(magmax >> 7) - max((int)((magmin1 + 1) >> 7), 1);
             uint32_t fmask = 0;
-            const int dbase = 32 * w;
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
-                cdouble_t* qr = q4 + grow[r] * EA_MAXD + dbase;
-                double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-                for (int i = 0; i < 32; i += 2) {
-                    a0 = __fma_rn(qr[i], kf[i], a0);
-                    a1 = __fma_rn(qr[i + 1], kf[i + 1], a1);
-                }
-                S.sc[w][r][lane] = a0 + a1;
+                S.sc[w][r][lane] = a0[r] + a1[r];
                 bool exact = qzero[r] || kzero || (qspread[r] + kspread <= spread_lim);
                 if (!exact) fmask |= 1u << r;
             }
             S.fm[w][lane] = fmask;
         }
-        __syncthreads();
+        if (it + 1 < ntiles) store_k(buf ^ 1);  // K(i+1); buffer buf^1 was last read in S(i-1)
+        if (it + 2 < ntiles) load_k(n0 + 2 * EA_TILE);
+        tick(2);
+        __syncthreads();  // [2]
+        tick(3);
 
-        // ---- B: wave w finishes row w
-        if (w < nrow) {
-            const int r = w;
-            const int64_t n = n0 + lane;
-            const bool vis = (n < k1) && visible(P, my_gtok, b, n);
-            double x0 = S.sc[0][r][lane], x1 = S.sc[1][r][lane], x2 = S.sc[2][r][lane], x3 = S.sc[3][r][lane];
-            bool slow = ((S.fm[0][lane] | S.fm[1][lane] | S.fm[2][lane] | S.fm[3][lane]) >> r) & 1;
+        // ---- B: lanes (row br, key 16w + bk)
+        {
+            const int key = 16 * w + bk;
+            const int64_t n = n0 + key;
+            const int64_t ti = n - my_tb;
+            const bool vis = brow_ok && (n < k1) && (n < my_kvl || (ti >= 0 && ti < 64 && ((my_tm >> ti) & 1)));
+            const int r = brow_ok ? br : 0;
+            double x0 = S.sc[0][r][key], x1 = S.sc[1][r][key], x2 = S.sc[2][r][key], x3 = S.sc[3][r][key];
+            bool slow = ((S.fm[0][key] | S.fm[1][key] | S.fm[2][key] | S.fm[3][key]) >> r) & 1;
             double ssum, sig, del;
             if (vis && slow) {
                 // every product separately, TwoSum-accumulated: exact up to the rounding of the
-                // error sum, bounded by 130 u E (E = sum of |TwoSum errors|)
-                cdouble_t* qr = q4 + my_grow * EA_MAXD;
+                // error sum, bounded by 256 u E (E = sum of |TwoSum errors|, 2 roundings per add)
+                cdouble_t* qr = (cdouble_t*)P.q64 + my_grow * EA_MAXD;
                 double s = 0.0, es = 0.0, ea = 0.0;
                 for (int c = 0; c < nchunk; ++c) {
-                    uint4 kv = S.K[lane * 16 + (c ^ (lane & 15))];
+                    uint4 kv = S.K[buf][key * 16 + (c ^ (key & 15))];
                     uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -390,7 +468,7 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
                 }
                 ssum = s;
                 sig = es;
-                del = ea * 0x1p-44;  // >= 2 u per accumulation of the error sum
+                del = ea * 0x1p-44;
             } else {
                 double e1, e2, e3;
                 double s = two_sum(x0, x1, &e1);
@@ -429,8 +507,9 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
                 if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
             }
             if (why) rflag = 1;
-            rflag = wave_max_i(rflag);
-            int tmax = wave_max_i(vis ? E + 23 : INT_MIN);
+            // maxima over each row's 16 lanes (one DPP row each)
+            rflag = row16_max(rflag);
+            int tmax = row16_max(vis ? E + 23 : INT_MIN);
             int Rnew = max(Rrun, tmax);
             double sc = 1.0;
             if (Rrun != INT_MIN && Rnew != Rrun) {
@@ -449,80 +528,115 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
             zacc += om;
             nvis += vis ? 1 : 0;
             Rrun = Rnew;
-            S.w[r][lane] = om;
-            if (lane == 0) S.scale[r] = sc;
-        }
-        __syncthreads();
-
-        // ---- P: channels 2*lane, 2*lane+1 over keys 16w .. 16w+15
-        if (lane < ndw) {
+            if (brow_ok) S.w[w][br][bk] = om;
+            // rescale this wave's accumulators by each row's factor (uniform per row)
 #pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                double sc = S.scale[r];
-                if (sc != 1.0) {
-                    acc[r][0] *= sc;
-                    acc[r][1] *= sc;
+            for (int rr = 0; rr < RB; ++rr) {
+                double f = __shfl(sc, rr * 16, 64);
+                if (f != 1.0) {
+                    acc[rr][0] *= f;
+                    acc[rr][1] *= f;
                 }
             }
+        }
+
+        tick(4);
+        // ---- P: channels 2*lane, 2*lane+1 over keys 16w .. 16w+15 (weights of this wave)
+        {
             typedef unsigned short us2 __attribute__((ext_vector_type(2)));
             us2 vm = __builtin_bit_cast(us2, vmx);
-            const uint32_t* Vd = reinterpret_cast<const uint32_t*>(S.V);
-#pragma unroll 4
-            for (int kk = 0; kk < 16; ++kk) {
-                int key = 16 * w + kk;
-                uint32_t vd = Vd[key * 64 + lane];
-                vm = __builtin_elementwise_max(vm, __builtin_bit_cast(us2, vd & 0x7FFF7FFFu));
-                double v0 = bf16lo_f64(vd), v1 = bf16hi_f64(vd);
+#pragma unroll 2
+            for (int kk = 0; kk < 16; kk += 2) {
+                uint32_t vd0 = vr[kk], vd1 = vr[kk + 1];
+                vm = __builtin_elementwise_max(vm, __builtin_bit_cast(us2, vd0 & 0x7FFF7FFFu));
+                vm = __builtin_elementwise_max(vm, __builtin_bit_cast(us2, vd1 & 0x7FFF7FFFu));
+                double v00 = bf16lo_f64(vd0), v01 = bf16hi_f64(vd0);
+                double v10 = bf16lo_f64(vd1), v11 = bf16hi_f64(vd1);
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
-                    double om = S.w[r][key];
-                    acc[r][0] = __fma_rn(om, v0, acc[r][0]);
-                    acc[r][1] = __fma_rn(om, v1, acc[r][1]);
+                    double2 om = *reinterpret_cast<const double2*>(&S.w[w][r][kk]);
+                    acc[r][0] = __fma_rn(om.x, v00, acc[r][0]);
+                    acc[r][1] = __fma_rn(om.x, v01, acc[r][1]);
+                    acc[r][0] = __fma_rn(om.y, v10, acc[r][0]);
+                    acc[r][1] = __fma_rn(om.y, v11, acc[r][1]);
                 }
             }
             vmx = __builtin_bit_cast(uint32_t, vm);
         }
+        if (it + 1 < ntiles) load_v(n0 + EA_TILE);
+        tick(5);
+    }
+
+    // ---- epilogue: merge the 4 wave partials of each row, write the split partial
+    {
+        // row scalars of this wave (lane 16 r holds row r's running exponent and flag)
+        double z = zacc;
+        int nv = nvis;
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {  // sums within each 16-lane row
+            z += __shfl_xor(z, o, 64);
+            nv += __shfl_xor(nv, o, 64);
+        }
+        if (bk == 0 && br < RB) {
+            S.wR[w][br] = rflag ? -0x7FFFFFFF : Rrun;  // INT_MIN = no key, -0x7FFFFFFF = flagged
+            S.wZ[w][br] = z;
+            S.wn[w][br] = nv;
+        }
     }
     __syncthreads();
-
-    // ---- epilogue: reduce N over the 4 waves, write the split partial
-    double* red = reinterpret_cast<double*>(&S.K[0]);  // 4 * EA_MAXRB * 128 doubles = 16 KB
-    uint32_t* vred = reinterpret_cast<uint32_t*>(&S.V[0]);
+    double* red = reinterpret_cast<double*>(&S.K[0][0]);  // 4 * EA_MAXRB * 128 doubles = 16 KB
     if (lane < ndw) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
             red[((w * EA_MAXRB) + r) * 128 + 2 * lane] = acc[r][0];
             red[((w * EA_MAXRB) + r) * 128 + 2 * lane + 1] = acc[r][1];
         }
-        vred[w * 64 + lane] = vmx;
     }
-    if (w < nrow) {
-        double z = wave_sum(zacc);
-        int nv = wave_sum_i(nvis);
-        if (lane == 0) {
-            int64_t o = pbase + my_grow;
-            P.pR[o] = Rrun;
-            P.pZ[o] = z;
-            P.pn[o] = rflag ? -1 : nv;
-        }
-    }
+    S.vred[w][lane] = vmx;
     __syncthreads();
     for (int x = tid; x < nrow * dv; x += EA_THREADS) {
         int r = x / dv, c = x % dv;
-        double s = 0.0;
-        for (int ww = 0; ww < 4; ++ww) s += red[((ww * EA_MAXRB) + r) * 128 + c];
+        int R = INT_MIN;
+        bool fl = false;
+        for (int ww = 0; ww < 4; ++ww) {
+            int rw = S.wR[ww][r];
+            if (rw == -0x7FFFFFFF) fl = true;
+            else R = max(R, rw);
+        }
+        double s = 0.0, zs = 0.0;
+        int nv = 0;
+        for (int ww = 0; ww < 4; ++ww) {
+            int rw = S.wR[ww][r];
+            if (rw == INT_MIN || rw == -0x7FFFFFFF) continue;
+            if (rw - R < -900) fl = true;
+            s += ldexp(red[((ww * EA_MAXRB) + r) * 128 + c], max(rw - R, -1000));
+            zs += ldexp(S.wZ[ww][r], max(rw - R, -1000));
+            nv += S.wn[ww][r];
+        }
         int lr = row0 + r;
         int t = lr / P.grp, gi = lr % P.grp;
-        P.pN[(pbase + row_index(P, b, t, hk * P.grp + gi)) * dv + c] = s;
+        int64_t o = pbase + row_index(P, b, t, hk * P.grp + gi);
+        P.pN[o * dv + c] = s;
+        if (c == 0) {
+            P.pR[o] = R;
+            P.pZ[o] = zs;
+            P.pn[o] = fl ? -1 : nv;
+        }
     }
     for (int c = tid; c < dv; c += EA_THREADS) {
         uint32_t m = 0;
         for (int ww = 0; ww < 4; ++ww) {
-            uint32_t a = vred[ww * 64 + (c >> 1)];
+            uint32_t a = S.vred[ww][c >> 1];
             m = max(m, (c & 1) ? (a >> 16) : (a & 0xFFFF));
         }
         // bf16 magnitude bits -> fp32 value (a NaN pattern keeps the row from certifying)
         P.pV[(((int64_t)split * P.nseg + seg) * P.nrb + rbk) * dv + c] = __uint_as_float(m << 16);
+    }
+    if (TIMERS) {
+        tick(6);
+        tclk[7] = (uint64_t)ntiles;
+        if (lane == 0)
+            for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
     }
 }
 
@@ -956,6 +1070,12 @@ __global__ void ea_kat_weight(int64_t n, const uint32_t* t, int32_t* M, int64_t*
     E2[i] = e2;
 }
 
+__global__ void __launch_bounds__(64) ea_kat_wave_max(int64_t nwaves, const int32_t* in, int32_t* out) {
+    if (blockIdx.x >= nwaves) return;
+    int v = wave_max_dpp(in[blockIdx.x * 64 + threadIdx.x]);
+    out[blockIdx.x * 64 + threadIdx.x] = v;
+}
+
 __global__ void ea_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, uint32_t* bits, int32_t* ok) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -1078,6 +1198,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.seq_len = bf->seq_len; P.kv_len = bf->kv_len; P.bt = bf->block_table; P.bt_off = bf->block_table_offset;
     P.tree_mask = bf->tree_mask; P.tree_base = bf->tree_base;
     P.out = bf->out; P.flags = bf->flags; P.stats = o->stats; P.merge_order = o->merge_order;
+    P.timers = o->timers;
     float af;
     memcpy(&af, &ab, 4);
     P.alpha = (double)af;
@@ -1118,7 +1239,9 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         static std::once_flag once;
         static hipError_t attr_err = hipSuccess;
         std::call_once(once, [] {
-            const void* fns[3] = {(const void*)ea_split<1>, (const void*)ea_split<2>, (const void*)ea_split<4>};
+            const void* fns[6] = {(const void*)ea_split<1, false>, (const void*)ea_split<2, false>,
+                                  (const void*)ea_split<4, false>, (const void*)ea_split<1, true>,
+                                  (const void*)ea_split<2, true>, (const void*)ea_split<4, true>};
             for (const void* f : fns) {
                 hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    (int)sizeof(SplitSmem));
@@ -1129,9 +1252,17 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         if (rc) return rc;
         dim3 grid((unsigned)(pl.nseg * pl.nrb), (unsigned)pl.nsplit);
         if ((rc = mark(1))) return rc;
-        if (pl.rb == 1) hipLaunchKernelGGL(ea_split<1>, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
-        else if (pl.rb == 2) hipLaunchKernelGGL(ea_split<2>, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
-        else hipLaunchKernelGGL(ea_split<4>, grid, dim3(EA_THREADS), sizeof(SplitSmem), st, P);
+        const dim3 blk(EA_THREADS);
+        const size_t lds = sizeof(SplitSmem);
+        if (o->timers) {
+            if (pl.rb == 1) hipLaunchKernelGGL((ea_split<1, true>), grid, blk, lds, st, P);
+            else if (pl.rb == 2) hipLaunchKernelGGL((ea_split<2, true>), grid, blk, lds, st, P);
+            else hipLaunchKernelGGL((ea_split<4, true>), grid, blk, lds, st, P);
+        } else {
+            if (pl.rb == 1) hipLaunchKernelGGL((ea_split<1, false>), grid, blk, lds, st, P);
+            else if (pl.rb == 2) hipLaunchKernelGGL((ea_split<2, false>), grid, blk, lds, st, P);
+            else hipLaunchKernelGGL((ea_split<4, false>), grid, blk, lds, st, P);
+        }
         rc = herr(hipGetLastError());
         if (rc) return rc;
     } else if ((rc = mark(1))) {
@@ -1241,6 +1372,12 @@ int ea_hip_kat_weight(int64_t n, const uint32_t* t_bits, int32_t* M, int64_t* E,
     if (n <= 0) return n < 0 ? -1 : 0;
     hipLaunchKernelGGL(ea_kat_weight, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n, t_bits,
                        M, E, status, M2, E2, status2);
+    return herr(hipGetLastError());
+}
+
+int ea_hip_kat_wave_max(int64_t nwaves, const int32_t* in, int32_t* out, ea_stream_t stream) {
+    if (nwaves <= 0) return nwaves < 0 ? -1 : 0;
+    hipLaunchKernelGGL(ea_kat_wave_max, dim3((unsigned)nwaves), dim3(64), 0, (hipStream_t)stream, nwaves, in, out);
     return herr(hipGetLastError());
 }
 

@@ -40,8 +40,7 @@ class Buffers(ctypes.Structure):
 
 class Options(ctypes.Structure):
     _fields_ = [("alpha_bits", ctypes.c_uint32), ("out_fp32", ctypes.c_int32), ("splits", ctypes.c_int32),
-                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P),
-                ("reserved", ctypes.c_int32 * 2)]
+                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P), ("timers", P)]
 
 
 STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
@@ -76,6 +75,8 @@ def load():
         lib.ea_hip_kat_round.restype = ctypes.c_int
         lib.ea_hip_kat_round_ratio.argtypes = [ctypes.c_int64] + [P] * 6 + [ctypes.c_int32, P, P, P]
         lib.ea_hip_kat_round_ratio.restype = ctypes.c_int
+        lib.ea_hip_kat_wave_max.argtypes = [ctypes.c_int64, P, P, P]
+        lib.ea_hip_kat_wave_max.restype = ctypes.c_int
         lib.ea_hip_version.restype = ctypes.c_char_p
         _lib = lib
     return _lib
@@ -143,7 +144,11 @@ class DeviceProblem:
         return Buffers(**ptr, out=self.out.data_ptr(), flags=self.flags.data_ptr())
 
 
-def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True, events=None) -> None:
+TIMER_PHASES = ["prologue", "tile_barrier", "scores", "score_barrier", "weights", "pv", "epilogue", "tiles"]
+
+
+def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True, events=None,
+               timers=None) -> None:
     """Enqueue one step on torch's current stream (no sync, no host copies, no allocation).
     `events`: optional ctypes array of 5 hipEvent_t handles recorded between the kernels."""
     lib = load()
@@ -152,7 +157,8 @@ def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool
         mo = merge_order if hasattr(merge_order, "data_ptr") else None
     o = Options(alpha_bits=alpha_bits, out_fp32=int(dp.out_fp32), splits=dp.splits, tier2=int(tier2),
                 merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr(),
-                events=None if events is None else ctypes.cast(events, P))
+                events=None if events is None else ctypes.cast(events, P),
+                timers=None if timers is None else timers.data_ptr())
     b = dp.buffers()
     _check(lib.ea_hip_attention(ctypes.byref(dp._geom_c), ctypes.byref(b), ctypes.byref(o), dp.workspace.data_ptr(),
                                 dp.ws_bytes, _stream_ptr(dp.torch)), "ea_hip_attention")

@@ -84,7 +84,12 @@ typedef struct ea_options {
                                path, [9..15] reserved */
     void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep, split,
                                combine and tier 2, and after tier 2 (per-kernel timing) */
-    int32_t reserved[2];
+    int64_t* timers;        /* optional device int64[16]: when set, the split kernel runs its
+                               phase-clock build and adds shader-clock cycles (s_memtime) summed
+                               over waves: [0] prologue, [1] wait for the tile barrier, [2] scores,
+                               [3] wait for the score barrier, [4] logits and weights, [5] P.V,
+                               [6] epilogue, [7] tiles; the reference's TIMERS build
+                               (src/exactattn/triton_kernels.py:747-766) */
 } ea_options;
 
 /* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
@@ -123,6 +128,10 @@ int ea_hip_kat_weight(int64_t n, const uint32_t* t_bits, int32_t* M, int64_t* E,
                       int64_t* E2, int32_t* status2, ea_stream_t stream);
 int ea_hip_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, uint32_t* bits, int32_t* ok,
                      ea_stream_t stream);
+/* ea_hip_kat_wave_max: each 64-lane wave's max of in[64 w .. 64 w + 63] into every lane of out
+ * (the DPP reduction the split kernel uses for row maxima and flags). No reference counterpart:
+ * the reference's reductions are Triton's tl.max. */
+int ea_hip_kat_wave_max(int64_t nwaves, const int32_t* in, int32_t* out, ea_stream_t stream);
 int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo, const uint64_t* b_hi,
                            const uint64_t* b_lo, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
                            int32_t* overflow, ea_stream_t stream);

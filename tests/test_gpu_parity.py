@@ -115,6 +115,25 @@ def test_round_ratio_kat_matches_oracle(gpu):
                 assert int(gb[i]) == wb, (a, b, e, neg, fp32)
 
 
+def test_wave_max_dpp_kat(gpu):
+    import torch
+    from exactattention_amd import hip
+    rng = np.random.default_rng(2)
+    x = rng.integers(-(1 << 31), (1 << 31) - 1, size=(300, 64), dtype=np.int64).astype(np.int32)
+    x[0] = np.iinfo(np.int32).min
+    x[1, 37] = np.iinfo(np.int32).max
+    x[2] = np.arange(64)[::-1]
+    for i in range(3, 67):
+        x[i] = -5
+        x[i, i - 3] = 7  # the max in each lane position
+    xi = torch.from_numpy(x).cuda()
+    out = torch.zeros_like(xi)
+    assert hip.load().ea_hip_kat_wave_max(x.shape[0], xi.data_ptr(), out.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), np.repeat(x.max(axis=1, keepdims=True), 64, axis=1))
+
+
 def test_certify_round_kat(gpu):
     """certify_round on exact points (r = 0) equals RN of the point; with r > 0 it never certifies
     an interval that holds a rounding midpoint."""
