@@ -58,12 +58,14 @@ def attention_hip(q_bits, k_bits, v_bits, alpha, kv_len=None, row_ptr=None, key_
     v = np.asarray(v_bits, dtype=np.uint16)
     R, n = q.shape[0], k.shape[0]
     if row_ptr is None:
-        if kv_len is None:
-            kv_len = np.full(R, n)
-        kv_len = np.asarray(kv_len, dtype=np.int64)
-        row_ptr = np.concatenate([[0], np.cumsum(kv_len)]).astype(np.int64)
-        key_idx = np.concatenate([np.arange(x) for x in kv_len]).astype(np.int64) if R else np.zeros(0, np.int64)
-    prob = problem.csr(q, k, v, row_ptr, key_idx)
+        # prefix rows: one segment of R tokens over one contiguous cache (shares K/V tiles)
+        kv_len = np.full(R, n) if kv_len is None else np.asarray(kv_len, dtype=np.int64).reshape(R)
+        if np.any(kv_len < 0) or np.any(kv_len > n):
+            raise ValueError("kv_len must lie in [0, n]")
+        prob = problem.contiguous(q.reshape(1, R, 1, -1), k.reshape(1, 1, n, -1), v.reshape(1, 1, n, -1),
+                                  kv_len.reshape(1, R))
+    else:
+        prob = problem.csr(q, k, v, row_ptr, key_idx)
     res, flags, _ = attention_problem(prob, _alpha_bits(alpha), out, splits, merge_order, True, fallback, device)
     return _finish(res.reshape(R, -1), out), flags
 

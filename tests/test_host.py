@@ -1,0 +1,136 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every symbol the header
+declares, argument validation returns the documented codes before any device work, the problem
+builders lay out what the geometry says, and the benchmark configurations are deterministic."""
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from exactattention_amd import configs, problem
+from exactattention_amd.formats import default_alpha_bits
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "exactattn_hip.h")
+
+
+def _lib():
+    from exactattention_amd import hip
+    if not hip.available():
+        pytest.skip("libexactattn_hip.so not built (run __graft_entry__.build())")
+    return hip.load()
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\**\s*(ea_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    names = _declared_functions()
+    assert len(names) >= 8, names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert b"gfx950" in lib.ea_hip_version()
+
+
+def _c2_geom(**over):
+    p = problem.paged(np.zeros((32, 1, 16, 128), np.uint16), np.zeros((8192, 16, 8, 128), np.uint16),
+                      np.zeros((8192, 16, 8, 128), np.uint16), np.zeros((32, 256), np.int32),
+                      np.full((32, 1), 4096), np.full(32, 4096))
+    g = dict(p["geom"])
+    g.update(over)
+    return g
+
+
+def _ws(g, splits=0):
+    from exactattention_amd import hip
+    lib = _lib()
+    o = hip.Options(splits=splits, tier2=1)
+    nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
+    rc = lib.ea_hip_workspace_size(ctypes.byref(hip.geometry(g)), ctypes.byref(o), ctypes.byref(nb),
+                                   ctypes.byref(ns))
+    return rc, nb.value, ns.value
+
+
+def test_workspace_size_and_split_plan():
+    rc, nb, ns = _ws(_c2_geom(), splits=8)
+    assert rc == 0 and ns == 8
+    rows = 32 * 16
+    assert nb >= rows * 128 * 8 + 8 * rows * 128 * 8  # q in fp64 + the N partials
+    rc, _, ns_auto = _ws(_c2_geom())
+    assert rc == 0 and 1 <= ns_auto <= 64
+
+
+@pytest.mark.parametrize("bad,code", [
+    (dict(num_q_heads=12, num_kv_heads=8), -1),   # heads not a multiple
+    (dict(head_dim=256), -1),                    # above 128
+    (dict(head_dim=100), -1),                    # not a multiple of 8
+    (dict(head_dim_v=127), -1),                  # odd
+    (dict(page_size=12), -1),                    # not a power of two
+    (dict(num_tokens=0), -1),
+])
+def test_workspace_size_rejects_bad_geometry(bad, code):
+    assert _ws(_c2_geom(**bad))[0] == code
+
+
+def test_negative_splits_is_an_option_error():
+    assert _ws(_c2_geom(), splits=-1)[0] == -2
+
+
+def test_attention_validates_before_any_device_work():
+    from exactattention_amd import hip
+    lib = _lib()
+    g = hip.geometry(_c2_geom())
+    fake = 4096  # never dereferenced: each call below returns before touching memory or the device
+    full = hip.Buffers(q=fake, k=fake, v=fake, seq_len=fake, kv_len=fake, out=fake, flags=fake)
+    nan = hip.Options(alpha_bits=0x7FC00000, tier2=1)
+    ok = hip.Options(alpha_bits=default_alpha_bits(128), tier2=1)
+    _, nb, _ = _ws(_c2_geom())
+    # missing required buffer
+    rc = lib.ea_hip_attention(ctypes.byref(g), ctypes.byref(hip.Buffers(q=fake)), ctypes.byref(ok), fake, nb, None)
+    assert rc == -1
+    # workspace too small
+    rc = lib.ea_hip_attention(ctypes.byref(g), ctypes.byref(full), ctypes.byref(ok), fake, nb - 1, None)
+    assert rc == -2
+    # non-finite alpha
+    rc = lib.ea_hip_attention(ctypes.byref(g), ctypes.byref(full), ctypes.byref(nan), fake, nb, None)
+    assert rc == -3
+
+
+def test_to_paged_preserves_every_key():
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 0x3F80, (2, 1, 4, 16), dtype=np.uint16)
+    k = rng.integers(0, 0x3F80, (2, 2, 37, 16), dtype=np.uint16)
+    v = rng.integers(0, 0x3F80, (2, 2, 37, 16), dtype=np.uint16)
+    base = problem.contiguous(q, k, v, np.full((2, 1), 37))
+    for ps in (1, 4, 16):
+        for layout in ("NHD", "HND"):
+            p = problem.to_paged(base, ps, np.random.default_rng(ps), layout)
+            g = p["geom"]
+            kp = p["k"].reshape(-1)
+            for b in range(2):
+                for hk in range(2):
+                    for n in range(37):
+                        page = p["block_table"][b, n // ps]
+                        off = page * g["k_page_stride"] + (n % ps) * g["k_slot_stride"] + hk * g["k_head_stride"]
+                        assert np.array_equal(kp[off:off + 16], k[b, hk, n]), (ps, layout, b, hk, n)
+
+
+def test_configs_are_deterministic_and_sized():
+    a, b = configs.c1(), configs.c1()
+    for key in ("q", "k", "v", "kv_len"):
+        assert np.array_equal(a[key], b[key])
+    assert int(a["kv_len"].sum()) == 63520
+    assert configs.alpha_bits() == 0x3E0293EE
+
+
+def test_bench_refuses_several_gpus():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
