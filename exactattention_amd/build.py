@@ -6,6 +6,7 @@ import os
 import subprocess
 import sys
 
+SOURCES = ["ea_hip.hip", "ea_decode.hip"]
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libexactattn_hip.so")
@@ -22,7 +23,7 @@ def build(verbose: bool = False) -> str:
     gen = os.path.join(CSRC, "gen_tables.py")
     subprocess.run([sys.executable, gen], check=True, stdout=subprocess.DEVNULL)
     tmp = LIB + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, "-o", tmp, os.path.join(CSRC, "ea_hip.hip")]
+    cmd = [hipcc, *HIPCC_FLAGS, "-o", tmp] + [os.path.join(CSRC, f) for f in SOURCES]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

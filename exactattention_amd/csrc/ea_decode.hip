@@ -1,0 +1,488 @@
+// Tier-1 decode kernel for d = dv = 128 on gfx950: one wave per (segment, row block, KV split).
+//
+// The reference runs this step as its Triton split program (src/exactattn/triton_kernels.py:
+// 730-1077) over precomputed int8 slice planes (~1053 bytes per key and KV head). Here the wave
+// reads the raw bf16 K/V pages (512 bytes per key and KV head) and computes in fp64, which CDNA4
+// issues at the full VALU rate:
+//
+//   K tile  64 keys (16 KB), DMA'd by global_load_lds_dwordx4 straight into LDS (no VGPR
+//           round trip), 16-byte chunks XOR-swizzled by key so per-key reads are conflict-free;
+//           double-buffered, tile i+1 in flight while tile i is processed.
+//   S       lane = key: two fp64 FMA chains per row over the 128 dims, q as SGPR operands
+//           (scalar loads of the prep kernel's fp64 q). Rounding error of the chains is bounded
+//           by 66 u sum_b |q_b|_1 |k_b|_inf over four 32-dim blocks (|k_b|_inf from v_max3_f32
+//           on the fp32 patterns the conversion makes anyway).
+//   B       lane = key, every row: certified t = RN32(alpha s) from the interval, RN24(2^t)
+//           from the fp64 tables; pairs the interval cannot decide take the exact TwoSum path.
+//           Running per-row reference exponent from a DPP wave max; weights to LDS.
+//   P       lane = (key group g, 8 channels): V rows of 4 keys per dwordx4 load (1 KB per
+//           instruction, coalesced, page base on the scalar unit), double-buffered in VGPRs;
+//           exact products omega*v summed by FMA.
+// The epilogue reduces the 4 key groups and writes the split partial in the layout the combine
+// kernel reads (R, n, Z, N[dv] per split and row; max |v| per channel per row block).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+
+#include "ea_params.h"
+
+using namespace ea;
+
+namespace {
+
+constexpr int DT = 64;  // keys per tile = lanes
+
+struct DecodeSmem {
+    uint4 K[2][DT * 16];   // 2 x 16 KB; reused by the epilogue reduction
+    double w[DT][4];       // weights of the tile, [key][row]
+    double T1[256], T2[256];
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt vmcnt(n), expcnt/lgkmcnt untouched (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[5:4] in bits 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ float absf(float x) { return __builtin_fabsf(x); }
+
+}  // namespace
+
+template <int RB, int PGL>
+__global__ void __launch_bounds__(64) ea_decode(Params P) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    DecodeSmem& S = *reinterpret_cast<DecodeSmem*>(smem_raw);
+    const int lane = threadIdx.x;
+    const int g = lane >> 4, c8 = lane & 15;
+
+    const int item = blockIdx.x;
+    const int seg = item / P.nrb, rbk = item % P.nrb;
+    const int split = blockIdx.y;
+    const int Hkv = P.g.num_kv_heads;
+    const int b = seg / Hkv;
+    const int hk = seg % Hkv;
+    const int row0 = rbk * P.rb;
+    const int nrow = min(RB, P.r_seg - row0);
+
+    for (int i = lane; i < 256; i += 64) {
+        S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
+        S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
+    }
+
+    cint_t* kvl4 = (cint_t*)P.kv_len;
+    cint_t* qinfo4 = (cint_t*)P.qinfo;
+    cdouble_t* qn4 = (cdouble_t*)P.qn;
+    // rows of the block (a short block repeats its last row; repeats are never written). Key
+    // positions, lengths and row indices fit 31 bits (checked by the launcher).
+    int grow[RB];
+    int kvl[RB];
+    uint64_t tmk[RB];
+    int rflag[RB];
+    int kend = 0;
+    int tb = 0;
+    if (P.tree_mask) tb = ((cint_t*)P.tree_base)[b];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        int lr = row0 + min(r, nrow - 1);
+        int t = lr / P.grp, gi = lr % P.grp;
+        grow[r] = (int)row_index(P, b, t, hk * P.grp + gi);
+        int tok = b * P.g.num_tokens + t;
+        kvl[r] = kvl4[tok];
+        tmk[r] = P.tree_mask ? ((const uint64_t __attribute__((address_space(4)))*)P.tree_mask)[tok] : 0ull;
+        int e = kvl[r];
+        if (tmk[r]) e = max(e, tb + 64 - (int)__clzll(tmk[r]));
+        kend = max(kend, e);
+        rflag[r] = qinfo4[grow[r] * 5 + 4] ? 1 : 0;
+    }
+    const int slen = ((cint_t*)P.seq_len)[b];
+    if (kend > slen) kend = slen;
+    const int k0 = split * P.split_len;
+    const int k1 = min(k0 + P.split_len, kend);
+    const int64_t pbase = (int64_t)split * P.rows;
+    cint_t* btb = (cint_t*)P.bt + (P.bt ? (P.bt_off ? P.bt_off[b] : (int64_t)b * P.g.block_table_stride) : 0);
+    const int pshift = P.pshift;
+    const int pmask = (1 << pshift) - 1;
+    // byte strides; the slot part of an address goes into the 32-bit soffset
+    const int64_t kps2 = 2 * P.g.k_page_stride, vps2 = 2 * P.g.v_page_stride;
+    const int kss2 = (int)(2 * P.g.k_slot_stride), vss2 = (int)(2 * P.g.v_slot_stride);
+    const char* kh = (const char*)(P.k + (int64_t)hk * P.g.k_head_stride);
+    const char* vh = (const char*)(P.v + (int64_t)hk * P.g.v_head_stride);
+    // per-lane byte offsets inside a 4-key group: K lane (g, p) brings chunk p ^ ((4j + g) & 15)
+    // of key 4j + g (the XOR depends on j only through j & 3); V lane (g, c8) channels 8 c8 ..
+    int koff[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) koff[jj] = g * kss2 + ((c8 ^ ((4 * jj + g) & 15)) << 4);
+    const int voff = g * vss2 + (c8 << 4);
+
+    // Group j of the tile at n0 holds keys n0+4j .. n0+4j+3, all in one page (page size >= 4 and
+    // n0 % 64 == 0). Pages are looked up every PGL keys (PGL <= page size, or the whole
+    // sequence without a block table); inside a lookup interval the slot advances by 4 keys per
+    // group. `page_rs` returns the buffer resource at the page start and the slot of key n.
+    auto page_rs = [&](int n, const char* head, int64_t ps2, int* slot) __attribute__((always_inline)) {
+        int64_t pg;
+        if (P.bt) {
+            pg = btb[n >> pshift];
+            *slot = n & pmask;
+        } else {
+            pg = b;
+            *slot = n;
+        }
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(head + pg * ps2), (short)0, -1, 0x00020000);
+    };
+    // K tile at n0 -> LDS buffer `buf`: instruction j writes the 1 KB of keys 4j..4j+3; lanes whose
+    // key is past k1 re-read their group's first key into slots no row looks at.
+    auto issue_k = [&](int n0, int buf) __attribute__((always_inline)) {
+        __amdgpu_buffer_rsrc_t rs;
+        int slot = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int nj = n0 + 4 * j;
+            if (nj < k1) {
+                if ((4 * j) % PGL == 0) rs = page_rs(nj, kh, kps2, &slot);
+                const int sl = slot + (4 * j) % PGL;
+                const int off = (nj + g < k1) ? koff[j & 3] : koff[j & 3] - g * kss2;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)&S.K[buf][j * 64], 16, off, sl * kss2, 0, 2);
+            }
+        }
+    };
+    auto issue_v = [&](int n0, u32x4 (&vr)[16]) __attribute__((always_inline)) {
+        __amdgpu_buffer_rsrc_t rs;
+        int slot = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int nj = n0 + 4 * j;
+            u32x4 x = {0, 0, 0, 0};
+            if (nj < k1) {
+                if ((4 * j) % PGL == 0) rs = page_rs(nj, vh, vps2, &slot);
+                const int sl = slot + (4 * j) % PGL;
+                if (nj + g < k1) x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, sl * vss2, 2);
+            }
+            vr[j] = x;
+        }
+    };
+
+    // per-row state
+    int Rrun[RB];
+    double zacc[RB];
+    int nvis[RB];
+    double pacc[RB][8];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        Rrun[r] = INT_MIN;
+        zacc[r] = 0.0;
+        nvis[r] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) pacc[r][c] = 0.0;
+    }
+    float vmx[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) vmx[c] = 0.0f;
+
+    const double alpha = P.alpha;
+    const double gam = 66.0 * 0x1p-53 * (1.0 + 0x1p-20);
+    const int ntiles = (k1 > k0) ? (int)((k1 - k0 + DT - 1) / DT) : 0;
+
+    u32x4 vr[16];
+    if (ntiles > 0) {
+        issue_k(k0, 0);
+        issue_v(k0, vr);
+    }
+    __syncthreads();  // tables visible
+
+    for (int it = 0; it < ntiles; ++it) {
+        const int buf = it & 1;
+        const int n0 = k0 + it * DT;
+        const bool more = it + 1 < ntiles;
+        const bool nfull = n0 + 2 * DT <= k1;
+        // Issue order: K(it), V(it) (after P(it-1)), K(it+1) (now). Loads complete in order, so
+        // K(it) has landed once at most 16 loads are outstanding (V(it) is 16 instructions, or
+        // K(it+1) is); V(it) once K(it+1) (16 instructions when tile it+1 is full) remains.
+        if (more) issue_k(n0 + DT, buf ^ 1);  // buf^1 was last read by S(it-1)
+        wait_vm<16>();
+        __syncthreads();
+
+        // ---- S: lane = key, fp64 FMA chains (q through the scalar cache)
+        double a0[RB], a1[RB];
+        float km[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < RB; ++r) a0[r] = a1[r] = 0.0;
+        {
+            // q (fp64, prep kernel) comes through the scalar cache in 4-dim halves, two halves
+            // ahead of use, ping-pong between two SGPR sets. The base of the loads for half h+2 is
+            // an opaque zero that consumes both FMA chains after half h: the compiler can neither
+            // hoist all 128 x RB q values (they fit no register file) nor delay one chain and keep
+            // its q values alive. The loads stay ordinary scalar loads (compiler lgkmcnt
+            // accounting intact).
+            double qA[RB][4], qB[RB][4];
+            typedef const double* dptr;
+            dptr qrow[RB];
+#pragma unroll
+            for (int r = 0; r < RB; ++r) qrow[r] = P.q64 + (int64_t)grow[r] * EA_MAXD;
+            // hands out copies of the row pointers that the compiler cannot see through
+            auto gate = [&](dptr (&o)[RB]) __attribute__((always_inline)) {
+                if constexpr (RB == 1) {
+                    asm volatile("s_mov_b64 %0, %1" : "=&s"(o[0]) : "s"(qrow[0]), "v"(a0[0]), "v"(a1[0]));
+                } else if constexpr (RB == 2) {
+                    asm volatile("s_mov_b64 %0, %2\n\ts_mov_b64 %1, %3"
+                                 : "=&s"(o[0]), "=&s"(o[1])
+                                 : "s"(qrow[0]), "s"(qrow[1]), "v"(a0[0]), "v"(a1[0]), "v"(a0[1]), "v"(a1[1]));
+                } else {
+                    asm volatile("s_mov_b64 %0, %4\n\ts_mov_b64 %1, %5\n\ts_mov_b64 %2, %6\n\ts_mov_b64 %3, %7"
+                                 : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
+                                 : "s"(qrow[0]), "s"(qrow[1]), "s"(qrow[2]), "s"(qrow[3]), "v"(a0[0]), "v"(a1[0]),
+                                   "v"(a0[1]), "v"(a1[1]), "v"(a0[2]), "v"(a1[2]), "v"(a0[3]), "v"(a1[3]));
+                }
+            };
+            auto qload = [&](int h, double (&qv)[RB][4]) __attribute__((always_inline)) {
+                dptr o[RB];
+                gate(o);
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    cdouble_t* q4 = (cdouble_t*)o[r];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qv[r][i] = q4[4 * h + i];
+                }
+            };
+            qload(0, qA);
+            qload(1, qB);
+            double kf[8];
+            auto half = [&](int h, double (&qc)[RB][4]) __attribute__((always_inline)) {
+                __builtin_amdgcn_sched_barrier(0);
+                const int c = h >> 1;
+                if ((h & 1) == 0) {
+                    const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
+                    const uint32_t kd[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float lo = __uint_as_float(kd[j] << 16), hi = __uint_as_float(kd[j] & 0xFFFF0000u);
+                        km[c >> 2] = fmaxf(fmaxf(km[c >> 2], absf(lo)), absf(hi));
+                        kf[2 * j] = (double)lo;
+                        kf[2 * j + 1] = (double)hi;
+                    }
+                }
+                const int o = 4 * (h & 1);
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    a0[r] = __fma_rn(qc[r][0], kf[o + 0], a0[r]);
+                    a1[r] = __fma_rn(qc[r][1], kf[o + 1], a1[r]);
+                    a0[r] = __fma_rn(qc[r][2], kf[o + 2], a0[r]);
+                    a1[r] = __fma_rn(qc[r][3], kf[o + 3], a1[r]);
+                }
+                if (h + 2 < 32) qload(h + 2, qc);
+            };
+#pragma unroll
+            for (int h = 0; h < 32; h += 2) {
+                half(h, qA);
+                half(h + 1, qB);
+            }
+        }
+
+        // ---- B: lane = key, every row
+        __builtin_amdgcn_sched_barrier(0);
+        const int n = n0 + lane;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int ti = n - tb;
+            const bool vis = (n < k1) && (n < kvl[r] || (ti >= 0 && ti < 64 && ((tmk[r] >> ti) & 1)));
+            double s = a0[r] + a1[r];
+            const double bnd = __fma_rn(qn4[grow[r] * 4 + 0], (double)km[0],
+                                __fma_rn(qn4[grow[r] * 4 + 1], (double)km[1],
+                                __fma_rn(qn4[grow[r] * 4 + 2], (double)km[2], qn4[grow[r] * 4 + 3] * (double)km[3])));
+            double del = gam * bnd * (1.0 + 0x1p-40) + 0x1p-1060;
+            int32_t M = 1 << 23, E = -23;
+            int why = 0;  // 1 score not certified, 2 weight not certified, 3 weight out of range
+            bool slow = false;
+            if (vis && !rflag[r]) {
+                uint32_t tbits = 0;
+                int ls = isfinite(s) ? logit_cert(alpha, s, 0.0, del, &tbits) : 3;
+                if (ls == 3 && isfinite(s)) {
+                    // exact path: every product separately, TwoSum-accumulated
+                    slow = true;
+                    cdouble_t* qr = (cdouble_t*)P.q64 + (int64_t)grow[r] * EA_MAXD;
+                    double ss = 0.0, es = 0.0, ea = 0.0;
+                    for (int c = 0; c < 16; ++c) {
+                        const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
+                        const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            double e0, e1;
+                            ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
+                            ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
+                            es += e0 + e1;
+                            ea += fabs(e0) + fabs(e1);
+                        }
+                    }
+                    ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1 : logit_cert(alpha, ss, es, ea * 0x1p-44, &tbits);
+                }
+                if (ls == 2 || ls == 3) {
+                    why = 1;
+                } else if (ls == 0) {
+                    int ws = weight_f64(tbits, S.T1, S.T2, &M, &E);
+                    if (ws) {
+                        int32_t M2 = 0;
+                        int64_t E2 = 0;
+                        if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
+                            M = M2;
+                            E = (int32_t)E2;
+                        } else {
+                            why = 2;
+                        }
+                    }
+                }
+            }
+            if (P.stats) {
+                const uint64_t b1 = __ballot(why == 1), b2 = __ballot(why == 2), b3 = __ballot(slow);
+                if (lane == 0 && b1) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)__popcll(b1));
+                if (lane == 0 && b2) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)__popcll(b2));
+                if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
+            }
+            const bool live = vis && why == 0;
+            const int tmax = wave_max_dpp(live ? E + 23 : INT_MIN);
+            const int Rnew = max(Rrun[r], tmax);
+            const bool far = live && (E - Rnew < -1000);
+            if (__ballot(why != 0 || far)) rflag[r] = 1;
+            if (Rrun[r] != INT_MIN && Rnew != Rrun[r]) {
+                const int dsh = Rrun[r] - Rnew;
+                if (dsh < -900) rflag[r] = 1;
+                const double f = ldexp(1.0, max(dsh, -1000));
+                zacc[r] *= f;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) pacc[r][c] *= f;
+            }
+            Rrun[r] = Rnew;
+            double om = (live && !far) ? ldexp((double)M, E - Rnew) : 0.0;
+            if (rflag[r]) om = 0.0;
+            zacc[r] += om;
+            nvis[r] += vis ? 1 : 0;
+            S.w[lane][r] = om;
+        }
+        __syncthreads();  // weights visible to the P roles
+
+        // ---- P: lane = (key group g, channels 8 c8 .. 8 c8 + 7)
+        if (more && nfull) wait_vm<16>();  // V(it) landed; K(it+1) may stay in flight
+        else wait_vm<0>();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (j % 2 == 0) __builtin_amdgcn_sched_barrier(0);
+            const int kk = 4 * j + g;
+            double om[RB];
+#pragma unroll
+            for (int r = 0; r < RB; ++r) om[r] = S.w[kk][r];
+            const uint32_t vd[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float lo = __uint_as_float(vd[q] << 16), hi = __uint_as_float(vd[q] & 0xFFFF0000u);
+                vmx[2 * q] = fmaxf(vmx[2 * q], absf(lo));
+                vmx[2 * q + 1] = fmaxf(vmx[2 * q + 1], absf(hi));
+                const double dlo = (double)lo, dhi = (double)hi;
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    pacc[r][2 * q] = __fma_rn(om[r], dlo, pacc[r][2 * q]);
+                    pacc[r][2 * q + 1] = __fma_rn(om[r], dhi, pacc[r][2 * q + 1]);
+                }
+            }
+        }
+        if (more) issue_v(n0 + DT, vr);  // V(it+1) into the registers P(it) just consumed
+        __syncthreads();                  // S.w and the K buffer are free for the next tile
+    }
+
+    // ---- epilogue: reduce the 4 key groups, write the split partial
+    double* red = reinterpret_cast<double*>(&S.K[0][0]);  // [g][r][128]: 4 * RB KB <= 16 KB
+    float* vred = reinterpret_cast<float*>(&S.K[1][0]);   // [g][128]
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) red[(g * RB + r) * 128 + 8 * c8 + c] = pacc[r][c];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) vred[g * 128 + 8 * c8 + c] = vmx[c];
+    double zs[RB];
+    int ns[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        zs[r] = wave_sum(zacc[r]);
+        ns[r] = wave_sum_i(nvis[r]);
+    }
+    __syncthreads();
+    for (int x = lane; x < nrow * 128; x += 64) {
+        const int r = x >> 7, c = x & 127;
+        double s = red[(0 * RB + r) * 128 + c] + red[(1 * RB + r) * 128 + c];
+        s += red[(2 * RB + r) * 128 + c] + red[(3 * RB + r) * 128 + c];
+        int64_t gr = 0;
+#pragma unroll
+        for (int rr = 0; rr < RB; ++rr)
+            if (rr == r) gr = grow[rr];
+        P.pN[(pbase + gr) * 128 + c] = s;
+    }
+    for (int c = lane; c < 128; c += 64) {
+        float m = fmaxf(fmaxf(vred[c], vred[128 + c]), fmaxf(vred[256 + c], vred[384 + c]));
+        P.pV[(((int64_t)split * P.nseg + seg) * P.nrb + rbk) * 128 + c] = m;
+    }
+    if (lane == 0) {
+        if (P.stats && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)nrow);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            if (r < nrow) {
+                const int64_t o = pbase + grow[r];
+                P.pR[o] = Rrun[r];
+                P.pZ[o] = zs[r];
+                P.pn[o] = rflag[r] ? -1 : ns[r];
+            }
+        }
+    }
+}
+
+// Launches the decode kernel when the geometry allows it; returns 1 if launched, 0 if the caller
+// must use the general split kernel, or a negative HIP error code.
+namespace {
+template <int RB>
+const void* decode_fn(int pgl) {
+    if (pgl == 4) return (const void*)ea_decode<RB, 4>;
+    if (pgl == 16) return (const void*)ea_decode<RB, 16>;
+    return (const void*)ea_decode<RB, 64>;
+}
+}  // namespace
+
+int ea::ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st) {
+    const ea_geometry& g = P.g;
+    if (g.head_dim != 128 || g.head_dim_v != 128) return 0;
+    if (P.bt && P.pshift < 2) return 0;
+    if (rb != 1 && rb != 2 && rb != 4) return 0;
+    // 16-byte alignment of every K/V row start (dwordx4 loads)
+    if (((uintptr_t)P.k | (uintptr_t)P.v) & 15) return 0;
+    if ((g.k_page_stride | g.k_slot_stride | g.k_head_stride | g.v_page_stride | g.v_slot_stride | g.v_head_stride) & 7)
+        return 0;
+    // 31-bit key positions, rows and slot byte offsets (the kernel's scalar arithmetic)
+    const int64_t lim = (int64_t)1 << 30;
+    const int64_t slots = P.bt ? ((int64_t)1 << P.pshift) : (int64_t)g.max_seq_len + 64;
+    if (P.rows >= lim || (int64_t)g.max_seq_len + 64 >= lim) return 0;
+    if (slots * 2 * g.k_slot_stride >= lim || slots * 2 * g.v_slot_stride >= lim) return 0;
+    // page lookups every PGL keys, PGL <= page size (one lookup per 64-key tile without a table)
+    const int pgl = !P.bt ? 64 : (P.pshift >= 6 ? 64 : (P.pshift >= 4 ? 16 : 4));
+    const void* fn = rb == 1 ? decode_fn<1>(pgl) : (rb == 2 ? decode_fn<2>(pgl) : decode_fn<4>(pgl));
+    static std::mutex mu;
+    static bool attr_done = false;
+    static hipError_t attr_err = hipSuccess;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        if (!attr_done) {
+            const void* fns[9] = {decode_fn<1>(4), decode_fn<1>(16), decode_fn<1>(64), decode_fn<2>(4), decode_fn<2>(16),
+                                  decode_fn<2>(64), decode_fn<4>(4), decode_fn<4>(16), decode_fn<4>(64)};
+            for (const void* f : fns) {
+                hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem));
+                if (e != hipSuccess) attr_err = e;
+            }
+            attr_done = true;
+        }
+    }
+    if (attr_err != hipSuccess) return -100 - (int)attr_err;
+    Params Pc = P;
+    void* args[] = {&Pc};
+    hipError_t e = hipLaunchKernel(fn, grid, dim3(64), args, sizeof(DecodeSmem), st);
+    return e == hipSuccess ? 1 : -100 - (int)e;
+}

@@ -13,6 +13,7 @@
 // host fallback) and docs/SPEC.md (the definition the bits must equal).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -20,138 +21,9 @@
 
 #include "../../include/exactattn_hip.h"
 #include "ea_device.h"
+#include "ea_params.h"
 
 using namespace ea;
-
-#define EA_TILE 64
-#define EA_THREADS 256
-#define EA_MAXRB 4
-#define EA_MAXD 128
-#define EA_MAXDV 128
-#define EA_T2_BLOCKS 32
-
-// ------------------------------------------------------------------------------------------------
-// Kernel parameters
-// ------------------------------------------------------------------------------------------------
-struct Params {
-    ea_geometry g;
-    const uint16_t* q;
-    const uint16_t* k;
-    const uint16_t* v;
-    const int32_t* seq_len;
-    const int32_t* kv_len;
-    const int32_t* bt;
-    const int64_t* bt_off;
-    const uint64_t* tree_mask;
-    const int32_t* tree_base;
-    void* out;
-    uint8_t* flags;
-    int64_t* stats;
-    int64_t* timers;
-    const int32_t* merge_order;
-    double alpha;
-    int32_t am, ae;
-    int32_t out_fp32;
-    int32_t nsplit, split_len;
-    int32_t grp, r_seg, rb, nrb, nseg;
-    int32_t pshift;
-    int32_t dlog;
-    int64_t rows;
-    // workspace
-    double* q64;      // rows * EA_MAXD
-    int32_t* qinfo;   // rows * 5: per 32-dim block (FQmax << 16) | FQmin', then a NaN/inf flag
-    int32_t* pR;      // nsplit * rows
-    int32_t* pn;      // nsplit * rows (visible keys, or -1 for a tier-1 flag)
-    double* pZ;       // nsplit * rows
-    double* pN;       // nsplit * rows * dv
-    float* pV;        // nsplit * nseg * nrb * dv : max |v| per channel over the block's keys
-    int32_t* wl;      // rows
-    int32_t* wl_cnt;  // 1
-    int32_t* t2M;     // EA_T2_BLOCKS * max_keys
-    int64_t* t2E;     // EA_T2_BLOCKS * max_keys
-    int32_t t2_keys;
-};
-
-__device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
-    return (b * P.g.num_tokens + t) * P.g.num_q_heads + hq;
-}
-
-// global element offset of key n of sequence b, kv head hk (K when isv = 0, V when 1)
-__device__ __forceinline__ int64_t kv_off(const Params& P, int64_t b, int64_t n, int hk, int isv) {
-    int64_t page, slot;
-    if (P.bt) {
-        int64_t off = P.bt_off ? P.bt_off[b] : b * (int64_t)P.g.block_table_stride;
-        page = P.bt[off + (n >> P.pshift)];
-        slot = n & ((1 << P.pshift) - 1);
-    } else {
-        page = b;
-        slot = n;
-    }
-    if (isv) return page * P.g.v_page_stride + slot * P.g.v_slot_stride + (int64_t)hk * P.g.v_head_stride;
-    return page * P.g.k_page_stride + slot * P.g.k_slot_stride + (int64_t)hk * P.g.k_head_stride;
-}
-
-__device__ __forceinline__ bool visible(const Params& P, int64_t tok, int64_t b, int64_t n) {
-    if (n < P.kv_len[tok]) return true;
-    if (P.tree_mask) {
-        int64_t i = n - P.tree_base[b];
-        if (i >= 0 && i < 64) return (P.tree_mask[tok] >> i) & 1;
-    }
-    return false;
-}
-
-// end of the visible key range of a query token
-__device__ __forceinline__ int64_t vis_end(const Params& P, int64_t tok, int64_t b) {
-    int64_t e = P.kv_len[tok];
-    if (P.tree_mask) {
-        uint64_t m = P.tree_mask[tok];
-        if (m) {
-            int64_t te = P.tree_base[b] + 64 - __clzll(m);
-            if (te > e) e = te;
-        }
-    }
-    return e;
-}
-
-// Max over the 64 lanes with DPP row shifts and row broadcasts (no LDS round trip); every lane
-// receives the result. gfx9 DPP controls: row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
-// row_bcast:31 = 0x143; lanes without a source keep their own value (the max identity here).
-__device__ __forceinline__ int wave_max_dpp(int x) {
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xA, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xC, 0xF, false));
-    return __builtin_amdgcn_readlane(x, 63);
-}
-
-// Max within each 16-lane DPP row (lanes 16r .. 16r+15); every lane of the row receives it.
-__device__ __forceinline__ int row16_max(int x) {
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false));
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0xF, false));
-    // lane 15 of each row now holds the row's max: broadcast it within the row
-    return __shfl(x, (threadIdx.x & 48) | 15, 64);
-}
-
-__device__ __forceinline__ double wave_sum(double x) {
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
-__device__ __forceinline__ int wave_max_i(int x) {
-    for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o, 64));
-    return x;
-}
-__device__ __forceinline__ int wave_min_i(int x) {
-    for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o, 64));
-    return x;
-}
-__device__ __forceinline__ int wave_sum_i(int x) {
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
 
 // ------------------------------------------------------------------------------------------------
 // Kernel 1: q rows to fp64 plus per-32-dim-block exponent ranges. One wave per row.
@@ -172,9 +44,12 @@ __global__ void __launch_bounds__(256) ea_prep(Params P) {
     for (int blk = 0; blk < 4; ++blk) {
         int i = blk * 32 + (lane & 31);
         int fmax = 0, fmin = 0x1FF;
+        double aq = 0.0;
         if (lane < 32 && i < d) {
             uint32_t x = qr[i];
-            P.q64[row * EA_MAXD + i] = (double)__uint_as_float(x << 16);
+            double qv = (double)__uint_as_float(x << 16);
+            P.q64[row * EA_MAXD + i] = qv;
+            aq = fabs(qv);
             int f = (x >> 7) & 0xFF;
             if (f == 0xFF) bad = 1;
             if (x & 0x7FFF) {
@@ -186,7 +61,13 @@ __global__ void __launch_bounds__(256) ea_prep(Params P) {
         }
         fmax = wave_max_i(fmax);
         fmin = wave_min_i(fmin);
-        if (lane == 0) P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
+        // sum |q_i| over the block: <= 32 roundings of relative size 2^-53 each, so scaling the
+        // fp64 sum by (1 + 2^-40) gives an upper bound (NaN/inf propagate; the row is flagged)
+        aq = wave_sum(aq);
+        if (lane == 0) {
+            P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
+            P.qn[row * 4 + blk] = aq * (1.0 + 0x1p-40);
+        }
     }
     bad = wave_max_i(bad);
     if (lane == 0) P.qinfo[row * 5 + 4] = bad;
@@ -223,9 +104,6 @@ struct SplitSmem {
     int32_t wn[4][EA_MAXRB];
     uint32_t vred[4][64];                // 1 KB
 };
-
-typedef const double __attribute__((address_space(4))) cdouble_t;
-typedef const int32_t __attribute__((address_space(4))) cint_t;
 
 template <int RB, bool TIMERS>
 __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
@@ -1103,7 +981,7 @@ namespace {
 struct Plan {
     int nsplit, split_len, rb, nrb, r_seg, grp, nseg, pshift, dlog;
     int64_t rows;
-    size_t off_q64, off_qinfo, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
+    size_t off_q64, off_qinfo, off_qn, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
     int t2_keys;
 };
 
@@ -1149,6 +1027,7 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     size_t off = 0;
     pl->off_q64 = off; off = align_up(off + (size_t)R * EA_MAXD * 8);
     pl->off_qinfo = off; off = align_up(off + (size_t)R * 5 * 4);
+    pl->off_qn = off; off = align_up(off + (size_t)R * 4 * 8);
     pl->off_pR = off; off = align_up(off + (size_t)pl->nsplit * R * 4);
     pl->off_pn = off; off = align_up(off + (size_t)pl->nsplit * R * 4);
     pl->off_pZ = off; off = align_up(off + (size_t)pl->nsplit * R * 8);
@@ -1216,6 +1095,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     char* ws = (char*)workspace;
     P.q64 = (double*)(ws + pl.off_q64);
     P.qinfo = (int32_t*)(ws + pl.off_qinfo);
+    P.qn = (double*)(ws + pl.off_qn);
     P.pR = (int32_t*)(ws + pl.off_pR);
     P.pn = (int32_t*)(ws + pl.off_pn);
     P.pZ = (double*)(ws + pl.off_pZ);
@@ -1254,7 +1134,13 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         if ((rc = mark(1))) return rc;
         const dim3 blk(EA_THREADS);
         const size_t lds = sizeof(SplitSmem);
-        if (o->timers) {
+        int dec = 0;
+        if (!o->timers && !getenv("EA_FORCE_GENERAL")) {
+            dec = ea_launch_decode(P, pl.rb, grid, st);
+            if (dec < 0) return dec;
+        }
+        if (dec) {
+        } else if (o->timers) {
             if (pl.rb == 1) hipLaunchKernelGGL((ea_split<1, true>), grid, blk, lds, st, P);
             else if (pl.rb == 2) hipLaunchKernelGGL((ea_split<2, true>), grid, blk, lds, st, P);
             else hipLaunchKernelGGL((ea_split<4, true>), grid, blk, lds, st, P);

@@ -1,0 +1,150 @@
+// Shared kernel parameters and wave-level helpers of the certified attention kernels (gfx950).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/exactattn_hip.h"
+#include "ea_device.h"
+
+namespace ea {
+
+#define EA_TILE 64
+#define EA_THREADS 256
+#define EA_MAXRB 4
+#define EA_MAXD 128
+#define EA_MAXDV 128
+#define EA_T2_BLOCKS 32
+
+// ------------------------------------------------------------------------------------------------
+// Kernel parameters
+// ------------------------------------------------------------------------------------------------
+struct Params {
+    ea_geometry g;
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const int32_t* seq_len;
+    const int32_t* kv_len;
+    const int32_t* bt;
+    const int64_t* bt_off;
+    const uint64_t* tree_mask;
+    const int32_t* tree_base;
+    void* out;
+    uint8_t* flags;
+    int64_t* stats;
+    int64_t* timers;
+    const int32_t* merge_order;
+    double alpha;
+    int32_t am, ae;
+    int32_t out_fp32;
+    int32_t nsplit, split_len;
+    int32_t grp, r_seg, rb, nrb, nseg;
+    int32_t pshift;
+    int32_t dlog;
+    int64_t rows;
+    // workspace
+    double* q64;      // rows * EA_MAXD
+    int32_t* qinfo;   // rows * 5: per 32-dim block (FQmax << 16) | FQmin', then a NaN/inf flag
+    double* qn;       // rows * 4: per 32-dim block an upper bound of sum |q_i| (fp64)
+    int32_t* pR;      // nsplit * rows
+    int32_t* pn;      // nsplit * rows (visible keys, or -1 for a tier-1 flag)
+    double* pZ;       // nsplit * rows
+    double* pN;       // nsplit * rows * dv
+    float* pV;        // nsplit * nseg * nrb * dv : max |v| per channel over the block's keys
+    int32_t* wl;      // rows
+    int32_t* wl_cnt;  // 1
+    int32_t* t2M;     // EA_T2_BLOCKS * max_keys
+    int64_t* t2E;     // EA_T2_BLOCKS * max_keys
+    int32_t t2_keys;
+};
+
+__device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
+    return (b * P.g.num_tokens + t) * P.g.num_q_heads + hq;
+}
+
+// global element offset of key n of sequence b, kv head hk (K when isv = 0, V when 1)
+__device__ __forceinline__ int64_t kv_off(const Params& P, int64_t b, int64_t n, int hk, int isv) {
+    int64_t page, slot;
+    if (P.bt) {
+        int64_t off = P.bt_off ? P.bt_off[b] : b * (int64_t)P.g.block_table_stride;
+        page = P.bt[off + (n >> P.pshift)];
+        slot = n & ((1 << P.pshift) - 1);
+    } else {
+        page = b;
+        slot = n;
+    }
+    if (isv) return page * P.g.v_page_stride + slot * P.g.v_slot_stride + (int64_t)hk * P.g.v_head_stride;
+    return page * P.g.k_page_stride + slot * P.g.k_slot_stride + (int64_t)hk * P.g.k_head_stride;
+}
+
+__device__ __forceinline__ bool visible(const Params& P, int64_t tok, int64_t b, int64_t n) {
+    if (n < P.kv_len[tok]) return true;
+    if (P.tree_mask) {
+        int64_t i = n - P.tree_base[b];
+        if (i >= 0 && i < 64) return (P.tree_mask[tok] >> i) & 1;
+    }
+    return false;
+}
+
+// end of the visible key range of a query token
+__device__ __forceinline__ int64_t vis_end(const Params& P, int64_t tok, int64_t b) {
+    int64_t e = P.kv_len[tok];
+    if (P.tree_mask) {
+        uint64_t m = P.tree_mask[tok];
+        if (m) {
+            int64_t te = P.tree_base[b] + 64 - __clzll(m);
+            if (te > e) e = te;
+        }
+    }
+    return e;
+}
+
+// Max over the 64 lanes with DPP row shifts and row broadcasts (no LDS round trip); every lane
+// receives the result. gfx9 DPP controls: row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143; lanes without a source keep their own value (the max identity here).
+__device__ __forceinline__ int wave_max_dpp(int x) {
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xA, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xC, 0xF, false));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Max within each 16-lane DPP row (lanes 16r .. 16r+15); every lane of the row receives it.
+__device__ __forceinline__ int row16_max(int x) {
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0xF, false));
+    // lane 15 of each row now holds the row's max: broadcast it within the row
+    return __shfl(x, (threadIdx.x & 48) | 15, 64);
+}
+
+__device__ __forceinline__ double wave_sum(double x) {
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+    for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_min_i(int x) {
+    for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_sum_i(int x) {
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+
+// Launches the d = dv = 128 decode kernel (ea_decode.hip) when the geometry allows it: returns 1
+// when launched, 0 when the caller must run the general split kernel, -100 - e on a HIP error.
+int ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st);
+
+typedef const double __attribute__((address_space(4))) cdouble_t;
+typedef const int32_t __attribute__((address_space(4))) cint_t;
+
+}  // namespace ea

@@ -264,3 +264,68 @@ def test_fixture_sha256(gpu):
         got, flags, st = _run(prob, ab, splits=8)
         assert not np.any(flags), st
         assert hashlib.sha256(got.reshape(L, -1).tobytes()).hexdigest() == info["sha256"], key
+
+
+# ---------------------------------------------------------------------------------------------
+# the d = 128 decode kernel (one wave per segment row block and split)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("vkind", ["normal", "wide", "dupes"])
+def test_decode_kernel_kinds_match_oracle(gpu, kind, vkind):
+    rng = np.random.default_rng(hash(("dec", kind, vkind)) % (1 << 32))
+    prob = _rand_problem(rng, kind, vkind, B=2, T=1, Hq=4, Hkv=2, S=300, d=128, dv=128, causal=False)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    for splits in (1, 3):
+        got, flags, st = _run(prob, ab, splits=splits)
+        assert st["decode_kernel_rows"] == prob["q"].shape[0] * prob["q"].shape[2], st
+        assert not np.any(flags == 1), (splits, flags, st)
+        assert np.array_equal(got, want), (splits, st)
+
+
+@pytest.mark.parametrize("hq,hkv,T", [(4, 4, 1), (8, 2, 1), (4, 2, 2), (2, 1, 3), (16, 8, 1)])
+@pytest.mark.parametrize("ps", [0, 4, 16, 64])
+def test_decode_kernel_shapes_pages_ragged(gpu, hq, hkv, T, ps):
+    """Row blocks of 1, 2 and 4 rows (and a partial one), contiguous and paged caches of page
+    size 4, 16 and 64 (NHD), sequence lengths around the 64-key tile edges."""
+    rng = np.random.default_rng(1000 * hq + 100 * hkv + 10 * T + ps)
+    B, d = 6, 128
+    seq = np.array([1, 63, 64, 65, 129, 200])
+    q = bf16(rng, (B, T, hq, d))
+    k = bf16(rng, (B, hkv, 200, d))
+    v = bf16(rng, (B, hkv, 200, d))
+    kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 1, None) for b in range(B)])
+    prob = problem.contiguous(q, k, v, kv, seq_len=seq)
+    if ps:
+        prob = problem.to_paged(prob, ps, np.random.default_rng(ps), "NHD")
+    ab = default_alpha_bits(d)
+    want, _ = _oracle(prob, ab)
+    for splits in (1, 2):
+        got, flags, st = _run(prob, ab, splits=splits)
+        assert st["decode_kernel_rows"] > 0, st
+        assert not np.any(flags), (splits, st)
+        assert np.array_equal(got, want), (splits, st)
+
+
+def test_decode_kernel_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
+    rng = np.random.default_rng(44)
+    prob = _rand_problem(rng, "normal", "normal", B=1, T=8, Hq=2, Hkv=1, S=200, d=128, dv=128)
+    prob["seq_len"][:] = 200
+    prob["kv_len"][:] = 125 + 10 * np.arange(8)
+    prob["k"][0, 0, 140, 3] = 0x7FC0   # NaN key at position 140
+    prob["v"][0, 0, 162, 100] = 0xFF80  # -inf value at position 162
+    ab = default_alpha_bits(128)
+    got, flags, st = _run(prob, ab)
+    assert st["decode_kernel_rows"] > 0, st
+    kvl = prob["kv_len"]
+    clean = {**prob, "k": prob["k"].copy(), "v": prob["v"].copy()}
+    clean["k"][0, 0, 140, 3] = 0
+    clean["v"][0, 0, 162, 100] = 0
+    want, _ = _oracle(clean, ab)  # rows that do not see the non-finite keys are unaffected
+    for t in range(8):
+        for h in range(2):
+            r = t * 2 + h
+            assert flags[r] == (2 if kvl[t] > 140 else 0), (t, h, flags)
+            if kvl[t] <= 140:
+                assert np.array_equal(got[0, t, h], want[0, t, h]), (t, h)
