@@ -33,9 +33,11 @@ namespace {
 
 constexpr int DT = 64;  // keys per tile = lanes
 
+template <int RB>
 struct DecodeSmem {
-    uint4 K[2][DT * 16];   // 2 x 16 KB; reused by the epilogue reduction
-    double w[DT][4];       // weights of the tile, [key][row]
+    uint4 K[2][DT * 16];   // 2 x 16 KB K tiles; reused by the epilogue reduction
+    double w[2][DT][RB];   // weights of a tile, [key][row], double-buffered between the waves
+    double sc[2][RB];      // per-row rescale of the running P.V sums before that tile
     double T1[256], T2[256];
 };
 
@@ -55,10 +57,10 @@ __device__ __forceinline__ float absf(float x) { return __builtin_fabsf(x); }
 }  // namespace
 
 template <int RB, int PGL>
-__global__ void __launch_bounds__(64) ea_decode(Params P) {
+__global__ void __launch_bounds__(128) ea_decode(Params P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    DecodeSmem& S = *reinterpret_cast<DecodeSmem*>(smem_raw);
-    const int lane = threadIdx.x;
+    DecodeSmem<RB>& S = *reinterpret_cast<DecodeSmem<RB>*>(smem_raw);
+    const int lane = threadIdx.x & 63;
     const int g = lane >> 4, c8 = lane & 15;
 
     const int item = blockIdx.x;
@@ -70,7 +72,7 @@ __global__ void __launch_bounds__(64) ea_decode(Params P) {
     const int row0 = rbk * P.rb;
     const int nrow = min(RB, P.r_seg - row0);
 
-    for (int i = lane; i < 256; i += 64) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
         S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
         S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
     }
@@ -123,316 +125,363 @@ __global__ void __launch_bounds__(64) ea_decode(Params P) {
     // Group j of the tile at n0 holds keys n0+4j .. n0+4j+3, all in one page (page size >= 4 and
     // n0 % 64 == 0). Pages are looked up every PGL keys (PGL <= page size, or the whole
     // sequence without a block table); inside a lookup interval the slot advances by 4 keys per
-    // group. `page_rs` returns the buffer resource at the page start and the slot of key n.
+    // group. Lanes whose key is at or past k1 get the offset EA_OOB: the buffer unit's range
+    // check (offset >= num_records) returns zeros without a memory access, so every tile issues
+    // exactly 16 K and 16 V instructions with no branches. Lookup indices are clamped to k1 - 1
+    // so the block table is never read past the sequence.
+    constexpr int EA_OOB = (int)0x80000000u;
     auto page_rs = [&](int n, const char* head, int64_t ps2, int* slot) __attribute__((always_inline)) {
         int64_t pg;
+        const int nc = min(n, k1 - 1);
         if (P.bt) {
-            pg = btb[n >> pshift];
+            pg = btb[nc >> pshift];
             *slot = n & pmask;
         } else {
             pg = b;
             *slot = n;
         }
-        return __builtin_amdgcn_make_buffer_rsrc((void*)(head + pg * ps2), (short)0, -1, 0x00020000);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(head + pg * ps2), (short)0, 0x7FFFFFFF, 0x00020000);
     };
-    // K tile at n0 -> LDS buffer `buf`: instruction j writes the 1 KB of keys 4j..4j+3; lanes whose
-    // key is past k1 re-read their group's first key into slots no row looks at.
+    // K tile at n0 -> LDS buffer `buf`: instruction j writes the 1 KB of keys 4j..4j+3
     auto issue_k = [&](int n0, int buf) __attribute__((always_inline)) {
         __amdgpu_buffer_rsrc_t rs;
         int slot = 0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int nj = n0 + 4 * j;
-            if (nj < k1) {
-                if ((4 * j) % PGL == 0) rs = page_rs(nj, kh, kps2, &slot);
-                const int sl = slot + (4 * j) % PGL;
-                const int off = (nj + g < k1) ? koff[j & 3] : koff[j & 3] - g * kss2;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)&S.K[buf][j * 64], 16, off, sl * kss2, 0, 2);
-            }
+            if ((4 * j) % PGL == 0) rs = page_rs(nj, kh, kps2, &slot);
+            const int sl = slot + (4 * j) % PGL;
+            const int off = (nj + g < k1) ? koff[j & 3] : EA_OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)&S.K[buf][j * 64], 16, off, sl * kss2, 0, 2);
         }
     };
-    auto issue_v = [&](int n0, u32x4 (&vr)[16]) __attribute__((always_inline)) {
+    auto issue_v = [&](int n0, u32x4 (&vr)[16], double d0, double d1) __attribute__((always_inline)) {
         __amdgpu_buffer_rsrc_t rs;
         int slot = 0;
+        int vo = voff;
+        asm volatile("" : "+v"(vo) : "v"(d0), "v"(d1));
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int nj = n0 + 4 * j;
-            u32x4 x = {0, 0, 0, 0};
-            if (nj < k1) {
-                if ((4 * j) % PGL == 0) rs = page_rs(nj, vh, vps2, &slot);
-                const int sl = slot + (4 * j) % PGL;
-                if (nj + g < k1) x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, sl * vss2, 2);
-            }
-            vr[j] = x;
+            if ((4 * j) % PGL == 0) rs = page_rs(nj, vh, vps2, &slot);
+            const int sl = slot + (4 * j) % PGL;
+            const int off = (nj + g < k1) ? vo : EA_OOB;
+            vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, sl * vss2, 2);
         }
     };
-
-    // per-row state
-    int Rrun[RB];
-    double zacc[RB];
-    int nvis[RB];
-    double pacc[RB][8];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        Rrun[r] = INT_MIN;
-        zacc[r] = 0.0;
-        nvis[r] = 0;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) pacc[r][c] = 0.0;
-    }
-    float vmx[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) vmx[c] = 0.0f;
 
     const double alpha = P.alpha;
     const double gam = 66.0 * 0x1p-53 * (1.0 + 0x1p-20);
     const int ntiles = (k1 > k0) ? (int)((k1 - k0 + DT - 1) / DT) : 0;
+    // Both roles run ntiles + 1 loop iterations with one barrier each (and the prologue barrier):
+    // iteration it has wave A publish the weights of tile it, wave B consume those of tile it - 1.
+    const int role = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 
-    u32x4 vr[16];
-    if (ntiles > 0) {
-        issue_k(k0, 0);
-        issue_v(k0, vr);
-    }
-    __syncthreads();  // tables visible
-
-    for (int it = 0; it < ntiles; ++it) {
-        const int buf = it & 1;
-        const int n0 = k0 + it * DT;
-        const bool more = it + 1 < ntiles;
-        const bool nfull = n0 + 2 * DT <= k1;
-        // Issue order: K(it), V(it) (after P(it-1)), K(it+1) (now). Loads complete in order, so
-        // K(it) has landed once at most 16 loads are outstanding (V(it) is 16 instructions, or
-        // K(it+1) is); V(it) once K(it+1) (16 instructions when tile it+1 is full) remains.
-        if (more) issue_k(n0 + DT, buf ^ 1);  // buf^1 was last read by S(it-1)
-        wait_vm<16>();
-        __syncthreads();
+    if (role == 0) {
+        // ============ wave A: K tiles, scores, certified logits and weights
+        int Rrun[RB];
+        double zacc[RB];
+        int nvis[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            Rrun[r] = INT_MIN;
+            zacc[r] = 0.0;
+            nvis[r] = 0;
+        }
+        if (ntiles > 0) issue_k(k0, 0);
+        __syncthreads();  // tables visible
+        for (int it = 0; it <= ntiles; ++it) {
+            if (it < ntiles) {
+                const int buf = it & 1;
+                const int n0 = k0 + it * DT;
+                const bool more = it + 1 < ntiles;
+                // K(it+1) into the buffer S(it-1) read; K(it) has landed once only K(it+1)'s 16
+                // instructions may be outstanding
+                if (more) {
+                    issue_k(n0 + DT, buf ^ 1);
+                    wait_vm<16>();
+                } else {
+                    wait_vm<0>();
+                }
 
         // ---- S: lane = key, fp64 FMA chains (q through the scalar cache)
-        double a0[RB], a1[RB];
-        float km[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int r = 0; r < RB; ++r) a0[r] = a1[r] = 0.0;
-        {
-            // q (fp64, prep kernel) comes through the scalar cache in 4-dim halves, two halves
-            // ahead of use, ping-pong between two SGPR sets. The base of the loads for half h+2 is
-            // an opaque zero that consumes both FMA chains after half h: the compiler can neither
-            // hoist all 128 x RB q values (they fit no register file) nor delay one chain and keep
-            // its q values alive. The loads stay ordinary scalar loads (compiler lgkmcnt
-            // accounting intact).
-            double qA[RB][4], qB[RB][4];
-            typedef const double* dptr;
-            dptr qrow[RB];
-#pragma unroll
-            for (int r = 0; r < RB; ++r) qrow[r] = P.q64 + (int64_t)grow[r] * EA_MAXD;
-            // hands out copies of the row pointers that the compiler cannot see through
-            auto gate = [&](dptr (&o)[RB]) __attribute__((always_inline)) {
-                if constexpr (RB == 1) {
-                    asm volatile("s_mov_b64 %0, %1" : "=&s"(o[0]) : "s"(qrow[0]), "v"(a0[0]), "v"(a1[0]));
-                } else if constexpr (RB == 2) {
-                    asm volatile("s_mov_b64 %0, %2\n\ts_mov_b64 %1, %3"
-                                 : "=&s"(o[0]), "=&s"(o[1])
-                                 : "s"(qrow[0]), "s"(qrow[1]), "v"(a0[0]), "v"(a1[0]), "v"(a0[1]), "v"(a1[1]));
-                } else {
-                    asm volatile("s_mov_b64 %0, %4\n\ts_mov_b64 %1, %5\n\ts_mov_b64 %2, %6\n\ts_mov_b64 %3, %7"
-                                 : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
-                                 : "s"(qrow[0]), "s"(qrow[1]), "s"(qrow[2]), "s"(qrow[3]), "v"(a0[0]), "v"(a1[0]),
-                                   "v"(a0[1]), "v"(a1[1]), "v"(a0[2]), "v"(a1[2]), "v"(a0[3]), "v"(a1[3]));
-                }
-            };
-            auto qload = [&](int h, double (&qv)[RB][4]) __attribute__((always_inline)) {
-                dptr o[RB];
-                gate(o);
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    cdouble_t* q4 = (cdouble_t*)o[r];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) qv[r][i] = q4[4 * h + i];
-                }
-            };
-            qload(0, qA);
-            qload(1, qB);
-            double kf[8];
-            auto half = [&](int h, double (&qc)[RB][4]) __attribute__((always_inline)) {
-                __builtin_amdgcn_sched_barrier(0);
-                const int c = h >> 1;
-                if ((h & 1) == 0) {
-                    const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
-                    const uint32_t kd[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float lo = __uint_as_float(kd[j] << 16), hi = __uint_as_float(kd[j] & 0xFFFF0000u);
-                        km[c >> 2] = fmaxf(fmaxf(km[c >> 2], absf(lo)), absf(hi));
-                        kf[2 * j] = (double)lo;
-                        kf[2 * j + 1] = (double)hi;
+            double a0[RB], a1[RB];
+            float km[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+            for (int r = 0; r < RB; ++r) a0[r] = a1[r] = 0.0;
+            {
+                // q (fp64, prep kernel) comes through the scalar cache in 4-dim halves, two halves
+                // ahead of use, ping-pong between two SGPR sets. The base of the loads for half h+2 is
+                // an opaque zero that consumes both FMA chains after half h: the compiler can neither
+                // hoist all 128 x RB q values (they fit no register file) nor delay one chain and keep
+                // its q values alive. The loads stay ordinary scalar loads (compiler lgkmcnt
+                // accounting intact).
+                double qA[RB][4], qB[RB][4];
+                typedef const double* dptr;
+                dptr qrow[RB];
+    #pragma unroll
+                for (int r = 0; r < RB; ++r) qrow[r] = P.q64 + (int64_t)grow[r] * EA_MAXD;
+                // hands out copies of the row pointers that the compiler cannot see through
+                auto gate = [&](dptr (&o)[RB]) __attribute__((always_inline)) {
+                    if constexpr (RB == 1) {
+                        asm volatile("s_mov_b64 %0, %1" : "=&s"(o[0]) : "s"(qrow[0]), "v"(a0[0]), "v"(a1[0]));
+                    } else if constexpr (RB == 2) {
+                        asm volatile("s_mov_b64 %0, %2\n\ts_mov_b64 %1, %3"
+                                     : "=&s"(o[0]), "=&s"(o[1])
+                                     : "s"(qrow[0]), "s"(qrow[1]), "v"(a0[0]), "v"(a1[0]), "v"(a0[1]), "v"(a1[1]));
+                    } else {
+                        asm volatile("s_mov_b64 %0, %4\n\ts_mov_b64 %1, %5\n\ts_mov_b64 %2, %6\n\ts_mov_b64 %3, %7"
+                                     : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
+                                     : "s"(qrow[0]), "s"(qrow[1]), "s"(qrow[2]), "s"(qrow[3]), "v"(a0[0]), "v"(a1[0]),
+                                       "v"(a0[1]), "v"(a1[1]), "v"(a0[2]), "v"(a1[2]), "v"(a0[3]), "v"(a1[3]));
                     }
-                }
-                const int o = 4 * (h & 1);
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    a0[r] = __fma_rn(qc[r][0], kf[o + 0], a0[r]);
-                    a1[r] = __fma_rn(qc[r][1], kf[o + 1], a1[r]);
-                    a0[r] = __fma_rn(qc[r][2], kf[o + 2], a0[r]);
-                    a1[r] = __fma_rn(qc[r][3], kf[o + 3], a1[r]);
-                }
-                if (h + 2 < 32) qload(h + 2, qc);
-            };
-#pragma unroll
-            for (int h = 0; h < 32; h += 2) {
-                half(h, qA);
-                half(h + 1, qB);
-            }
-        }
-
-        // ---- B: lane = key, every row
-        __builtin_amdgcn_sched_barrier(0);
-        const int n = n0 + lane;
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            const int ti = n - tb;
-            const bool vis = (n < k1) && (n < kvl[r] || (ti >= 0 && ti < 64 && ((tmk[r] >> ti) & 1)));
-            double s = a0[r] + a1[r];
-            const double bnd = __fma_rn(qn4[grow[r] * 4 + 0], (double)km[0],
-                                __fma_rn(qn4[grow[r] * 4 + 1], (double)km[1],
-                                __fma_rn(qn4[grow[r] * 4 + 2], (double)km[2], qn4[grow[r] * 4 + 3] * (double)km[3])));
-            double del = gam * bnd * (1.0 + 0x1p-40) + 0x1p-1060;
-            int32_t M = 1 << 23, E = -23;
-            int why = 0;  // 1 score not certified, 2 weight not certified, 3 weight out of range
-            bool slow = false;
-            if (vis && !rflag[r]) {
-                uint32_t tbits = 0;
-                int ls = isfinite(s) ? logit_cert(alpha, s, 0.0, del, &tbits) : 3;
-                if (ls == 3 && isfinite(s)) {
-                    // exact path: every product separately, TwoSum-accumulated
-                    slow = true;
-                    cdouble_t* qr = (cdouble_t*)P.q64 + (int64_t)grow[r] * EA_MAXD;
-                    double ss = 0.0, es = 0.0, ea = 0.0;
-                    for (int c = 0; c < 16; ++c) {
+                };
+                auto qload = [&](int h, double (&qv)[RB][4]) __attribute__((always_inline)) {
+                    dptr o[RB];
+                    gate(o);
+    #pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        cdouble_t* q4 = (cdouble_t*)o[r];
+    #pragma unroll
+                        for (int i = 0; i < 4; ++i) qv[r][i] = q4[4 * h + i];
+                    }
+                };
+                qload(0, qA);
+                qload(1, qB);
+                double kf[8];
+                auto half = [&](int h, double (&qc)[RB][4]) __attribute__((always_inline)) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int c = h >> 1;
+                    if ((h & 1) == 0) {
                         const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
-                        const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
+                        const uint32_t kd[4] = {kv.x, kv.y, kv.z, kv.w};
+    #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            double e0, e1;
-                            ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
-                            ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
-                            es += e0 + e1;
-                            ea += fabs(e0) + fabs(e1);
+                            const float lo = __uint_as_float(kd[j] << 16), hi = __uint_as_float(kd[j] & 0xFFFF0000u);
+                            km[c >> 2] = fmaxf(fmaxf(km[c >> 2], absf(lo)), absf(hi));
+                            kf[2 * j] = (double)lo;
+                            kf[2 * j + 1] = (double)hi;
                         }
                     }
-                    ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1 : logit_cert(alpha, ss, es, ea * 0x1p-44, &tbits);
+                    const int o = 4 * (h & 1);
+    #pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        a0[r] = __fma_rn(qc[r][0], kf[o + 0], a0[r]);
+                        a1[r] = __fma_rn(qc[r][1], kf[o + 1], a1[r]);
+                        a0[r] = __fma_rn(qc[r][2], kf[o + 2], a0[r]);
+                        a1[r] = __fma_rn(qc[r][3], kf[o + 3], a1[r]);
+                    }
+                    if (h + 2 < 32) qload(h + 2, qc);
+                };
+    #pragma unroll
+                for (int h = 0; h < 32; h += 2) {
+                    half(h, qA);
+                    half(h + 1, qB);
                 }
-                if (ls == 2 || ls == 3) {
-                    why = 1;
-                } else if (ls == 0) {
-                    int ws = weight_f64(tbits, S.T1, S.T2, &M, &E);
-                    if (ws) {
-                        int32_t M2 = 0;
-                        int64_t E2 = 0;
-                        if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
-                            M = M2;
-                            E = (int32_t)E2;
-                        } else {
-                            why = 2;
+            }
+
+            // ---- B: lane = key, every row
+            __builtin_amdgcn_sched_barrier(0);
+            const int n = n0 + lane;
+    #pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                __builtin_amdgcn_sched_barrier(0);  // one row at a time (bounded live temporaries)
+                const int ti = n - tb;
+                const bool vis = (n < k1) && (n < kvl[r] || (ti >= 0 && ti < 64 && ((tmk[r] >> ti) & 1)));
+                double s = a0[r] + a1[r];
+                const double bnd = __fma_rn(qn4[grow[r] * 4 + 0], (double)km[0],
+                                    __fma_rn(qn4[grow[r] * 4 + 1], (double)km[1],
+                                    __fma_rn(qn4[grow[r] * 4 + 2], (double)km[2], qn4[grow[r] * 4 + 3] * (double)km[3])));
+                double del = gam * bnd * (1.0 + 0x1p-40) + 0x1p-1060;
+                int32_t M = 1 << 23, E = -23;
+                int why = 0;  // 1 score not certified, 2 weight not certified, 3 weight out of range
+                bool slow = false;
+                if (vis && !rflag[r]) {
+                    uint32_t tbits = 0;
+                    int ls = isfinite(s) ? logit_cert(alpha, s, 0.0, del, &tbits) : 3;
+                    if (ls == 3 && isfinite(s)) {
+                        // exact path: every product separately, TwoSum-accumulated
+                        slow = true;
+                        cdouble_t* qr = (cdouble_t*)P.q64 + (int64_t)grow[r] * EA_MAXD;
+                        double ss = 0.0, es = 0.0, ea = 0.0;
+                        for (int c = 0; c < 16; ++c) {
+                            const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
+                            const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+    #pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                double e0, e1;
+                                ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
+                                ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
+                                es += e0 + e1;
+                                ea += fabs(e0) + fabs(e1);
+                            }
+                        }
+                        ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1 : logit_cert(alpha, ss, es, ea * 0x1p-44, &tbits);
+                    }
+                    if (ls == 2 || ls == 3) {
+                        why = 1;
+                    } else if (ls == 0) {
+                        int ws = weight_f64(tbits, S.T1, S.T2, &M, &E);
+                        if (ws) {
+                            int32_t M2 = 0;
+                            int64_t E2 = 0;
+                            if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
+                                M = M2;
+                                E = (int32_t)E2;
+                            } else {
+                                why = 2;
+                            }
                         }
                     }
                 }
-            }
-            if (P.stats) {
-                const uint64_t b1 = __ballot(why == 1), b2 = __ballot(why == 2), b3 = __ballot(slow);
-                if (lane == 0 && b1) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)__popcll(b1));
-                if (lane == 0 && b2) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)__popcll(b2));
-                if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
-            }
-            const bool live = vis && why == 0;
-            const int tmax = wave_max_dpp(live ? E + 23 : INT_MIN);
-            const int Rnew = max(Rrun[r], tmax);
-            const bool far = live && (E - Rnew < -1000);
-            if (__ballot(why != 0 || far)) rflag[r] = 1;
-            if (Rrun[r] != INT_MIN && Rnew != Rrun[r]) {
-                const int dsh = Rrun[r] - Rnew;
-                if (dsh < -900) rflag[r] = 1;
-                const double f = ldexp(1.0, max(dsh, -1000));
-                zacc[r] *= f;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) pacc[r][c] *= f;
-            }
-            Rrun[r] = Rnew;
-            double om = (live && !far) ? ldexp((double)M, E - Rnew) : 0.0;
-            if (rflag[r]) om = 0.0;
-            zacc[r] += om;
-            nvis[r] += vis ? 1 : 0;
-            S.w[lane][r] = om;
-        }
-        __syncthreads();  // weights visible to the P roles
-
-        // ---- P: lane = (key group g, channels 8 c8 .. 8 c8 + 7)
-        if (more && nfull) wait_vm<16>();  // V(it) landed; K(it+1) may stay in flight
-        else wait_vm<0>();
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (j % 2 == 0) __builtin_amdgcn_sched_barrier(0);
-            const int kk = 4 * j + g;
-            double om[RB];
-#pragma unroll
-            for (int r = 0; r < RB; ++r) om[r] = S.w[kk][r];
-            const uint32_t vd[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float lo = __uint_as_float(vd[q] << 16), hi = __uint_as_float(vd[q] & 0xFFFF0000u);
-                vmx[2 * q] = fmaxf(vmx[2 * q], absf(lo));
-                vmx[2 * q + 1] = fmaxf(vmx[2 * q + 1], absf(hi));
-                const double dlo = (double)lo, dhi = (double)hi;
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    pacc[r][2 * q] = __fma_rn(om[r], dlo, pacc[r][2 * q]);
-                    pacc[r][2 * q + 1] = __fma_rn(om[r], dhi, pacc[r][2 * q + 1]);
+                if (P.stats) {
+                    const uint64_t b1 = __ballot(why == 1), b2 = __ballot(why == 2), b3 = __ballot(slow);
+                    if (lane == 0 && b1) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)__popcll(b1));
+                    if (lane == 0 && b2) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)__popcll(b2));
+                    if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
                 }
+                const bool live = vis && why == 0;
+                const int tmax = wave_max_dpp(live ? E + 23 : INT_MIN);
+                const int Rnew = max(Rrun[r], tmax);
+                const bool far = live && (E - Rnew < -1000);
+                if (__ballot(why != 0 || far)) rflag[r] = 1;
+                double f = 1.0;  // rescale of the running sums to the new reference exponent
+                if (Rrun[r] != INT_MIN && Rnew != Rrun[r]) {
+                    const int dsh = Rrun[r] - Rnew;
+                    if (dsh < -900) rflag[r] = 1;
+                    f = ldexp(1.0, max(dsh, -1000));
+                    zacc[r] *= f;
+                }
+                if (lane == 0) S.sc[buf][r] = f;
+                Rrun[r] = Rnew;
+                double om = (live && !far) ? ldexp((double)M, E - Rnew) : 0.0;
+                if (rflag[r]) om = 0.0;
+                zacc[r] += om;
+                nvis[r] += vis ? 1 : 0;
+                S.w[buf][lane][r] = om;
             }
+                }
+            __syncthreads();  // weights of tile it published; wave B is done with tile it - 1
         }
-        if (more) issue_v(n0 + DT, vr);  // V(it+1) into the registers P(it) just consumed
-        __syncthreads();                  // S.w and the K buffer are free for the next tile
-    }
-
-    // ---- epilogue: reduce the 4 key groups, write the split partial
-    double* red = reinterpret_cast<double*>(&S.K[0][0]);  // [g][r][128]: 4 * RB KB <= 16 KB
-    float* vred = reinterpret_cast<float*>(&S.K[1][0]);   // [g][128]
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) red[(g * RB + r) * 128 + 8 * c8 + c] = pacc[r][c];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) vred[g * 128 + 8 * c8 + c] = vmx[c];
-    double zs[RB];
-    int ns[RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        zs[r] = wave_sum(zacc[r]);
-        ns[r] = wave_sum_i(nvis[r]);
-    }
-    __syncthreads();
-    for (int x = lane; x < nrow * 128; x += 64) {
-        const int r = x >> 7, c = x & 127;
-        double s = red[(0 * RB + r) * 128 + c] + red[(1 * RB + r) * 128 + c];
-        s += red[(2 * RB + r) * 128 + c] + red[(3 * RB + r) * 128 + c];
-        int64_t gr = 0;
-#pragma unroll
-        for (int rr = 0; rr < RB; ++rr)
-            if (rr == r) gr = grow[rr];
-        P.pN[(pbase + gr) * 128 + c] = s;
-    }
-    for (int c = lane; c < 128; c += 64) {
-        float m = fmaxf(fmaxf(vred[c], vred[128 + c]), fmaxf(vred[256 + c], vred[384 + c]));
-        P.pV[(((int64_t)split * P.nseg + seg) * P.nrb + rbk) * 128 + c] = m;
-    }
-    if (lane == 0) {
-        if (P.stats && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)nrow);
+        double zs[RB];
+        int ns[RB];
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            if (r < nrow) {
-                const int64_t o = pbase + grow[r];
-                P.pR[o] = Rrun[r];
-                P.pZ[o] = zs[r];
-                P.pn[o] = rflag[r] ? -1 : ns[r];
+            zs[r] = wave_sum(zacc[r]);
+            ns[r] = wave_sum_i(nvis[r]);
+        }
+        if (lane == 0) {
+            if (P.stats && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)nrow);
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                if (r < nrow) {
+                    const int64_t o = pbase + grow[r];
+                    P.pR[o] = Rrun[r];
+                    P.pZ[o] = zs[r];
+                    P.pn[o] = rflag[r] ? -1 : ns[r];
+                }
             }
+        }
+    } else {
+        // ============ wave B: V tiles (double-buffered in VGPRs) and the P.V sums
+        double pacc[RB][8];
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) pacc[r][c] = 0.0;
+        // max |v| over this lane's 8 channels and keys (a per-channel bound only needs to be >=
+        // the channel's own maximum)
+        float vmx = 0.0f;
+        u32x4 vA[16], vB[16];
+        if (ntiles > 0) {
+            issue_v(k0, vA, 0.0, 0.0);
+            issue_v(k0 + DT, vB, 0.0, 0.0);
+        }
+        // P of tile t with its V in vr; then V(t+2) into vr
+        auto pv = [&](int t, u32x4 (&vr)[16]) __attribute__((always_inline)) {
+            const int buf = t & 1;
+            // V loads complete in issue order: V(t) has landed once only V(t+1)'s 16 instructions
+            // may be outstanding
+            wait_vm<16>();
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const double f = S.sc[buf][r];
+                if (f != 1.0) {
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) pacc[r][c] *= f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int kk = 4 * j + g;
+                double om[RB];
+#pragma unroll
+                for (int r = 0; r < RB; ++r) om[r] = S.w[buf][kk][r];
+                const uint32_t vd[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float lo = __uint_as_float(vd[q] << 16), hi = __uint_as_float(vd[q] & 0xFFFF0000u);
+                    vmx = fmaxf(fmaxf(vmx, absf(lo)), absf(hi));
+                    const double dlo = (double)lo, dhi = (double)hi;
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        pacc[r][2 * q] = __fma_rn(om[r], dlo, pacc[r][2 * q]);
+                        pacc[r][2 * q + 1] = __fma_rn(om[r], dhi, pacc[r][2 * q + 1]);
+                    }
+                }
+                // zero-instruction fence: every sum and the next group's V registers count as
+                // rewritten here, so groups stay in order (otherwise the compiler runs each sum's
+                // chain over all 16 groups, which needs every group's converted V at once)
+#pragma unroll
+                for (int r = 0; r < RB; ++r)
+                    asm volatile("" : "+v"(pacc[r][0]), "+v"(pacc[r][1]), "+v"(pacc[r][2]), "+v"(pacc[r][3]),
+                                 "+v"(pacc[r][4]), "+v"(pacc[r][5]), "+v"(pacc[r][6]), "+v"(pacc[r][7]));
+                if (j + 1 < 16) asm volatile("" : "+v"(vr[j + 1]), "+v"(vmx));
+            }
+            // V(t+2) into vr, issued only after the last sums of tile t (its offsets depend on them)
+            issue_v(k0 + (t + 2) * DT, vr, pacc[0][0], pacc[RB - 1][7]);
+        };
+        // Barriers pair one to one with wave A's ntiles + 2: the prologue barrier, then one before
+        // each tile (its weights are published by then) and one after the last. Straight-line
+        // pairs keep vA and vB free of merges (no register copies).
+        __syncthreads();  // prologue barrier (tables visible)
+        int t = 0;
+        for (; t + 1 < ntiles; t += 2) {
+            __syncthreads();
+            pv(t, vA);
+            __syncthreads();
+            pv(t + 1, vB);
+        }
+        if (t < ntiles) {
+            __syncthreads();
+            pv(t, vA);
+        }
+        __syncthreads();  // barrier ntiles + 1: wave A runs one loop iteration past its last tile
+        // reduce the 4 key groups (lanes 16 apart) through LDS; the K buffers are free once the
+        // loop's last barrier has passed
+        double* red = reinterpret_cast<double*>(&S.K[0][0]);  // [g][r][128]: 4 * RB KB <= 16 KB
+        float* vred = reinterpret_cast<float*>(&S.K[1][0]);   // [g][16]
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) red[(g * RB + r) * 128 + 8 * c8 + c] = pacc[r][c];
+        vred[g * 16 + c8] = vmx;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        for (int x = lane; x < nrow * 128; x += 64) {
+            const int r = x >> 7, c = x & 127;
+            double sum = red[(0 * RB + r) * 128 + c] + red[(1 * RB + r) * 128 + c];
+            sum += red[(2 * RB + r) * 128 + c] + red[(3 * RB + r) * 128 + c];
+            int64_t gr = 0;
+#pragma unroll
+            for (int rr = 0; rr < RB; ++rr)
+                if (rr == r) gr = grow[rr];
+            P.pN[(pbase + gr) * 128 + c] = sum;
+        }
+        for (int c = lane; c < 128; c += 64) {
+            const int q = c >> 3;
+            const float m = fmaxf(fmaxf(vred[q], vred[16 + q]), fmaxf(vred[32 + q], vred[48 + q]));
+            P.pV[(((int64_t)split * P.nseg + seg) * P.nrb + rbk) * 128 + c] = m;
         }
     }
 }
@@ -474,7 +523,7 @@ int ea::ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st) {
             const void* fns[9] = {decode_fn<1>(4), decode_fn<1>(16), decode_fn<1>(64), decode_fn<2>(4), decode_fn<2>(16),
                                   decode_fn<2>(64), decode_fn<4>(4), decode_fn<4>(16), decode_fn<4>(64)};
             for (const void* f : fns) {
-                hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem));
+                hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem<4>));
                 if (e != hipSuccess) attr_err = e;
             }
             attr_done = true;
@@ -483,6 +532,7 @@ int ea::ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st) {
     if (attr_err != hipSuccess) return -100 - (int)attr_err;
     Params Pc = P;
     void* args[] = {&Pc};
-    hipError_t e = hipLaunchKernel(fn, grid, dim3(64), args, sizeof(DecodeSmem), st);
+    const size_t lds = rb == 1 ? sizeof(DecodeSmem<1>) : (rb == 2 ? sizeof(DecodeSmem<2>) : sizeof(DecodeSmem<4>));
+    hipError_t e = hipLaunchKernel(fn, grid, dim3(128), args, lds, st);
     return e == hipSuccess ? 1 : -100 - (int)e;
 }
