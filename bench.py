@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 METRIC = "decode KV GB/s & prefill int8-MFMA TOPS (% roofline), bit-exact, fallback-row %"
 HBM_PEAK_GBS = 8000.0
 GOLDEN = os.path.join(ROOT, "tests", "golden", "baseline_sha256.json")
-TRAFFIC = os.path.join(ROOT, "profiles", "ea_split_C2_traffic.md")
+TRAFFIC = os.path.join(ROOT, "profiles", "ea_decode_C2_traffic.md")
 
 
 def algorithmic_bytes(prob: dict) -> int:
@@ -185,7 +185,7 @@ def main():
                    "head_dim": 128, "kv_len": 4096, "page_size": 16, "layout": "NHD", "nsplit": dp.nsplit,
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "ea_split",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "ea_decode",
                      "kernel_ms": round(split_ms, 5)},
         "kernels_ms": {k: round(float(phases[:, j].mean()), 5) for j, k in enumerate(("prep", "split", "combine",
                                                                                       "tier2"))},
