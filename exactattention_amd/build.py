@@ -6,16 +6,19 @@ import os
 import subprocess
 import sys
 
-SOURCES = ["ea_hip.hip", "ea_decode.hip"]
+SOURCES = ["ea_hip.hip", "ea_decode.hip", "ea_prefill.hip"]
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libexactattn_hip.so")
 
 # -packed-fp32-ops: never emit packed fp32 VALU ops (their forms have misbehaved on this pool).
 # -fno-gpu-flush-denormals-to-zero: bf16 subnormals convert exactly through fp32.
+# -amdgpu-mfma-vgpr-form=1: MFMA operands and accumulators in VGPRs; the prefill kernel's int32
+#  accumulators are also read by VALU folds, and the AGPR file then serves as cheap spill space
+#  (the AGPR form spills the kernel's working set to scratch).
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
                "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-               "-Wall", "-Wno-unused-function"]
+               "-mllvm", "-amdgpu-mfma-vgpr-form=1", "-Wall", "-Wno-unused-function"]
 
 
 def build(verbose: bool = False) -> str:

@@ -982,7 +982,9 @@ struct Plan {
     int nsplit, split_len, rb, nrb, r_seg, grp, nseg, pshift, dlog;
     int64_t rows;
     size_t off_q64, off_qinfo, off_qn, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
+    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr;
     int t2_keys;
+    int prefill, pf_ntiles, pf_nrb;
 };
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1038,6 +1040,14 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->t2_keys = maxlen + 64;
     pl->off_t2M = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 4);
     pl->off_t2E = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 8);
+    pl->prefill = (!o->timers && ea_prefill_eligible(*g, pl->grp, &pl->pf_ntiles, &pl->pf_nrb)) ? 1 : 0;
+    pl->off_pfq = pl->off_pfqm = pl->off_pfkv = pl->off_pfscr = 0;
+    if (pl->prefill) {
+        pl->off_pfq = off; off = align_up(off + (size_t)R * 512);
+        pl->off_pfqm = off; off = align_up(off + (size_t)R * sizeof(PfQMeta));
+        pl->off_pfkv = off; off = align_up(off + (size_t)pl->nseg * pl->pf_ntiles * EA_PF_TILE_BYTES);
+        pl->off_pfscr = off; off = align_up(off + (size_t)pl->nseg * pl->pf_nrb * 256 * 64 * 8);
+    }
     pl->total = off;
     return 0;
 }
@@ -1106,12 +1116,33 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.t2M = (int32_t*)(ws + pl.off_t2M);
     P.t2E = (int64_t*)(ws + pl.off_t2E);
     P.t2_keys = pl.t2_keys;
+    P.pfq = (uint8_t*)(ws + pl.off_pfq);
+    P.pfqm = (void*)(ws + pl.off_pfqm);
+    P.pfkv = (uint8_t*)(ws + pl.off_pfkv);
+    P.pfscr = (double*)(ws + pl.off_pfscr);
+    P.pf_ntiles = pl.pf_ntiles;
+    P.pf_nrb = pl.pf_nrb;
     hipStream_t st = (hipStream_t)stream;
     unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
     auto mark = [&](int i) -> int {
         return o->events ? herr(hipEventRecord((hipEvent_t)o->events[i], st)) : 0;
     };
     if ((rc = mark(0))) return rc;
+    if (pl.prefill) {
+        // int8-MFMA prefill: slicing, then one kernel that certifies and writes every row; the
+        // rows it leaves go to tier 2
+        if ((rc = ea_launch_prefill(P, st))) return rc;
+        if ((rc = mark(1))) return rc;
+        if ((rc = ea_launch_prefill_main(P, st))) return rc;
+        if ((rc = mark(2))) return rc;
+        if ((rc = mark(3))) return rc;
+        if (o->tier2) {
+            hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_THREADS), 0, st, P);
+            rc = herr(hipGetLastError());
+            if (rc) return rc;
+        }
+        return mark(4);
+    }
     hipLaunchKernelGGL(ea_prep, dim3(rb4), dim3(256), 0, st, P);
     rc = herr(hipGetLastError());
     if (rc) return rc;

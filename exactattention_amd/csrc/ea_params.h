@@ -56,6 +56,13 @@ struct Params {
     int32_t* t2M;     // EA_T2_BLOCKS * max_keys
     int64_t* t2E;     // EA_T2_BLOCKS * max_keys
     int32_t t2_keys;
+    // int8-MFMA prefill path (ea_prefill.hip)
+    uint8_t* pfq;     // rows * 512: q digit planes
+    void* pfqm;       // rows * sizeof(PfQMeta)
+    uint8_t* pfkv;    // nseg * pf_ntiles * EA_PF_TILE_BYTES: K/V digit tiles and tile metadata
+    double* pfscr;    // nseg * pf_nrb * 256 lanes * 64: per-lane sums of completed epochs
+    int32_t pf_ntiles;  // 64-key tiles per segment
+    int32_t pf_nrb;     // 64-row blocks per segment
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
@@ -143,6 +150,40 @@ __device__ __forceinline__ int wave_sum_i(int x) {
 // Launches the d = dv = 128 decode kernel (ea_decode.hip) when the geometry allows it: returns 1
 // when launched, 0 when the caller must run the general split kernel, -100 - e on a HIP error.
 int ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st);
+
+// int8-MFMA prefill path (ea_prefill.hip). A tile holds 64 keys of one segment:
+//   [0, 32768)       K digit planes t = 0..3: [t][key 64][128 bytes], 16-byte chunk c of key k
+//                    stored at chunk c ^ (k & 7)
+//   [32768, 65536)   V digit planes t = 0..3: [t][channel 128][64 bytes], key 16kt + 4g + i at
+//                    byte 16 (g ^ ((channel >> 2) & 3)) + 4kt + i
+//   [65536, 69632)   PfTileMeta
+#define EA_PF_TILE_BYTES 69632
+#define EA_PF_META_OFF 65536
+struct PfQMeta {
+    int32_t lsb;    // q = X * 2^lsb, |X| < 2^30
+    int32_t flags;  // bit 0: digit 0 nonzero somewhere; bit 1: NaN/inf; bits 8..15: inexact elements
+    double qA;      // sum_i sum_s |d_s,i| 2^(8s)
+    double qX;      // max_i |X_i|
+    double a;       // alpha * 2^lsb
+};
+struct PfTileMeta {
+    int32_t lsbk[64];
+    int32_t vlsb[64];
+    double kA[64];    // max_i sum_t |d_t,i| 2^(8t)
+    double kX[64];    // max_i |X_i|
+    int32_t kfl[64];  // bit 0: NaN/inf in the key's K or V row; bits 8..15: inexact K elements
+    double EV[128];   // per channel: (2^38 + 1) / 2 * (inexact V elements of the tile)
+    int32_t tfl;      // bit kt: a key of 16-key group kt needs K digit 0; bit 4: a NaN/inf key;
+                      // bit 5: a key with inexact K elements
+    int32_t pad;
+    double EVt;       // (2^38 + 1) / 2 * (inexact V elements of the tile, all channels)
+};
+// Returns 1 when the prefill path handles this geometry (and sets the tile and block counts),
+// 0 otherwise.
+int ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb);
+// Enqueue the slicing kernels (q rows, K/V tiles), then the prefill kernel; 0 or -100 - e.
+int ea_launch_prefill(const Params& P, hipStream_t st);
+int ea_launch_prefill_main(const Params& P, hipStream_t st);
 
 typedef const double __attribute__((address_space(4))) cdouble_t;
 typedef const int32_t __attribute__((address_space(4))) cint_t;

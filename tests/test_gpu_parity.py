@@ -329,3 +329,109 @@ def test_decode_kernel_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
             assert flags[r] == (2 if kvl[t] > 140 else 0), (t, h, flags)
             if kvl[t] <= 140:
                 assert np.array_equal(got[0, t, h], want[0, t, h]), (t, h)
+
+
+# ---------------------------------------------------------------------------------------------
+# the int8-MFMA prefill kernel (64 rows per block, balanced radix-256 digits)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.fixture
+def force_prefill(monkeypatch):
+    monkeypatch.setenv("EA_PREFILL", "1")
+
+
+def _rows(prob):
+    return prob["q"].shape[0] * prob["q"].shape[1] * prob["q"].shape[2]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("vkind", ["normal", "wide", "dupes"])
+def test_prefill_kernel_kinds_match_oracle(gpu, force_prefill, kind, vkind):
+    rng = np.random.default_rng(hash(("pf", kind, vkind)) % (1 << 32))
+    prob = _rand_problem(rng, kind, vkind, B=2, T=40, Hq=4, Hkv=2, S=150, d=128, dv=128)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    got, flags, st = _run(prob, ab)
+    assert st["prefill_kernel_rows"] == _rows(prob), st
+    assert not np.any(flags == 1), st
+    assert np.array_equal(got, want), st
+
+
+@pytest.mark.parametrize("out", ["bf16", "fp32"])
+def test_prefill_causal_matches_oracle_and_decode(gpu, out):
+    """A causal prefill of 200 tokens (no forcing: T >= 64 selects the kernel) equals the oracle,
+    and each token's row equals a single-token decode over the same keys."""
+    rng = np.random.default_rng(31)
+    B, T, Hq, Hkv, d = 1, 200, 4, 2, 128
+    q = bf16(rng, (B, T, Hq, d))
+    k = bf16(rng, (B, Hkv, T, d))
+    v = bf16(rng, (B, Hkv, T, d))
+    prob = problem.contiguous(q, k, v, (np.arange(T) + 1).reshape(1, T))
+    ab = default_alpha_bits(d)
+    want, _ = _oracle(prob, ab, out)
+    got, flags, st = _run(prob, ab, out)
+    assert st["prefill_kernel_rows"] == _rows(prob), st
+    assert not np.any(flags), st
+    assert np.array_equal(got, want), st
+    # token-by-token decode (decode kernel) over the same keys
+    dec = problem.contiguous(q.transpose(1, 0, 2, 3), np.repeat(k, T, axis=0), np.repeat(v, T, axis=0),
+                             (np.arange(T) + 1).reshape(T, 1))
+    got_d, fl_d, st_d = _run(dec, ab, out)
+    assert st_d["prefill_kernel_rows"] == 0 and not np.any(fl_d)
+    assert np.array_equal(got_d.reshape(got.shape[1:]), got[0])
+
+
+def test_prefill_paged_gqa_ragged(gpu, force_prefill):
+    """Paged NHD cache (page 16), GQA 4, ragged sequence lengths (partial 64-row blocks and
+    partial 64-key tiles), rows whose prefix is empty."""
+    rng = np.random.default_rng(32)
+    B, T, Hq, Hkv, d = 3, 37, 8, 2, 128
+    seq = np.array([37, 90, 130])
+    q = bf16(rng, (B, T, Hq, d))
+    k = bf16(rng, (B, Hkv, 130, d))
+    v = bf16(rng, (B, Hkv, 130, d))
+    kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    kv[0, :3] = 0
+    base = problem.contiguous(q, k, v, kv, seq_len=seq)
+    prob = problem.to_paged(base, 16, np.random.default_rng(3), "NHD")
+    ab = default_alpha_bits(d)
+    want, _ = _oracle(base, ab)
+    got, flags, st = _run(prob, ab)
+    assert st["prefill_kernel_rows"] == _rows(prob), st
+    assert not np.any(flags), st
+    assert np.array_equal(got, want)
+
+
+def test_prefill_nonfinite_flags_exactly_the_rows_that_see_them(gpu, force_prefill):
+    rng = np.random.default_rng(45)
+    T = 80
+    prob = _rand_problem(rng, "normal", "normal", B=1, T=T, Hq=2, Hkv=1, S=T, d=128, dv=128)
+    prob["seq_len"][:] = T
+    prob["kv_len"][:] = np.arange(T) + 1
+    prob["k"][0, 0, 50, 3] = 0x7FC0   # NaN key at position 50
+    prob["v"][0, 0, 70, 100] = 0xFF80  # -inf value at position 70
+    prob["q"][0, 10, 1, 5] = 0x7F80    # inf in one query row
+    ab = default_alpha_bits(128)
+    got, flags, st = _run(prob, ab)
+    clean = {**prob, "k": prob["k"].copy(), "v": prob["v"].copy(), "q": prob["q"].copy()}
+    clean["k"][0, 0, 50, 3] = 0
+    clean["v"][0, 0, 70, 100] = 0
+    clean["q"][0, 10, 1, 5] = 0
+    want, _ = _oracle(clean, ab)
+    for t in range(T):
+        for h in range(2):
+            bad = t >= 50 or (t == 10 and h == 1)
+            assert flags[t * 2 + h] == (2 if bad else 0), (t, h)
+            if not bad:
+                assert np.array_equal(got[0, t, h], want[0, t, h]), (t, h)
+
+
+def test_prefill_c3_golden_hash(gpu):
+    """BASELINE config C3 at full size (4096 tokens, 16/8 heads): the committed oracle hash."""
+    p = configs.c3()
+    ab = configs.alpha_bits()
+    got, flags, st = _run(p, ab)
+    gold = json.load(open(os.path.join(GOLD, "baseline_sha256.json")))["C3"]["sha256"]
+    assert st["prefill_kernel_rows"] == _rows(p), st
+    assert not np.any(flags), st
+    assert hashlib.sha256(got.tobytes()).hexdigest() == gold, st
