@@ -1046,7 +1046,7 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
         pl->off_pfq = off; off = align_up(off + (size_t)R * 512);
         pl->off_pfqm = off; off = align_up(off + (size_t)R * sizeof(PfQMeta));
         pl->off_pfkv = off; off = align_up(off + (size_t)pl->nseg * pl->pf_ntiles * EA_PF_TILE_BYTES);
-        pl->off_pfscr = off; off = align_up(off + (size_t)pl->nseg * pl->pf_nrb * 256 * 64 * 8);
+        pl->off_pfscr = off; off = align_up(off + (size_t)pl->nseg * pl->pf_nrb * 512 * 32 * 8);
     }
     pl->total = off;
     return 0;

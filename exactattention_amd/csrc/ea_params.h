@@ -60,7 +60,7 @@ struct Params {
     uint8_t* pfq;     // rows * 512: q digit planes
     void* pfqm;       // rows * sizeof(PfQMeta)
     uint8_t* pfkv;    // nseg * pf_ntiles * EA_PF_TILE_BYTES: K/V digit tiles and tile metadata
-    double* pfscr;    // nseg * pf_nrb * 256 lanes * 64: per-lane sums of completed epochs
+    double* pfscr;    // nseg * pf_nrb * 512 lanes * 32: per-lane sums of completed epochs
     int32_t pf_ntiles;  // 64-key tiles per segment
     int32_t pf_nrb;     // 64-row blocks per segment
 };

@@ -323,6 +323,34 @@ __global__ void __launch_bounds__(256) ea_pf_kvslice(Params P) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// w = RN24(2^t) = M 2^E for an exact fp32 t (bits), from the fp64 tables (T1 pre-scaled by 2^23)
+// and the cubic; false when undecided or |t| >= 2^30 (the 128-bit enclosure decides those).
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool table_weight(uint32_t tbits, const double* T1s, const double* T2, int* Mout,
+                                             int* Eout) {
+    const uint32_t field = (tbits >> 23) & 0xFF;
+    if (field < 102) {  // |t| < 2^-25: 2^t rounds to 1
+        *Mout = 1 << 23;
+        *Eout = -23;
+        return true;
+    }
+    if (field >= 127 + 30) return false;
+    const double c1 = u64_as_f64(EA_C_BITS[0]), c2 = u64_as_f64(EA_C_BITS[1]), c3 = u64_as_f64(EA_C_BITS[2]);
+    const double d0 = (double)__uint_as_float(tbits);
+    const double fl = floor(d0);
+    const double f = d0 - fl;
+    const int i = ((int)(f * 65536.0)) & 0xFFFF;
+    const double rr = __fma_rn(-(double)i, 0x1p-16, f);
+    const double poly = rr * __fma_rn(rr, __fma_rn(rr, c3, c2), c1);
+    const double aa = T1s[i >> 8] * T2[i & 255];
+    const double Y = __fma_rn(aa, poly, aa);
+    const double Yr = (Y + 0x1.8p52) - 0x1.8p52;
+    *Mout = (int)Yr;
+    *Eout = (int)fl - 23;
+    return fabs(Y - Yr) <= 0.5 - 0x1p-26;
+}
+
+// ------------------------------------------------------------------------------------------------
 // Branch-free certified t = RN32(alpha s) and w = RN24(2^t) = M 2^E for the main kernel.
 // x: the fp64 score in units 2^(lsbq + lk), within dx of the exact integer; a = alpha 2^lsbq.
 // The interval [a x 2^lk - a dx 2^lk, ...] rounds to t0 = RN32(p) when it lies inside the
@@ -372,14 +400,17 @@ __device__ __forceinline__ bool lean_weight(double x, double adx, int lk, double
 // Lane (g = lane / 16, j = lane % 16):
 //   score layout  row j, keys 16 kt + 4 g + i (i = 0..3)
 //   P.V layout    rows 4 g + i, channels 16 ct + j
-// LDS: K planes + tile metadata double-buffered, V planes single-buffered (its DMA overlaps the
-// next tile's score phase), exp2 tables, the pair exchanges.
+// LDS: K and V planes single-buffered (the next tile's K planes load during this tile's weight
+// and P.V phases, its V planes during the next score phase), tile metadata double-buffered, the
+// block's q digits, exp2 tables, the pair exchanges.
 // ------------------------------------------------------------------------------------------------
-constexpr int PF_KB = 36864;                    // K planes (32 KB) + tile metadata (4 KB)
-constexpr int PF_OFF_V = 2 * PF_KB;             // V planes (32 KB)
-constexpr int PF_OFF_T = PF_OFF_V + 32768;      // T1 * 2^23, T2 (4 KB)
-constexpr int PF_OFF_WD = PF_OFF_T + 4096;      // weight digits: 8 waves x 5 planes x 2 x 64 lanes
-constexpr int PF_OFF_X = PF_OFF_WD + 8 * 2560;  // per-lane exchange: 8 waves x 64 lanes x 16 B
+constexpr int PF_OFF_V = 0;                      // V planes (32 KB), single buffer
+constexpr int PF_OFF_K = 32768;                  // K planes (32 KB), single buffer
+constexpr int PF_OFF_M = 65536;                  // tile metadata, 2 x 4 KB
+constexpr int PF_OFF_Q = PF_OFF_M + 8192;        // q digits of the block's 64 rows (32 KB)
+constexpr int PF_OFF_T = PF_OFF_Q + 32768;       // T1 * 2^23, T2 (4 KB)
+constexpr int PF_OFF_WD = PF_OFF_T + 4096;       // weight digits: 8 waves x 5 planes x 2 x 64 lanes
+constexpr int PF_OFF_X = PF_OFF_WD + 8 * 2560;   // per-lane exchange: 8 waves x 64 lanes x 16 B
 constexpr int PF_LDS = PF_OFF_X + 8 * 1024;
 
 struct PfX {
@@ -387,7 +418,12 @@ struct PfX {
     double c;
 };
 
-__global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
+template <int SPLIT, int NWB>
+__global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
+    constexpr int RPB = 16 * NWB / SPLIT;  // rows per block
+    constexpr int NKT = 4 / SPLIT;     // key groups of 16 per wave
+    constexpr int NCT = 8 / SPLIT;     // channel tiles of 16 per wave
+    constexpr int NKI = 32 / NWB;      // K (and V) DMA instructions per wave and tile
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int s_kend;
     double* const T1s = (double*)(smem + PF_OFF_T);
@@ -396,7 +432,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
     PfX* const s_x = (PfX*)(smem + PF_OFF_X);              // [wave][lane 64]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rg = w >> 1, hh = w & 1;
+    const int rg = w / SPLIT, hh = w % SPLIT;
     const int g = lane >> 4, j = lane & 15;
     const int nseg = P.nseg;
     const int seg = blockIdx.x % nseg;
@@ -405,8 +441,10 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
     const int64_t b = seg / Hkv;
     const int hk = seg % Hkv;
     const int T = P.g.num_tokens;
+    uint32_t* const wd_w = s_wd + w * 640 + lane;               // this wave's digit planes (SPLIT 2)
+    const uint32_t* const wd_r = s_wd + (w & ~1) * 640 + lane;  // the pair's, in key-group order
     // per-lane scratch: fp64 sums of completed epochs, then the final quotients
-    double* const scr = P.pfscr + (((int64_t)blockIdx.x * 8 + w) * 64 + lane) * 32;
+    double* const scr = P.pfscr + (((int64_t)blockIdx.x * NWB + w) * 64 + lane) * (8 * NCT);
 
     if (tid == 0) s_kend = 0;
     if (tid < 256) {
@@ -414,7 +452,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
         T2[tid] = u64_as_f64(EA_T2_BITS[tid]);
     }
     // ---- this lane's row in the score layout
-    const int lr = rbk * 64 + rg * 16 + j;
+    const int lr = rbk * RPB + rg * 16 + j;
     const bool rvalid = lr < P.r_seg;
     const int lrc = rvalid ? lr : P.r_seg - 1;
     int tq;
@@ -432,9 +470,17 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
         const int kw = wave_max_i(ve);
         if (lane == 0) atomicMax(&s_kend, kw);
     }
-    // q digits (B operand of the score MFMA): row j, dims 64 h + 16 g .. + 15, plane s; loaded
-    // from memory (L2) for each tile so they do not occupy registers across the P.V phase
-    const uint8_t* const qsrc = P.pfq + grow * 512 + 16 * g;
+    // q digits of the block's rows into LDS: [row 64][plane 4][128 bytes]; rows past the segment
+    // repeat its last row
+    for (int c = tid; c < RPB * 32; c += 64 * NWB) {
+        const int r = c >> 5, q16 = c & 31;
+        const int lrr = min(rbk * RPB + r, P.r_seg - 1);
+        int tt;
+        const int64_t gr = seg_row(P, b, hk, lrr, &tt);
+        *(uint4*)(smem + PF_OFF_Q + r * 512 + q16 * 16) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
+    }
+    // this lane's q digits (B operand of the score MFMA): row j, dims 64 h + 16 g .. + 15, plane s
+    const uint8_t* const qlds = smem + PF_OFF_Q + (rg * 16 + j) * 512 + 16 * g;
     const PfQMeta qm = ((const PfQMeta*)P.pfqm)[grow];
     const bool needq = __ballot(rvalid && (qm.flags & 1)) != 0;
     // |a| times the fold error factor 6.01 u and sum_i A_q,i: the score bound is this * A_k
@@ -456,25 +502,26 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
         const uint8_t* src = P.pfkv + ((int64_t)seg * P.pf_ntiles + tile) * EA_PF_TILE_BYTES;
         return __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, EA_PF_TILE_BYTES, 0x00020000);
     };
-    auto issue_k = [&](int tile, int buf) __attribute__((always_inline)) {
+    // one lane offset for every DMA instruction; the per-instruction offset goes in soffset
+    const int vlane = lane * 16;
+    auto issue_k = [&](int tile) __attribute__((always_inline)) {
         __amdgpu_buffer_rsrc_t rs = rsrc(tile);
-        uint8_t* dst = smem + buf * PF_KB;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int off = (q * 8 + w) * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + off), 16, off + lane * 16, 0, 0, 0);
+        for (int q = 0; q < NKI; ++q) {
+            const int off = (q * NWB + w) * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_K + off), 16, vlane, off, 0, 0);
         }
-        if (w < 4)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + 32768 + w * 1024), 16,
-                                                     EA_PF_META_OFF + w * 1024 + lane * 16, 0, 0, 0);
+        if (NWB == 4 || w < 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_M + (tile & 1) * 4096 + w * 1024),
+                                                     16, vlane, EA_PF_META_OFF + w * 1024, 0, 0);
     };
     auto issue_v = [&](int tile) __attribute__((always_inline)) {
         __amdgpu_buffer_rsrc_t rs = rsrc(tile);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int off = (q * 8 + w) * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_V + off), 16,
-                                                     32768 + off + lane * 16, 0, 0, 0);
+        for (int q = 0; q < NKI; ++q) {
+            const int off = (q * NWB + w) * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_V + off), 16, vlane, 32768 + off,
+                                                     0, 0);
         }
     };
 
@@ -485,9 +532,9 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
     int nv = 0;
     int nfrac = 0;   // this wave's keys of the current epoch whose scaled weight may have a fraction
     // P.V state (P.V layout): int32 accumulators of digit weights 256^1 .. 256^7, 4 channel tiles
-    v4i pacc[4][7];
+    v4i pacc[NCT][7];
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
+    for (int cc = 0; cc < NCT; ++cc)
 #pragma unroll
         for (int k = 0; k < 7; ++k) pacc[cc][k] = (v4i){0, 0, 0, 0};
     double EVs = 0.0;  // inexact V elements of the epoch's tiles, times (2^38 + 1) / 2
@@ -496,37 +543,29 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
     uint32_t failbits = 0;
 
     if (ntiles > 0) {
-        issue_k(0, 0);
+        issue_k(0);
         issue_v(0);
     }
     for (int it = 0; it <= ntiles; ++it) {
         const bool last = it == ntiles;
-        const int buf = it & 1;
-        const uint8_t* Kt = smem + buf * PF_KB;
-        const PfTileMeta* TM = (const PfTileMeta*)(Kt + 32768);
-        v4i Mk[2], Ek[2];
+        const uint8_t* Kt = smem + PF_OFF_K;
+        const PfTileMeta* TM = (const PfTileMeta*)(smem + PF_OFF_M + (it & 1) * 4096);
+        v4i Mk[NKT], Ek[NKT];
         int nb = base;
         bool do_fold;
         int nf_pair = 0;  // the pair's nfrac (epoch so far)
         bool k_next = false;
         if (!last) {
-            wait_vm<4>();     // K(it) and its metadata landed; V(it) (4 instructions) may be in flight
-            __syncthreads();  // for every wave; K buffer buf ^ 1 is free
+            wait_vm<NKI>();   // K(it) and its metadata landed; V(it) (NKI instructions) may be in flight
+            __syncthreads();  // for every wave
             k_next = it + 1 < ntiles;
-            if (k_next) issue_k(it + 1, buf ^ 1);
             const int tfl = TM->tfl;
             const bool lossy = lossy_q || (tfl & 32);
             uint32_t slowmask = 0;  // pairs the fast path left undecided (cold path below)
             int gm = INT_MIN;
-            v4i qd[4][2];
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-                    qd[s][h] = (s == 0 && !needq) ? (v4i){0, 0, 0, 0} : *(const v4i*)(qsrc + 128 * s + 64 * h);
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int kt = 2 * hh + kk;
+            for (int kk = 0; kk < NKT; ++kk) {
+                const int kt = NKT * hh + kk;
                 v4i acc[7];
 #pragma unroll
                 for (int k = 0; k < 7; ++k) acc[k] = (v4i){0, 0, 0, 0};
@@ -542,7 +581,8 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
 #pragma unroll
                         for (int s = 0; s < 4; ++s) {
                             if (s == 0 && !needq) continue;
-                            acc[s + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, qd[s][h], acc[s + t], 0, 0, 0);
+                            const v4i Bq = *(const v4i*)(qlds + 128 * s + 64 * h);
+                            acc[s + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bq, acc[s + t], 0, 0, 0);
                         }
                     }
                 }
@@ -582,17 +622,36 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
                     if (good) gm = max(gm, E + vl4[i]);
                 }
             }
-            // ---- cold path: exact recompute of the pairs the fast path left undecided
+            // ---- cold path: exact decision for the pairs the fast path left undecided. The exact
+            // integer score comes from the digit planes in LDS (no memory traffic); only pairs
+            // whose digits are inexact (elements rounded at slicing) read the bf16 inputs.
             if (__builtin_expect(__ballot(slowmask != 0) != 0, 0)) {
-                for (int p = 0; p < 8; ++p) {
+                if (P.stats && lane == 0) atomicAdd((unsigned long long*)&P.stats[12], 1ull);
+                for (int p = 0; p < 4 * NKT; ++p) {
                     if (!((slowmask >> p) & 1)) continue;
                     const int kk = p >> 2, i = p & 3;
-                    const int key = 16 * (2 * hh + kk) + 4 * g + i;
+                    const int key = 16 * (NKT * hh + kk) + 4 * g + i;
                     const int n = it * 64 + key;
+                    const int kf = TM->kfl[key];
                     uint32_t tbits = 0;
                     int ls = 3;
-                    if (!qbad) {
-                        ++nslow;
+                    ++nslow;
+                    if (!qbad && !((qm.flags >> 8) & 0xFF) && !(kf >> 8)) {
+                        const int8_t* qrow = (const int8_t*)(smem + PF_OFF_Q + (rg * 16 + j) * 512);
+                        const int8_t* krow = (const int8_t*)(Kt + key * 128);
+                        i128 S = 0;
+                        for (int c = 0; c < 128; ++c) {
+                            const int kc = (((c >> 4) ^ (key & 7)) << 4) | (c & 15);
+                            int xq = 0, xk = 0;
+#pragma unroll
+                            for (int sp = 3; sp >= 0; --sp) {
+                                xq = xq * 256 + (int)qrow[128 * sp + c];
+                                xk = xk * 256 + (int)krow[8192 * sp + kc];
+                            }
+                            S += (i128)((int64_t)xq * (int64_t)xk);
+                        }
+                        ls = rn32_prod(P.am, S, P.ae + qm.lsb + TM->lsbk[key], &tbits);
+                    } else if (!qbad) {
                         const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)tq * P.g.q_tok_stride +
                                              (int64_t)(hk * P.grp + lrc % P.grp) * P.g.q_head_stride;
                         const uint16_t* kr = P.k + kv_off(P, b, n, hk, 0);
@@ -606,6 +665,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
                         }
                         ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1
                                                                     : logit_cert(P.alpha, ss, es, ea * 0x1p-44, &tbits);
+                        if (ls == 1) tbits = 0;
                     }
                     int32_t M = 0, E = 0;
                     bool live = false;
@@ -614,6 +674,8 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
                     } else if (ls == 3) {
                         unc = 1;
                         ++nunc_s;
+                    } else if (table_weight(tbits, T1s, T2, &M, &E)) {
+                        live = true;
                     } else {
                         // the 128-bit enclosure of 2^t decides RN24 (ea_device.h weight_wide)
                         int32_t M2 = 0;
@@ -628,7 +690,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
                         }
                     }
 #pragma unroll
-                    for (int q = 0; q < 2; ++q)
+                    for (int q = 0; q < NKT; ++q)
                         if (q == kk) {
 #pragma unroll
                             for (int r = 0; r < 4; ++r)
@@ -644,12 +706,14 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
             // when a weight would exceed 2^38 (G - base > 14 for G = E + vlsb)
             gm = max(gm, __shfl_xor(gm, 16, 64));
             gm = max(gm, __shfl_xor(gm, 32, 64));
-            s_x[w * 64 + lane] = PfX{gm, nfrac, 0.0};
-            __syncthreads();
-            {
+            if (SPLIT == 2) s_x[w * 64 + lane] = PfX{gm, nfrac, 0.0};
+            __syncthreads();  // every wave is done with the K planes of tile it
+            if (k_next) issue_k(it + 1);
+            nf_pair = nfrac;
+            if (SPLIT == 2) {
                 const PfX o = s_x[(w ^ 1) * 64 + lane];
                 gm = max(gm, o.a);
-                nf_pair = nfrac + o.b;
+                nf_pair += o.b;
             }
             const bool need_rb = gm != INT_MIN && (base == INT_MIN || gm > base + 14);
             nb = need_rb ? gm - 10 : base;
@@ -664,12 +728,13 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
             dom |= __shfl_xor(dom, 32, 64);
             unc |= __shfl_xor(unc, 16, 64);
             unc |= __shfl_xor(unc, 32, 64);
-            s_x[w * 64 + lane] = PfX{nv, nfrac | (dom << 24) | (unc << 25), z};
-            __syncthreads();
-            {
+            nf_pair = nfrac;
+            if (SPLIT == 2) {
+                s_x[w * 64 + lane] = PfX{nv, nfrac | (dom << 24) | (unc << 25), z};
+                __syncthreads();
                 const PfX o = s_x[(w ^ 1) * 64 + lane];
                 nv += o.a;
-                nf_pair = nfrac + (o.b & 0xFFFFFF);
+                nf_pair += o.b & 0xFFFFFF;
                 dom |= (o.b >> 24) & 1;
                 unc |= (o.b >> 25) & 1;
                 z += o.c;
@@ -677,6 +742,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
             do_fold = true;
         }
         if (do_fold) {
+            if (P.stats && lane == 0 && !last) atomicAdd((unsigned long long*)&P.stats[11], 1ull);
             // fold the int32 P.V accumulators (units 2^base of each row) into fp64 with a bound.
             // Before the last tile: add into scr, rescaled to the new bases. At the end: the
             // quotient N/Z and its error radius per (row, channel), certified further below.
@@ -702,7 +768,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
             nfrac = 0;
             const double omit = (double)ep_tiles * 0x1p20;  // pair (0, 0): 64 keys x 2^14
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
+            for (int cc = 0; cc < NCT; ++cc) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     double h = (double)pacc[cc][6][i], ha = fabs(h);
@@ -758,9 +824,10 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
         // ---- move bases, then this wave's weight digits (A operand of the P.V MFMA) and Z
         if (nb != base && base != INT_MIN) z = ldexp(z, max(base - nb, -1100));
         base = nb;
+        v4i Wd[5];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const int kt = 2 * hh + kk;
+        for (int kk = 0; kk < NKT; ++kk) {
+            const int kt = NKT * hh + kk;
             uint32_t L[4], H[4];
             const v4i vl4 = *(const v4i*)&TM->vlsb[16 * kt + 4 * g];
 #pragma unroll
@@ -782,34 +849,49 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
             const uint32_t b23 = __builtin_amdgcn_perm(L[3], L[2], 0x07030602u);
             const uint32_t e01 = __builtin_amdgcn_perm(H[1], H[0], 0x05010400u);
             const uint32_t e23 = __builtin_amdgcn_perm(H[3], H[2], 0x05010400u);
-            uint32_t* wd = s_wd + (w * 10 + kk) * 64 + lane;
-            wd[0 * 128] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
-            wd[1 * 128] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
-            wd[2 * 128] = __builtin_amdgcn_perm(b23, b01, 0x05040100u) ^ 0x80808080u;
-            wd[3 * 128] = __builtin_amdgcn_perm(b23, b01, 0x07060302u) ^ 0x80808080u;
-            wd[4 * 128] = __builtin_amdgcn_perm(e23, e01, 0x05040100u) ^ 0x80808080u;
+            const uint32_t d0 = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
+            const uint32_t d1 = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
+            const uint32_t d2 = __builtin_amdgcn_perm(b23, b01, 0x05040100u) ^ 0x80808080u;
+            const uint32_t d3 = __builtin_amdgcn_perm(b23, b01, 0x07060302u) ^ 0x80808080u;
+            const uint32_t d4 = __builtin_amdgcn_perm(e23, e01, 0x05040100u) ^ 0x80808080u;
+            if (SPLIT == 2) {
+                uint32_t* wd = wd_w + kk * 64;
+                wd[0 * 128] = d0;
+                wd[1 * 128] = d1;
+                wd[2 * 128] = d2;
+                wd[3 * 128] = d3;
+                wd[4 * 128] = d4;
+            } else {
+                Wd[0][kt] = (int)d0;
+                Wd[1][kt] = (int)d1;
+                Wd[2][kt] = (int)d2;
+                Wd[3][kt] = (int)d3;
+                Wd[4][kt] = (int)d4;
+            }
         }
         // V(it) landed (only K(it+1) may still be in flight), the pair's digits are in LDS
         if (k_next) {
-            if (w < 4) wait_vm<5>();
-            else wait_vm<4>();
+            if (NWB == 4 || w < 4) wait_vm<NKI + 1>();
+            else wait_vm<NKI>();
         } else {
             wait_vm<0>();
         }
         __syncthreads();
-        v4i Wd[5];
+        if (SPLIT == 2) {
 #pragma unroll
-        for (int s = 0; s < 5; ++s)
+            for (int s = 0; s < 5; ++s)
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) Wd[s][kt] = (int)s_wd[((w & ~1) + (kt >> 1)) * 640 + (s * 2 + (kt & 1)) * 64 + lane];
+                for (int kt = 0; kt < 4; ++kt) Wd[s][kt] = (int)wd_r[(kt >> 1) * 640 + (s * 2 + (kt & 1)) * 64];
+        }
         // ---- P.V: pacc[cc][s + t - 1] += W digits s x V digits t (all pairs but (0, 0))
-        const uint8_t* Vt = smem + PF_OFF_V;
+        // channel 16 (4 hh + cc) + j: the 16-byte slot swizzle (ch >> 2) & 3 = (j >> 2) & 3 does not
+        // depend on cc, so every read is one lane base plus a constant
+        const uint8_t* Vt = smem + PF_OFF_V + (16 * NCT * hh + j) * 64 + ((g ^ ((j >> 2) & 3)) << 4);
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const int ch = 16 * (4 * hh + cc) + j;
+        for (int cc = 0; cc < NCT; ++cc) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const v4i B = *(const v4i*)(Vt + t * 8192 + ch * 64 + ((g ^ ((ch >> 2) & 3)) << 4));
+                const v4i B = *(const v4i*)(Vt + t * 8192 + cc * 1024);
 #pragma unroll
                 for (int s = 0; s < 5; ++s) {
                     if (s + t < 1) continue;
@@ -827,7 +909,7 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
     // ---- certified final rounding, one (row, channel) at a time
     if (ntiles > 0) {
 #pragma unroll 1
-        for (int e = 0; e < 16; ++e) {
+        for (int e = 0; e < 4 * NCT; ++e) {
             const int cc = e >> 2, i = e & 3;
             const double2 qd2 = *(const double2*)(scr + 2 * e);
             if (!(qd2.y >= 0.0)) continue;
@@ -836,11 +918,11 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
                 failbits |= 1u << (8 * i + cc);
                 continue;
             }
-            const int lri = rbk * 64 + rg * 16 + 4 * g + i;
+            const int lri = rbk * RPB + rg * 16 + 4 * g + i;
             if (lri < P.r_seg) {
                 const int hq = hk * P.grp + lri % P.grp;
                 const int64_t o = b * P.g.o_seq_stride + (int64_t)(lri / P.grp) * P.g.o_tok_stride +
-                                  (int64_t)hq * P.g.o_head_stride + 16 * (4 * hh + cc) + j;
+                                  (int64_t)hq * P.g.o_head_stride + 16 * (NCT * hh + cc) + j;
                 if (P.out_fp32) ((uint32_t*)P.out)[o] = bits;
                 else ((uint16_t*)P.out)[o] = (uint16_t)bits;
             }
@@ -869,10 +951,12 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
             const uint64_t bal = __ballot(((failbits >> (8 * i)) & 0xFF) != 0);
             if (((bal >> (16 * g)) & 0xFFFFull) != 0) fb |= 1u << i;
         }
-        __syncthreads();  // s_x reuse
-        s_x[w * 64 + lane].a = (int)fb;
-        __syncthreads();
-        fb |= (uint32_t)s_x[(w ^ 1) * 64 + lane].a;
+        if (SPLIT == 2) {
+            __syncthreads();  // s_x reuse
+            s_x[w * 64 + lane].a = (int)fb;
+            __syncthreads();
+            fb |= (uint32_t)s_x[(w ^ 1) * 64 + lane].a;
+        }
         failbits = fb;
     }
 #pragma unroll
@@ -880,14 +964,14 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
         const int di = __shfl(dom, 4 * g + i, 64), ui = __shfl(unc, 4 * g + i, 64), nvr = __shfl(nv, 4 * g + i, 64);
         const bool fin = !di && !ui && ((failbits >> i) & 1);  // a final rounding failed
         const int flag = di ? 2 : ((ui || fin) ? 1 : 0);
-        const int lri = rbk * 64 + rg * 16 + 4 * g + i;
+        const int lri = rbk * RPB + rg * 16 + 4 * g + i;
         if (lri >= P.r_seg) continue;
         if (flag || nvr == 0) {
             const int hq = hk * P.grp + lri % P.grp;
             const int64_t o = b * P.g.o_seq_stride + (int64_t)(lri / P.grp) * P.g.o_tok_stride +
-                              (int64_t)hq * P.g.o_head_stride + 64 * hh + j;
+                              (int64_t)hq * P.g.o_head_stride + 16 * NCT * hh + j;
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
+            for (int cc = 0; cc < NCT; ++cc) {
                 if (P.out_fp32) ((uint32_t*)P.out)[o + 16 * cc] = 0u;
                 else ((uint16_t*)P.out)[o + 16 * cc] = 0;
             }
@@ -911,6 +995,12 @@ __global__ void __launch_bounds__(512, 1) ea_pf_main(Params P) {
     }
 }
 
+namespace {
+// kernel shape: pair-split waves; 4 waves (32 rows, 1 wave per SIMD, 512 registers) by default,
+// EA_PF_SHAPE=8 selects 8 waves (64 rows, 2 waves per SIMD)
+int pf_rows_per_block() { return (getenv("EA_PF_SHAPE") && getenv("EA_PF_SHAPE")[0] == '8') ? 64 : 32; }
+}  // namespace
+
 int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb) {
     if (getenv("EA_PREFILL") && getenv("EA_PREFILL")[0] == '0') return 0;
     const bool force = getenv("EA_PREFILL") && getenv("EA_PREFILL")[0] == '1';
@@ -918,8 +1008,9 @@ int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb
     const int64_t r_seg = (int64_t)g.num_tokens * grp;
     if (!force && g.num_tokens < 64) return 0;
     if (r_seg >= (1 << 30) || (int64_t)g.max_seq_len + 64 >= (1 << 30)) return 0;
+    const int rpb = pf_rows_per_block();
     *ntiles = (g.max_seq_len + 63) / 64;
-    *nrb = (int)((r_seg + 63) / 64);
+    *nrb = (int)((r_seg + rpb - 1) / rpb);
     return 1;
 }
 
@@ -927,7 +1018,10 @@ int ea::ea_launch_prefill(const Params& P, hipStream_t st) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [] {
-        attr_err = hipFuncSetAttribute((const void*)ea_pf_main, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+        attr_err = hipFuncSetAttribute((const void*)ea_pf_main<2, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+        if (attr_err == hipSuccess)
+            attr_err = hipFuncSetAttribute((const void*)ea_pf_main<2, 8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           PF_LDS);
     });
     if (attr_err != hipSuccess) return -100 - (int)attr_err;
     Params Pc = P;
@@ -945,7 +1039,9 @@ int ea::ea_launch_prefill(const Params& P, hipStream_t st) {
 int ea::ea_launch_prefill_main(const Params& P, hipStream_t st) {
     Params Pc = P;
     if (P.nseg > 0 && P.pf_nrb > 0) {
-        hipLaunchKernelGGL(ea_pf_main, dim3((unsigned)(P.nseg * P.pf_nrb)), dim3(512), PF_LDS, st, Pc);
+        const dim3 grid((unsigned)(P.nseg * P.pf_nrb));
+        if (pf_rows_per_block() == 64) hipLaunchKernelGGL((ea_pf_main<2, 8>), grid, dim3(512), PF_LDS, st, Pc);
+        else hipLaunchKernelGGL((ea_pf_main<2, 4>), grid, dim3(256), PF_LDS, st, Pc);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return -100 - (int)e;
     }

@@ -45,7 +45,7 @@ class Options(ctypes.Structure):
 
 STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
          "undecided_weights", "uncertified_final", "slow_path_scores",
-         "decode_kernel_rows", "prefill_kernel_rows"]
+         "decode_kernel_rows", "prefill_kernel_rows", "prefill_epoch_folds", "prefill_cold_waves"]
 
 
 def available() -> bool:

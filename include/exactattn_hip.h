@@ -83,7 +83,9 @@ typedef struct ea_options {
                                roundings not certified, [8] scores taken by the per-pair exact
                                path, [9] rows whose tier 1 ran in the d = 128 decode
                                kernel, [10] rows whose tier 1 ran in the int8-MFMA
-                               prefill kernel, [11..15] reserved */
+                               prefill kernel, [11] prefill epoch folds before the last
+                               tile (waves), [12] prefill waves that ran the exact
+                               per-pair path, [13..15] reserved */
     void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep, split,
                                combine and tier 2, and after tier 2 (per-kernel timing) */
     int64_t* timers;        /* optional device int64[16]: when set, the split kernel runs its
