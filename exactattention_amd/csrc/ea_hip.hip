@@ -1040,7 +1040,7 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->t2_keys = maxlen + 64;
     pl->off_t2M = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 4);
     pl->off_t2E = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 8);
-    pl->prefill = (!o->timers && ea_prefill_eligible(*g, pl->grp, &pl->pf_ntiles, &pl->pf_nrb)) ? 1 : 0;
+    pl->prefill = ea_prefill_eligible(*g, pl->grp, &pl->pf_ntiles, &pl->pf_nrb) ? 1 : 0;
     pl->off_pfq = pl->off_pfqm = pl->off_pfkv = pl->off_pfscr = 0;
     if (pl->prefill) {
         pl->off_pfq = off; off = align_up(off + (size_t)R * 512);

@@ -155,7 +155,7 @@ int ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st);
 //   [0, 32768)       K digit planes t = 0..3: [t][key 64][128 bytes], 16-byte chunk c of key k
 //                    stored at chunk c ^ (k & 7)
 //   [32768, 65536)   V digit planes t = 0..3: [t][channel 128][64 bytes], key 16kt + 4g + i at
-//                    byte 16 (g ^ ((channel >> 2) & 3)) + 4kt + i
+//                    byte 16 (g ^ ((channel >> 1) & 3)) + 4kt + i
 //   [65536, 69632)   PfTileMeta
 #define EA_PF_TILE_BYTES 69632
 #define EA_PF_META_OFF 65536

@@ -291,7 +291,7 @@ __global__ void __launch_bounds__(256) ea_pf_kvslice(Params P) {
 #pragma unroll
             for (int k = 0; k < 32; ++k) {
                 const int ch = 32 * q4 + k;
-                s_v[sp * 8192 + ch * 64 + ((gq ^ ((ch >> 2) & 3)) << 4) + 4 * kt + ii] =
+                s_v[sp * 8192 + ch * 64 + ((gq ^ ((ch >> 1) & 3)) << 4) + 4 * kt + ii] =
                     (uint8_t)(S.dig[sp][k >> 2] >> (8 * (k & 3)));
             }
         if (S.inex) {
@@ -351,45 +351,101 @@ __device__ __forceinline__ bool table_weight(uint32_t tbits, const double* T1s, 
 }
 
 // ------------------------------------------------------------------------------------------------
-// Branch-free certified t = RN32(alpha s) and w = RN24(2^t) = M 2^E for the main kernel.
-// x: the fp64 score in units 2^(lsbq + lk), within dx of the exact integer; a = alpha 2^lsbq.
-// The interval [a x 2^lk - a dx 2^lk, ...] rounds to t0 = RN32(p) when it lies inside the
-// smaller half gap next to t0: 2^(e - 24) for |t0| in [2^e, 2^(e+1)), 2^(e - 25) when |t0| is a
-// power of two (the gap below it is half as wide); |alpha s| <= 2^-25 gives
-// w = 1. 2^f from the fp64 tables (pre-scaled by 2^23) and the cubic, rounded to an integer by
-// adding and subtracting 1.5 * 2^52; certified when |Y - RN(Y)| <= 1/2 - 2^-26 (the fp64
-// evaluation error is below 2^-26.9). Returns false when undecided (the exact path decides).
+// Branch-free certified t = RN32(alpha s) and w = RN24(2^t) = M 2^E for 4 pairs in lock step
+// (independent chains the scheduler interleaves). x: fp64 scores in units 2^(lsbq + lk), within
+// adx / |a| of the exact integers; a = alpha 2^lsbq. The interval around a x 2^lk rounds to
+// t0 = RN32(p) when it lies inside the smaller half gap next to t0: 2^(e - 24) for |t0| in
+// [2^e, 2^(e+1)), 2^(e - 25) when |t0| is a power of two (the gap below it is half as wide);
+// |alpha s| <= 2^-25 gives w = 1. 2^f from the fp64 tables (T1 pre-scaled by 2^23) and the
+// cubic, rounded to an integer by adding and subtracting 1.5 * 2^52; certified when
+// |Y - RN(Y)| <= 1/2 - 2^-26 (the fp64 evaluation error is below 2^-26.9). ok[i] false: the exact
+// path decides.
 // ------------------------------------------------------------------------------------------------
-__device__ __forceinline__ bool lean_weight(double x, double adx, int lk, double a, const double* T1s,
-                                            const double* T2, int* Mout, int* Eout) {
+__device__ __forceinline__ void lean_weight4(const double (&x)[4], const double (&adx)[4], const v4i& lk, double a,
+                                             const double* T1s, const double* T2, int (&M)[4], int (&E)[4],
+                                             bool (&ok)[4]) {
     const double c1 = u64_as_f64(EA_C_BITS[0]), c2 = u64_as_f64(EA_C_BITS[1]), c3 = u64_as_f64(EA_C_BITS[2]);
-    const double xs = ldexp(x, lk);
-    const double adel = ldexp(adx, lk) * (1.0 + 0x1p-50);
-    const double p = a * xs;
-    const double pe = __fma_rn(a, xs, -p);
-    const float tf = (float)p;
-    double d0 = (double)tf;
-    const double r = (p - d0) + pe;
-    // half the gap to the neighbours of t0: 2^(e - 24), or 2^(e - 25) below a power of two
-    const uint32_t hx = (uint32_t)__double2hiint(d0) & 0x7FF00000u;
-    const uint32_t hsh = (__float_as_uint(tf) & 0x7FFFFFu) ? (24u << 20) : (25u << 20);
-    const double h = __hiloint2double((int)(hx - hsh), 0);
-    const bool tiny = fabs(p) + fabs(pe) + adel <= 0x1p-25 * (1.0 - 0x1p-20);
-    const double ad0 = fabs(d0);
-    bool ok = tiny || (fabs(r) * (1.0 + 0x1p-52) + adel + 0x1p-1060 < h && ad0 >= 0x1p-24 && ad0 < 0x1p30);
-    d0 = tiny ? 0.0 : d0;
-    const double fl = floor(d0);
-    const double f = d0 - fl;
-    const int i = ((int)(f * 65536.0)) & 0xFFFF;
-    const double rr = __fma_rn(-(double)i, 0x1p-16, f);
-    const double poly = rr * __fma_rn(rr, __fma_rn(rr, c3, c2), c1);
-    const double aa = T1s[i >> 8] * T2[i & 255];
-    const double Y = __fma_rn(aa, poly, aa);
-    const double Yr = (Y + 0x1.8p52) - 0x1.8p52;
-    ok = ok && fabs(Y - Yr) <= 0.5 - 0x1p-26;
-    *Mout = (int)Yr;
-    *Eout = (int)fl - 23;
-    return ok;
+    double p[4], pe[4], d0[4], adel[4];
+    int idx[4];
+    double f[4], fl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const double xs = ldexp(x[i], lk[i]);
+        adel[i] = ldexp(adx[i], lk[i]) * (1.0 + 0x1p-50);
+        p[i] = a * xs;
+        pe[i] = __fma_rn(a, xs, -p[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float tf = (float)p[i];
+        const double t0 = (double)tf;
+        const double r = (p[i] - t0) + pe[i];
+        const uint32_t hx = (uint32_t)__double2hiint(t0) & 0x7FF00000u;
+        const uint32_t hsh = (__float_as_uint(tf) & 0x7FFFFFu) ? (24u << 20) : (25u << 20);
+        const double h = __hiloint2double((int)(hx - hsh), 0);
+        const bool tiny = fabs(p[i]) + fabs(pe[i]) + adel[i] <= 0x1p-25 * (1.0 - 0x1p-20);
+        const double at = fabs(t0);
+        const bool inner = (fabs(r) * (1.0 + 0x1p-52) + adel[i] + 0x1p-1060 < h) & (at >= 0x1p-24) & (at < 0x1p30);
+        ok[i] = tiny | inner;
+        d0[i] = tiny ? 0.0 : t0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        fl[i] = floor(d0[i]);
+        f[i] = d0[i] - fl[i];
+        idx[i] = ((int)(f[i] * 65536.0)) & 0xFFFF;
+    }
+    double aa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aa[i] = T1s[idx[i] >> 8] * T2[idx[i] & 255];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const double rr = __fma_rn(-(double)idx[i], 0x1p-16, f[i]);
+        const double poly = rr * __fma_rn(rr, __fma_rn(rr, c3, c2), c1);
+        const double Y = __fma_rn(aa[i], poly, aa[i]);
+        const double Yr = (Y + 0x1.8p52) - 0x1.8p52;
+        ok[i] = ok[i] & (fabs(Y - Yr) <= 0.5 - 0x1p-26);
+        M[i] = (int)Yr;
+        E[i] = (int)fl[i] - 23;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Scores of 16 keys x 16 rows for one key group: straight-line MFMAs over the digit pairs (all 16
+// when WIDE, else digits 1..3 of both: 9) into accumulators of equal weight, then the fp64 value of
+// sum_k acc_k 256^k for this lane's 4 keys. Adjacent accumulators combine exactly in int32
+// (|acc_k| <= 4 pairs x 2 x 64 x 2^14 = 2^23 for any k, and the pairs below reach 2^31 only with
+// k >= 4 of at most 3 pairs: acc_k 256 + acc_(k-1) < 2^30.6 + 2^23); at most 4 fp64 roundings.
+// kb[h]: this lane's K chunk base for dims 64 h + 16 g; qb[h]: its q chunk base (plane 0).
+// ------------------------------------------------------------------------------------------------
+template <bool WIDE>
+__device__ __forceinline__ void score_group(const uint8_t* const (&kb)[2], const uint8_t* const (&qb)[2], int kt,
+                                            double (&x)[4]) {
+    v4i acc[7];
+#pragma unroll
+    for (int k = 0; k < 7; ++k) acc[k] = (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        v4i Bq[4];
+#pragma unroll
+        for (int s = (WIDE ? 0 : 1); s < 4; ++s) Bq[s] = *(const v4i*)(qb[h] + 128 * s);
+#pragma unroll
+        for (int t = (WIDE ? 0 : 1); t < 4; ++t) {
+            const v4i A = *(const v4i*)(kb[h] + t * 8192 + kt * 2048);
+#pragma unroll
+            for (int s = (WIDE ? 0 : 1); s < 4; ++s)
+                acc[s + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bq[s], acc[s + t], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int hi32 = acc[6][i] * 256 + acc[5][i];
+        const int mid32 = acc[4][i] * 256 + acc[3][i];
+        double xx = __fma_rn(__fma_rn((double)hi32, 65536.0, (double)mid32), 256.0, (double)acc[2][i]);
+        if (WIDE) xx = __fma_rn(xx, 65536.0, (double)(acc[1][i] * 256 + acc[0][i]));
+        else xx *= 65536.0;
+        x[i] = xx;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -418,8 +474,20 @@ struct PfX {
     double c;
 };
 
-template <int SPLIT, int NWB>
+template <int SPLIT, int NWB, bool TIMERS>
 __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
+    // phase clocks (TIMERS build): shader cycles summed over waves into P.timers[0..7]:
+    // [0] wait for K + barrier, [1] scores and weights, [2] pair exchange, [3] epoch folds,
+    // [4] weight digits, [5] wait for V + barrier, [6] P.V, [7] barrier after P.V
+    uint64_t tclk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t tprev = TIMERS ? __builtin_amdgcn_s_memtime() : 0;
+    auto tick = [&](int ph) __attribute__((always_inline)) {
+        if (TIMERS) {
+            const uint64_t t = __builtin_amdgcn_s_memtime();
+            tclk[ph] += t - tprev;
+            tprev = t;
+        }
+    };
     constexpr int RPB = 16 * NWB / SPLIT;  // rows per block
     constexpr int NKT = 4 / SPLIT;     // key groups of 16 per wave
     constexpr int NCT = 8 / SPLIT;     // channel tiles of 16 per wave
@@ -470,17 +538,24 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const int kw = wave_max_i(ve);
         if (lane == 0) atomicMax(&s_kend, kw);
     }
-    // q digits of the block's rows into LDS: [row 64][plane 4][128 bytes]; rows past the segment
-    // repeat its last row
+    // q digits of the block's rows into LDS: [row][plane 4][128 bytes], 16-byte chunk c of row r
+    // at chunk c ^ (r & 7) (conflict-free reads across the 8 rows of a lane group); rows past the
+    // segment repeat its last row
     for (int c = tid; c < RPB * 32; c += 64 * NWB) {
         const int r = c >> 5, q16 = c & 31;
         const int lrr = min(rbk * RPB + r, P.r_seg - 1);
         int tt;
         const int64_t gr = seg_row(P, b, hk, lrr, &tt);
-        *(uint4*)(smem + PF_OFF_Q + r * 512 + q16 * 16) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
+        *(uint4*)(smem + PF_OFF_Q + r * 512 + ((q16 ^ (r & 7)) << 4)) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
     }
-    // this lane's q digits (B operand of the score MFMA): row j, dims 64 h + 16 g .. + 15, plane s
-    const uint8_t* const qlds = smem + PF_OFF_Q + (rg * 16 + j) * 512 + 16 * g;
+    // this lane's q digits (B operand of the score MFMA): row j, dims 64 h + 16 g .. + 15, plane s:
+    // chunk 8 s + 4 h + g of the row, swizzled
+    const uint8_t* const qlds = smem + PF_OFF_Q + (rg * 16 + j) * 512;
+    // (8 s + 4 h + g) ^ (j & 7) = 8 s + ((4 h + g) ^ (j & 7)): one base per h, plane s at + 128 s
+    const uint8_t* const qb[2] = {qlds + ((g ^ (j & 7)) << 4), qlds + (((4 + g) ^ (j & 7)) << 4)};
+    // K operand: key 16 kt + j, chunk (4 h + g) ^ (j & 7), plane t at + 8192 t, key group at + 2048 kt
+    const uint8_t* const kb[2] = {smem + PF_OFF_K + j * 128 + ((g ^ (j & 7)) << 4),
+                                  smem + PF_OFF_K + j * 128 + (((4 + g) ^ (j & 7)) << 4)};
     const PfQMeta qm = ((const PfQMeta*)P.pfqm)[grow];
     const bool needq = __ballot(rvalid && (qm.flags & 1)) != 0;
     // |a| times the fold error factor 6.01 u and sum_i A_q,i: the score bound is this * A_k
@@ -537,7 +612,9 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     for (int cc = 0; cc < NCT; ++cc)
 #pragma unroll
         for (int k = 0; k < 7; ++k) pacc[cc][k] = (v4i){0, 0, 0, 0};
-    double EVs = 0.0;  // inexact V elements of the epoch's tiles, times (2^38 + 1) / 2
+    double EVs[NCT];  // per channel: inexact V elements of the epoch's tiles, times (2^38 + 1) / 2
+#pragma unroll
+    for (int cc = 0; cc < NCT; ++cc) EVs[cc] = 0.0;
     int ep_tiles = 0;
     bool had_fold = false;  // scr holds the sums of earlier epochs
     uint32_t failbits = 0;
@@ -556,8 +633,10 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         int nf_pair = 0;  // the pair's nfrac (epoch so far)
         bool k_next = false;
         if (!last) {
+            tick(7);
             wait_vm<NKI>();   // K(it) and its metadata landed; V(it) (NKI instructions) may be in flight
             __syncthreads();  // for every wave
+            tick(0);
             k_next = it + 1 < ntiles;
             const int tfl = TM->tfl;
             const bool lossy = lossy_q || (tfl & 32);
@@ -566,60 +645,43 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
 #pragma unroll
             for (int kk = 0; kk < NKT; ++kk) {
                 const int kt = NKT * hh + kk;
-                v4i acc[7];
-#pragma unroll
-                for (int k = 0; k < 7; ++k) acc[k] = (v4i){0, 0, 0, 0};
-                const bool nk = (tfl >> kt) & 1;
-                const bool wide = needq || nk;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        if (t == 0 && !nk) continue;
-                        const v4i A =
-                            *(const v4i*)(Kt + t * 8192 + (16 * kt + j) * 128 + (((4 * h + g) ^ (j & 7)) << 4));
-#pragma unroll
-                        for (int s = 0; s < 4; ++s) {
-                            if (s == 0 && !needq) continue;
-                            const v4i Bq = *(const v4i*)(qlds + 128 * s + 64 * h);
-                            acc[s + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bq, acc[s + t], 0, 0, 0);
-                        }
-                    }
-                }
+                const bool wide = needq || ((tfl >> kt) & 1);
+                double x[4];
+                if (wide) score_group<true>(kb, qb, kt, x);
+                else score_group<false>(kb, qb, kt, x);
                 const v4i lsbk4 = *(const v4i*)&TM->lsbk[16 * kt + 4 * g];
                 const v4i kfl4 = *(const v4i*)&TM->kfl[16 * kt + 4 * g];
                 const v4i vl4 = *(const v4i*)&TM->vlsb[16 * kt + 4 * g];
                 const double2 kA01 = *(const double2*)&TM->kA[16 * kt + 4 * g];
                 const double2 kA23 = *(const double2*)&TM->kA[16 * kt + 4 * g + 2];
                 const double kA[4] = {kA01.x, kA01.y, kA23.x, kA23.y};
+                double adx[4];
+                bool vis[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = 16 * kt + 4 * g + i;
-                    const int n = it * 64 + key;
+                    const int n = it * 64 + 16 * kt + 4 * g + i;
                     const int ti = n - tbase;
-                    const bool vis = n < slen && (n < kvl || (ti >= 0 && ti < 64 && ((tmk >> ti) & 1)));
-                    double x = (double)acc[6][i];
+                    const bool intree = ((unsigned)ti < 64u) & (((tmk >> (ti & 63)) & 1ull) != 0);
+                    vis[i] = (n < slen) & ((n < kvl) | intree);
+                    adx[i] = adq * kA[i];
+                }
+                if (lossy) {
 #pragma unroll
-                    for (int k = 5; k >= 2; --k) x = __fma_rn(x, 256.0, (double)acc[k][i]);
-                    if (wide) {
-                        x = __fma_rn(x, 256.0, (double)acc[1][i]);
-                        x = __fma_rn(x, 256.0, (double)acc[0][i]);
-                    } else {
-                        x *= 65536.0;
-                    }
-                    const int kf = kfl4[i];
-                    double adx = adq * kA[i];
-                    if (lossy)
-                        adx = __fma_rn(aqL, TM->kX[key] + 1.0, __fma_rn((double)(kf >> 8), aqX, adx));
-                    int M, E;
-                    const bool ok = lean_weight(x, adx, lsbk4[i], qm.a, T1s, T2, &M, &E);
-                    const bool kbad = kf & 1;
-                    const bool good = vis && ok && !kbad;
-                    if (vis && kbad) dom = 1;
-                    if (vis && !ok && !kbad) slowmask |= 1u << (4 * kk + i);
-                    Mk[kk][i] = good ? M : 0;
-                    Ek[kk][i] = E;
-                    if (good) gm = max(gm, E + vl4[i]);
+                    for (int i = 0; i < 4; ++i)
+                        adx[i] = __fma_rn(aqL, TM->kX[16 * kt + 4 * g + i] + 1.0, __fma_rn((double)(kfl4[i] >> 8), aqX, adx[i]));
+                }
+                int M[4], E[4];
+                bool ok[4];
+                lean_weight4(x, adx, lsbk4, qm.a, T1s, T2, M, E, ok);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool kbad = kfl4[i] & 1;
+                    const bool good = vis[i] & ok[i] & !kbad;
+                    dom |= (vis[i] & kbad) ? 1 : 0;
+                    slowmask |= (vis[i] & !ok[i] & !kbad) ? (1u << (4 * kk + i)) : 0u;
+                    Mk[kk][i] = good ? M[i] : 0;
+                    Ek[kk][i] = E[i];
+                    gm = max(gm, good ? E[i] + vl4[i] : INT_MIN);
                 }
             }
             // ---- cold path: exact decision for the pairs the fast path left undecided. The exact
@@ -637,7 +699,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                     int ls = 3;
                     ++nslow;
                     if (!qbad && !((qm.flags >> 8) & 0xFF) && !(kf >> 8)) {
-                        const int8_t* qrow = (const int8_t*)(smem + PF_OFF_Q + (rg * 16 + j) * 512);
+                        const int8_t* qrow = (const int8_t*)qlds;
                         const int8_t* krow = (const int8_t*)(Kt + key * 128);
                         i128 S = 0;
                         for (int c = 0; c < 128; ++c) {
@@ -645,7 +707,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                             int xq = 0, xk = 0;
 #pragma unroll
                             for (int sp = 3; sp >= 0; --sp) {
-                                xq = xq * 256 + (int)qrow[128 * sp + c];
+                                xq = xq * 256 + (int)qrow[(((8 * sp + (c >> 4)) ^ (j & 7)) << 4) | (c & 15)];
                                 xk = xk * 256 + (int)krow[8192 * sp + kc];
                             }
                             S += (i128)((int64_t)xq * (int64_t)xk);
@@ -706,6 +768,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             // when a weight would exceed 2^38 (G - base > 14 for G = E + vlsb)
             gm = max(gm, __shfl_xor(gm, 16, 64));
             gm = max(gm, __shfl_xor(gm, 32, 64));
+            tick(1);
             if (SPLIT == 2) s_x[w * 64 + lane] = PfX{gm, nfrac, 0.0};
             __syncthreads();  // every wave is done with the K planes of tile it
             if (k_next) issue_k(it + 1);
@@ -718,6 +781,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             const bool need_rb = gm != INT_MIN && (base == INT_MIN || gm > base + 14);
             nb = need_rb ? gm - 10 : base;
             do_fold = ep_tiles > 0 && (__ballot(need_rb) != 0 || ep_tiles >= 256);
+            tick(2);
         } else {
             // row totals for the final rounding: this wave's 4 lanes of the row, then the partner
             z += __shfl_xor(z, 16, 64);
@@ -780,7 +844,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                     }
                     h *= 256.0;
                     ha *= 256.0;
-                    double en = 6.02 * 0x1p-53 * ha + EVs + omit + fr[i];
+                    double en = 6.02 * 0x1p-53 * ha + EVs[cc] + omit + fr[i];
                     double nn = h;
                     double2* sp = (double2*)(scr + 2 * (4 * cc + i));
                     if (had_fold) {
@@ -815,10 +879,12 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                     for (int k = 0; k < 7; ++k) pacc[cc][k][i] = 0;
                 }
             }
-            EVs = 0.0;
+#pragma unroll
+            for (int cc = 0; cc < NCT; ++cc) EVs[cc] = 0.0;
             ep_tiles = 0;
             had_fold = !last;
             wait_vm<0>();  // the scr stores are complete (keeps the DMA counts below exact)
+            tick(3);
         }
         if (last) break;
         // ---- move bases, then this wave's weight digits (A operand of the P.V MFMA) and Z
@@ -869,6 +935,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 Wd[4][kt] = (int)d4;
             }
         }
+        tick(4);
         // V(it) landed (only K(it+1) may still be in flight), the pair's digits are in LDS
         if (k_next) {
             if (NWB == 4 || w < 4) wait_vm<NKI + 1>();
@@ -877,6 +944,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             wait_vm<0>();
         }
         __syncthreads();
+        tick(5);
         if (SPLIT == 2) {
 #pragma unroll
             for (int s = 0; s < 5; ++s)
@@ -884,9 +952,9 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 for (int kt = 0; kt < 4; ++kt) Wd[s][kt] = (int)wd_r[(kt >> 1) * 640 + (s * 2 + (kt & 1)) * 64];
         }
         // ---- P.V: pacc[cc][s + t - 1] += W digits s x V digits t (all pairs but (0, 0))
-        // channel 16 (4 hh + cc) + j: the 16-byte slot swizzle (ch >> 2) & 3 = (j >> 2) & 3 does not
-        // depend on cc, so every read is one lane base plus a constant
-        const uint8_t* Vt = smem + PF_OFF_V + (16 * NCT * hh + j) * 64 + ((g ^ ((j >> 2) & 3)) << 4);
+        // channel 16 (NCT hh + cc) + j: the 16-byte slot swizzle (ch >> 1) & 3 = (j >> 1) & 3 does
+        // not depend on cc, so every read is one lane base plus a constant
+        const uint8_t* Vt = smem + PF_OFF_V + (16 * NCT * hh + j) * 64 + ((g ^ ((j >> 1) & 3)) << 4);
 #pragma unroll
         for (int cc = 0; cc < NCT; ++cc) {
 #pragma unroll
@@ -900,8 +968,10 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 }
             }
         }
-        EVs += TM->EVt;
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TM->EV[16 * (NCT * hh + cc) + j];
         ++ep_tiles;
+        tick(6);
         __syncthreads();  // every wave is done with the V buffer and the digit exchange
         if (it + 1 < ntiles) issue_v(it + 1);
     }
@@ -927,6 +997,11 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 else ((uint16_t*)P.out)[o] = (uint16_t)bits;
             }
         }
+    }
+    if (TIMERS && lane == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
+        atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)ntiles);
     }
     if (P.stats) {
         const int st5 = wave_sum_i(nunc_s), st6 = wave_sum_i(nunc_w), st8 = wave_sum_i(nslow);
@@ -1018,10 +1093,11 @@ int ea::ea_launch_prefill(const Params& P, hipStream_t st) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [] {
-        attr_err = hipFuncSetAttribute((const void*)ea_pf_main<2, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
-        if (attr_err == hipSuccess)
-            attr_err = hipFuncSetAttribute((const void*)ea_pf_main<2, 8>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           PF_LDS);
+        const void* fns[3] = {(const void*)ea_pf_main<2, 4, false>, (const void*)ea_pf_main<2, 4, true>,
+                              (const void*)ea_pf_main<2, 8, false>};
+        for (const void* f : fns)
+            if (attr_err == hipSuccess)
+                attr_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
     });
     if (attr_err != hipSuccess) return -100 - (int)attr_err;
     Params Pc = P;
@@ -1040,8 +1116,9 @@ int ea::ea_launch_prefill_main(const Params& P, hipStream_t st) {
     Params Pc = P;
     if (P.nseg > 0 && P.pf_nrb > 0) {
         const dim3 grid((unsigned)(P.nseg * P.pf_nrb));
-        if (pf_rows_per_block() == 64) hipLaunchKernelGGL((ea_pf_main<2, 8>), grid, dim3(512), PF_LDS, st, Pc);
-        else hipLaunchKernelGGL((ea_pf_main<2, 4>), grid, dim3(256), PF_LDS, st, Pc);
+        if (P.timers) hipLaunchKernelGGL((ea_pf_main<2, 4, true>), grid, dim3(256), PF_LDS, st, Pc);
+        else if (pf_rows_per_block() == 64) hipLaunchKernelGGL((ea_pf_main<2, 8, false>), grid, dim3(512), PF_LDS, st, Pc);
+        else hipLaunchKernelGGL((ea_pf_main<2, 4, false>), grid, dim3(256), PF_LDS, st, Pc);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return -100 - (int)e;
     }
