@@ -10,6 +10,11 @@ q, out, block table), the split kernel's roofline fraction timed with HIP events
 stream, bit-exactness against the committed golden hash, the tier-1 fallback-row rate, and the
 reference's own C++ certified CPU kernel (oracle/_ref, built from the reference source) timed on
 this host's cores as the CPU baseline.
+
+The "prefill" object holds config C3 (causal prefill, 4096 tokens, 16 query / 8 KV heads) on the
+int8-MFMA prefill kernel: step time, algorithmic int8 ops (visible pairs x 6912) over the
+ea_pf_main launch time as a fraction of the dense int8 MFMA peak, bit-exactness and fallback rows.
+`--only C3` runs just that workload (for profiler runs).
 """
 
 from __future__ import annotations
@@ -115,6 +120,85 @@ def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
             "wall_s": round(t, 3)}, res
 
 
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, vendor figure (256 CUs, 2.4 GHz)
+PF_TRAFFIC = os.path.join(ROOT, "profiles", "ea_pf_main_C3_traffic.md")
+
+
+def prefill_ops(prob: dict) -> int:
+    """Algorithmic int8 MFMA work of a step: visible query-key pairs x (3x4 score slice products
+    + 5x3 P.V slice products) x 128 x 2 ops (bound and recompute products excluded)."""
+    g = prob["geom"]
+    kv = prob["kv_len"].astype(np.int64)
+    pairs = int(kv.sum()) * g["num_q_heads"]
+    return pairs * (12 * g["head_dim"] * 2 + 15 * g["head_dim_v"] * 2), pairs
+
+
+def read_traffic(path: str):
+    if os.path.exists(path):
+        for ln in open(path):
+            if ln.startswith("traffic_bytes_per_launch:"):
+                return int(ln.split(":")[1])
+    return None
+
+
+def run_config(name: str, steps: int, warmup: int, splits: int = 0):
+    """Generate config `name`, run warm-up steps, check the bits against the golden hash, then time
+    `steps` steps with HIP events between the kernels (recorded on the launch stream)."""
+    import torch
+    from exactattention_amd import configs
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    t0 = time.time()
+    prob = configs.CONFIGS[name]()
+    ab = configs.alpha_bits()
+    gen_s = time.time() - t0
+    dp = DeviceProblem(prob, "bf16", splits, "cuda:0")
+    ev = HipEvents(5 * steps)
+    for _ in range(warmup):
+        launch_hip(dp, ab)
+    torch.cuda.synchronize()
+    out = dp.out.cpu().numpy().view(np.uint16)
+    golden = json.load(open(GOLDEN)).get(name, {}).get("sha256") if os.path.exists(GOLDEN) else None
+    bit_exact = (hashlib.sha256(out.tobytes()).hexdigest() == golden) if golden else None
+    dp.stats.zero_()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        launch_hip(dp, ab, events=ctypes.cast(ev.slot(5 * i), ctypes.POINTER(ctypes.c_void_p)))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    phases = np.array([[ev.ms(5 * i + j, 5 * i + j + 1) for j in range(4)] for i in range(steps)])
+    ev.close()
+    st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    return {"prob": prob, "ab": ab, "dp": dp, "out": out, "gen_s": gen_s, "bit_exact": bit_exact,
+            "ms_step": (t1 - t0) * 1e3 / steps, "phases": phases.mean(0), "stats": st}
+
+
+def prefill_line(steps: int, warmup: int) -> dict:
+    """C3 (causal prefill, 4096 tokens) on the int8-MFMA prefill kernel."""
+    import torch
+    r = run_config("C3", steps, warmup)
+    ops, pairs = prefill_ops(r["prob"])
+    st = r["stats"]
+    slice_ms, main_ms, _, t2_ms = (float(x) for x in r["phases"])
+    tops = ops / (main_ms * 1e-3) / 1e12
+    line = {
+        "workload": "C3 causal prefill (T=4096, 16 q / 8 KV heads, d=128)", "ms_per_step": round(r["ms_step"], 5),
+        "tops_step": round(ops / (r["ms_step"] * 1e-3) / 1e12, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s (int8)",
+                     "frac": round(tops / MFMA_I8_PEAK_TOPS, 4), "traffic": read_traffic(PF_TRAFFIC),
+                     "kernel": "ea_pf_main", "kernel_ms": round(main_ms, 5)},
+        "kernels_ms": {"slice": round(slice_ms, 5), "ea_pf_main": round(main_ms, 5), "tier2": round(t2_ms, 5)},
+        "algorithmic_ops_per_step": ops, "pairs_per_step": pairs,
+        "bit_exact": r["bit_exact"], "prefill_kernel_rows": st["prefill_kernel_rows"],
+        "fallback_rows_pct": round(100.0 * st["tier1_flagged"] / max(1, st["rows"]), 4),
+        "epoch_folds": st["prefill_epoch_folds"], "cold_waves": st["prefill_cold_waves"],
+        "input_gen_s": round(r["gen_s"], 1),
+    }
+    del r
+    torch.cuda.empty_cache()
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -122,6 +206,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill measurement")
+    ap.add_argument("--only", choices=("C2", "C3"), default=None,
+                    help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
                     help="after the timed steps, run 5 steps of the phase-clock build and report it")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -142,40 +229,18 @@ def main():
         sys.exit(2)
 
     import torch
-    from exactattention_amd import configs
-    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    from exactattention_amd.hip import launch_hip
 
-    t0 = time.time()
-    prob = configs.c2()
-    ab = configs.alpha_bits()
-    gen_s = time.time() - t0
-    dp = DeviceProblem(prob, "bf16", args.splits, "cuda:0")
+    if args.only == "C3":
+        print(json.dumps({"prefill": prefill_line(args.steps, args.warmup)}), flush=True)
+        return
+    r = run_config("C2", args.steps, args.warmup, args.splits)
+    prob, ab, dp, out, st = r["prob"], r["ab"], r["dp"], r["out"], r["stats"]
     nbytes = algorithmic_bytes(prob)
-    ev = HipEvents(5 * args.steps)
-    for _ in range(args.warmup):
-        launch_hip(dp, ab)
-    torch.cuda.synchronize()
-    out = dp.out.cpu().numpy().view(np.uint16)
-    golden = json.load(open(GOLDEN)).get("C2", {}).get("sha256") if os.path.exists(GOLDEN) else None
-    bit_exact = (hashlib.sha256(out.tobytes()).hexdigest() == golden) if golden else None
-    dp.stats.zero_()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        launch_hip(dp, ab, events=ctypes.cast(ev.slot(5 * i), ctypes.POINTER(ctypes.c_void_p)))
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    phases = np.array([[ev.ms(5 * i + j, 5 * i + j + 1) for j in range(4)] for i in range(args.steps)])
-    ev.close()
-    split_ms = float(phases[:, 1].mean())
-    st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    ms_step = r["ms_step"]
+    split_ms = float(r["phases"][1])
     flagged_pct = 100.0 * st["tier1_flagged"] / max(1, st["rows"])
-    traffic = None  # HBM bytes per split launch, from the committed rocprofv3 PMC summary
-    if os.path.exists(TRAFFIC):
-        for ln in open(TRAFFIC):
-            if ln.startswith("traffic_bytes_per_launch:"):
-                traffic = int(ln.split(":")[1])
+    traffic = read_traffic(TRAFFIC)  # HBM bytes per decode launch, from the committed rocprofv3 PMC summary
     achieved = nbytes / (split_ms * 1e-3) / 1e9
     line = {
         "metric": METRIC, "value": round(nbytes / (ms_step * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
@@ -187,12 +252,12 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "ea_decode",
                      "kernel_ms": round(split_ms, 5)},
-        "kernels_ms": {k: round(float(phases[:, j].mean()), 5) for j, k in enumerate(("prep", "split", "combine",
-                                                                                      "tier2"))},
-        "bit_exact": bit_exact, "fallback_rows_pct": round(flagged_pct, 4),
+        "kernels_ms": {k: round(float(r["phases"][j]), 5) for j, k in enumerate(("prep", "split", "combine",
+                                                                                  "tier2"))},
+        "bit_exact": r["bit_exact"], "fallback_rows_pct": round(flagged_pct, 4),
         "tier2_certified_rows": st["tier2_certified"], "uncertified_rows": st["uncertified"],
         "tier1_causes": {k: st[k] for k in ("uncertified_scores", "undecided_weights", "uncertified_final", "slow_path_scores")},
-        "input_gen_s": round(gen_s, 1),
+        "input_gen_s": round(r["gen_s"], 1),
     }
     if args.timers:
         from exactattention_amd.hip import TIMER_PHASES
@@ -205,7 +270,11 @@ def main():
         line["phase_clocks"] = {"cycles_per_wave_tile": {k: round(tv[i] / max(1.0, 4 * tv[7]), 1)
                                                          for i, k in enumerate(TIMER_PHASES[:7])},
                                 "share": {k: round(tv[i] / tot, 4) for i, k in enumerate(TIMER_PHASES[:7])}}
-    if not args.no_cpu:
+    del r, dp
+    torch.cuda.empty_cache()
+    if args.only is None and not args.no_prefill:
+        line["prefill"] = prefill_line(max(5, min(args.steps, 20)), 2)
+    if args.only is None and not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         cb, cres = cpu_baseline(prob, ab, threads)
         line["cpu_baseline"] = cb
