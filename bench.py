@@ -189,9 +189,10 @@ def prefill_line(steps: int, warmup: int) -> dict:
                      "kernel": "ea_pf_main", "kernel_ms": round(main_ms, 5)},
         "kernels_ms": {"slice": round(slice_ms, 5), "ea_pf_main": round(main_ms, 5), "tier2": round(t2_ms, 5)},
         "algorithmic_ops_per_step": ops, "pairs_per_step": pairs,
-        "bit_exact": r["bit_exact"], "prefill_kernel_rows": st["prefill_kernel_rows"],
+        "bit_exact": r["bit_exact"], "prefill_kernel_rows_per_step": st["prefill_kernel_rows"] // steps,
         "fallback_rows_pct": round(100.0 * st["tier1_flagged"] / max(1, st["rows"]), 4),
-        "epoch_folds": st["prefill_epoch_folds"], "cold_waves": st["prefill_cold_waves"],
+        "per_step": {"epoch_folds": st["prefill_epoch_folds"] / steps, "cold_waves": st["prefill_cold_waves"] / steps,
+                     "cold_pairs": st["slow_path_scores"] / steps},
         "input_gen_s": round(r["gen_s"], 1),
     }
     del r
