@@ -49,6 +49,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr double PF_U = 0x1p-53 * (1.0 + 0x1p-28);
+#ifndef PF_VALU_PER_MFMA
+#define PF_VALU_PER_MFMA 5
+#endif
 // 1.5 * 2^52 + 0x8080808080: y = Wf + this has the biased digits of Wf in its low 40 bits
 constexpr double PF_C40 = 6755399441055744.0 + (double)0x8080808080ull;
 
@@ -272,7 +275,7 @@ __global__ void __launch_bounds__(256) ea_pf_kvslice(Params P) {
         bad = S.bad;
         if (q4 == 0) {
             TM->lsbk[key] = S.lsb;
-            TM->kA[key] = S.amax;
+            TM->kA[key] = ldexp(S.amax, S.lsb);  // in absolute units: the score bound needs no rescale
             TM->kX[key] = (double)S.xmax;
         }
         int tf = (S.need4 ? 1 : 0) << (key >> 4);
@@ -352,56 +355,55 @@ __device__ __forceinline__ bool table_weight(uint32_t tbits, const double* T1s, 
 
 // ------------------------------------------------------------------------------------------------
 // Branch-free certified t = RN32(alpha s) and w = RN24(2^t) = M 2^E for 4 pairs in lock step
-// (independent chains the scheduler interleaves). x: fp64 scores in units 2^(lsbq + lk), within
-// adx / |a| of the exact integers; a = alpha 2^lsbq. The interval around a x 2^lk rounds to
-// t0 = RN32(p) when it lies inside the smaller half gap next to t0: 2^(e - 24) for |t0| in
-// [2^e, 2^(e+1)), 2^(e - 25) when |t0| is a power of two (the gap below it is half as wide);
-// |alpha s| <= 2^-25 gives w = 1. 2^f from the fp64 tables (T1 pre-scaled by 2^23) and the
-// cubic, rounded to an integer by adding and subtracting 1.5 * 2^52; certified when
-// |Y - RN(Y)| <= 1/2 - 2^-26 (the fp64 evaluation error is below 2^-26.9). ok[i] false: the exact
-// path decides.
+// (independent chains the scheduler interleaves). xs: fp64 scores in units 2^lsbq; a = alpha 2^lsbq;
+// adel >= (1 + 2^-50) |a| |xs - exact| (the score bound with its rounding slack). p + pe = a xs
+// exactly (FMA). The interval around p + pe rounds to t0 = RN32(p) when |p + pe - t0| + adel is
+// below the smaller half gap next to t0 (2^(e - 24) for |t0| in [2^e, 2^(e+1)), 2^(e - 25) when
+// |t0| is a power of two: the gap below it is half as wide); |alpha s| <= 2^-25 gives w = 1. 2^f from the
+// fp64 tables (T1 pre-scaled by 2^23) and the cubic in r = f - j 2^-16, evaluated on
+// rr = 2^16 r with the coefficients scaled by 2^-16, 2^-32, 2^-48 (every intermediate is the
+// unscaled evaluation times a power of two: the same bits); rounded to an integer by adding and
+// subtracting 1.5 * 2^52; certified when |Y - RN(Y)| <= 1/2 - 2^-26 (the fp64 evaluation error
+// is below 2^-26.9). ok[i] false: the exact path decides.
 // ------------------------------------------------------------------------------------------------
-__device__ __forceinline__ void lean_weight4(const double (&x)[4], const double (&adx)[4], const v4i& lk, double a,
-                                             const double* T1s, const double* T2, int (&M)[4], int (&E)[4],
-                                             bool (&ok)[4]) {
-    const double c1 = u64_as_f64(EA_C_BITS[0]), c2 = u64_as_f64(EA_C_BITS[1]), c3 = u64_as_f64(EA_C_BITS[2]);
-    double p[4], pe[4], d0[4], adel[4];
-    int idx[4];
-    double f[4], fl[4];
+__device__ __forceinline__ void cert4(const double (&xs)[4], const double (&adel)[4], double a, const double* T1s,
+                                      const double* T2, int (&M)[4], int (&E)[4], bool (&ok)[4]) {
+    const double c1 = u64_as_f64(EA_C_BITS[0]) * 0x1p-16, c2 = u64_as_f64(EA_C_BITS[1]) * 0x1p-32,
+                 c3 = u64_as_f64(EA_C_BITS[2]) * 0x1p-48;
+    double d0[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const double xs = ldexp(x[i], lk[i]);
-        adel[i] = ldexp(adx[i], lk[i]) * (1.0 + 0x1p-50);
-        p[i] = a * xs;
-        pe[i] = __fma_rn(a, xs, -p[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float tf = (float)p[i];
+        const double p = a * xs[i];
+        const double pe = __fma_rn(a, xs[i], -p);
+        const float tf = (float)p;
         const double t0 = (double)tf;
-        const double r = (p[i] - t0) + pe[i];
+        const double r = (p - t0) + pe;  // p - t0 is exact; one rounding, covered by 2^-50 below
+        const double at = fabs(t0);
+        // the smaller half gap next to t0: 2^(e - 24), or 2^(e - 25) when |t0| = 2^e
         const uint32_t hx = (uint32_t)__double2hiint(t0) & 0x7FF00000u;
         const uint32_t hsh = (__float_as_uint(tf) & 0x7FFFFFu) ? (24u << 20) : (25u << 20);
         const double h = __hiloint2double((int)(hx - hsh), 0);
-        const bool tiny = fabs(p[i]) + fabs(pe[i]) + adel[i] <= 0x1p-25 * (1.0 - 0x1p-20);
-        const double at = fabs(t0);
-        const bool inner = (fabs(r) * (1.0 + 0x1p-52) + adel[i] + 0x1p-1060 < h) & (at >= 0x1p-24) & (at < 0x1p30);
+        const bool tiny = fabs(p) + fabs(pe) + adel[i] <= 0x1p-25 * (1.0 - 0x1p-20);
+        const bool inner = (__fma_rn(fabs(r), 1.0 + 0x1p-50, adel[i]) < h) & (at >= 0x1p-24) & (at < 0x1p30);
         ok[i] = tiny | inner;
         d0[i] = tiny ? 0.0 : t0;
     }
+    double fl[4], rr[4];
+    int idx[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         fl[i] = floor(d0[i]);
-        f[i] = d0[i] - fl[i];
-        idx[i] = ((int)(f[i] * 65536.0)) & 0xFFFF;
+        const double t16 = (d0[i] - fl[i]) * 65536.0;  // exact: d0 is an fp32 value below 2^30
+        const double fi = floor(t16);
+        idx[i] = (int)fi;
+        rr[i] = t16 - fi;
     }
     double aa[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) aa[i] = T1s[idx[i] >> 8] * T2[idx[i] & 255];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const double rr = __fma_rn(-(double)idx[i], 0x1p-16, f[i]);
-        const double poly = rr * __fma_rn(rr, __fma_rn(rr, c3, c2), c1);
+        const double poly = rr[i] * __fma_rn(rr[i], __fma_rn(rr[i], c3, c2), c1);
         const double Y = __fma_rn(aa[i], poly, aa[i]);
         const double Yr = (Y + 0x1.8p52) - 0x1.8p52;
         ok[i] = ok[i] & (fabs(Y - Yr) <= 0.5 - 0x1p-26);
@@ -412,18 +414,12 @@ __device__ __forceinline__ void lean_weight4(const double (&x)[4], const double 
 
 // ------------------------------------------------------------------------------------------------
 // Scores of 16 keys x 16 rows for one key group: straight-line MFMAs over the digit pairs (all 16
-// when WIDE, else digits 1..3 of both: 9) into accumulators of equal weight, then the fp64 value of
-// sum_k acc_k 256^k for this lane's 4 keys. Adjacent accumulators combine exactly in int32
-// (|acc_k| <= 4 pairs x 2 x 64 x 2^14 = 2^23 for any k, and the pairs below reach 2^31 only with
-// k >= 4 of at most 3 pairs: acc_k 256 + acc_(k-1) < 2^30.6 + 2^23); at most 4 fp64 roundings.
-// kb[h]: this lane's K chunk base for dims 64 h + 16 g; qb[h]: its q chunk base (plane 0).
+// when WIDE, else digits 1..3 of both: 9) into accumulators of equal weight s + t. kb[h]: this
+// lane's K chunk base for dims 64 h + 16 g; qb[h]: its q chunk base (plane 0).
 // ------------------------------------------------------------------------------------------------
 template <bool WIDE>
-__device__ __forceinline__ void score_group(const uint8_t* const (&kb)[2], const uint8_t* const (&qb)[2], int kt,
-                                            double (&x)[4]) {
-    v4i acc[7];
-#pragma unroll
-    for (int k = 0; k < 7; ++k) acc[k] = (v4i){0, 0, 0, 0};
+__device__ __forceinline__ void score_mfma(const uint8_t* const (&kb)[2], const uint8_t* const (&qb)[2], int kt,
+                                           v4i (&acc)[7]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         v4i Bq[4];
@@ -437,48 +433,86 @@ __device__ __forceinline__ void score_group(const uint8_t* const (&kb)[2], const
                 acc[s + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bq[s], acc[s + t], 0, 0, 0);
         }
     }
+}
+
+// fp64 value of sum_k acc_k 256^k for this lane's 4 keys, times 2^lk (units 2^lsbq). Adjacent
+// accumulators combine exactly in int32 (|acc_k| <= 4 pairs x 2 x 64 x 2^14 = 2^23 for any k, and
+// the pairs below reach 2^31 only with k >= 4 of at most 3 pairs: acc_k 256 + acc_(k-1) < 2^30.6 +
+// 2^23); 3 fp64 roundings (the score bound allows 4). acc_0 = acc_1 = 0 for a narrow group.
+__device__ __forceinline__ void score_fold(const v4i (&acc)[7], const v4i& lk, double (&xs)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int hi32 = acc[6][i] * 256 + acc[5][i];
         const int mid32 = acc[4][i] * 256 + acc[3][i];
-        double xx = __fma_rn(__fma_rn((double)hi32, 65536.0, (double)mid32), 256.0, (double)acc[2][i]);
-        if (WIDE) xx = __fma_rn(xx, 65536.0, (double)(acc[1][i] * 256 + acc[0][i]));
-        else xx *= 65536.0;
-        x[i] = xx;
+        const int lo32 = acc[1][i] * 256 + acc[0][i];
+        const double xx = __fma_rn(__fma_rn((double)hi32, 65536.0, (double)mid32), 256.0, (double)acc[2][i]);
+        xs[i] = ldexp(__fma_rn(xx, 65536.0, (double)lo32), lk[i]);
     }
 }
 
 // ------------------------------------------------------------------------------------------------
-// Main kernel. Block = 8 waves over 64 consecutive rows (tokens x query heads of one KV head).
+// Main kernel. Block = 4 waves over 32 consecutive rows (tokens x query heads of one KV head).
 // Waves 2 rg and 2 rg + 1 share the 16 rows of row group rg; wave half hh = w & 1 takes the
 // scores and weights of key groups kt = 2 hh, 2 hh + 1 of each tile and the P.V sums of channel
-// tiles ct = 4 hh .. 4 hh + 3. The pair exchanges row maxima and weight digits through LDS.
-// Lane (g = lane / 16, j = lane % 16):
+// tiles ct = 4 hh .. 4 hh + 3. Lane (g = lane / 16, j = lane % 16):
 //   score layout  row j, keys 16 kt + 4 g + i (i = 0..3)
 //   P.V layout    rows 4 g + i, channels 16 ct + j
-// LDS: K and V planes single-buffered (the next tile's K planes load during this tile's weight
-// and P.V phases, its V planes during the next score phase), tile metadata double-buffered, the
-// block's q digits, exp2 tables, the pair exchanges.
+// Software pipeline, one step per tile it:
+//   B1    K(it) and its metadata landed; the pair's weight digits of tile it-1 are in sWD
+//         score MFMAs of tile it (K planes and q digits from LDS)
+//   B1.5  every wave has read the K planes: K(it+1) and its metadata start loading
+//         P.V MFMAs of tile it-1 interleaved with the certification of tile it
+//   B2    pair exchange of row maxima; V(it+1) starts loading into the buffer V(it-1) used;
+//         epoch fold when a base moves; weight digits of tile it to sWD
+// V and the metadata are double-buffered (the two parities are two copies of the step). The DMAs
+// are issued as inline asm, so the compiler adds no waits of its own; barriers are s_barrier after
+// lgkmcnt(0) (no vmcnt(0): DMAs stay in flight across them) and the DMA waits explicit vmcnt
+// counts, in issue order: K(it+1) and its metadata at B1.5, V(it+1) at B2.
 // ------------------------------------------------------------------------------------------------
-constexpr int PF_OFF_V = 0;                      // V planes (32 KB), single buffer
-constexpr int PF_OFF_K = 32768;                  // K planes (32 KB), single buffer
-constexpr int PF_OFF_M = 65536;                  // tile metadata, 2 x 4 KB
-constexpr int PF_OFF_Q = PF_OFF_M + 8192;        // q digits of the block's 64 rows (32 KB)
-constexpr int PF_OFF_T = PF_OFF_Q + 32768;       // T1 * 2^23, T2 (4 KB)
-constexpr int PF_OFF_WD = PF_OFF_T + 4096;       // weight digits: 8 waves x 5 planes x 2 x 64 lanes
-constexpr int PF_OFF_X = PF_OFF_WD + 8 * 2560;   // per-lane exchange: 8 waves x 64 lanes x 16 B
-constexpr int PF_LDS = PF_OFF_X + 8 * 1024;
-
 struct PfX {
     int32_t a, b;
     double c;
 };
 
-template <int SPLIT, int NWB, bool TIMERS>
+// s_waitcnt lgkmcnt(0) + s_barrier: LDS writes of every wave visible, outstanding DMAs untouched
+__device__ __forceinline__ void pf_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 16 bytes per lane from buffer rs at voff + soff into LDS at lds + 16 lane (M0 = lds, wave-
+// uniform). The DMA counts in vmcnt; its consumers wait with wait_vm<n>. The compiler's hazard
+// recognizer does not look inside inline asm: s_nop 4 gives the 5 wait states a VMEM read of an
+// SGPR needs after a VALU write of it (v_readlane of a spilled soffset or descriptor word), which
+// also covers the 1 wait state between an M0 write and an LDS DMA.
+__device__ __forceinline__ void pf_dma(const v4i& rs, uint32_t lds, int voff, int soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const lds_void_t*)p);
+}
+
+// LDS layout (dynamic): the DMA targets first, all below 104 KB
+constexpr int PF_OFF_K = 0;
+constexpr int PF_OFF_V0 = 32768;
+constexpr int PF_OFF_V1 = 65536;
+constexpr int PF_OFF_M0 = 98304;
+constexpr int PF_OFF_M1 = PF_OFF_M0 + 4096;
+constexpr int PF_OFF_Q = PF_OFF_M1 + 4096;  // 32 rows x 512 bytes
+constexpr int PF_OFF_T = PF_OFF_Q + 16384;
+constexpr int PF_OFF_WD = PF_OFF_T + 4096;  // 5 planes x 4 key groups x 2 row groups x 64 lanes x 4 B
+constexpr int PF_OFF_X = PF_OFF_WD + 10240;  // up to 8 waves x 64 lanes x 16 bytes
+constexpr int PF_OFF_KEND = PF_OFF_X + 8192;
+constexpr int PF_LDS = PF_OFF_KEND + 16;
+
+template <int N>
+struct PfPar {
+    static constexpr int value = N;
+};
+
+template <int NWB, bool TIMERS>
 __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     // phase clocks (TIMERS build): shader cycles summed over waves into P.timers[0..7]:
-    // [0] wait for K + barrier, [1] scores and weights, [2] pair exchange, [3] epoch folds,
-    // [4] weight digits, [5] wait for V + barrier, [6] P.V, [7] barrier after P.V
+    // [0] wait for K + barrier, [1] score MFMAs + barrier, [2] P.V + certification,
+    // [3] cold path and bad keys, [4] pair exchange, [5] epoch folds, [6] weight digits, [7] rest
     uint64_t tclk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint64_t tprev = TIMERS ? __builtin_amdgcn_s_memtime() : 0;
     auto tick = [&](int ph) __attribute__((always_inline)) {
@@ -488,16 +522,23 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             tprev = t;
         }
     };
-    constexpr int RPB = 16 * NWB / SPLIT;  // rows per block
-    constexpr int NKT = 4 / SPLIT;     // key groups of 16 per wave
-    constexpr int NCT = 8 / SPLIT;     // channel tiles of 16 per wave
-    constexpr int NKI = 32 / NWB;      // K (and V) DMA instructions per wave and tile
+    constexpr int SPLIT = NWB / 2;         // waves per row group of 16 rows
+    constexpr int RPB = 16 * NWB / SPLIT;  // rows per block (32)
+    constexpr int NKT = 4 / SPLIT;         // key groups of 16 per wave
+    constexpr int NCT = 8 / SPLIT;         // channel tiles of 16 per wave
+    constexpr int NKI = 32 / NWB;          // K (and V) DMA instructions per wave and tile
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int s_kend;
-    double* const T1s = (double*)(smem + PF_OFF_T);
-    double* const T2 = T1s + 256;
-    uint32_t* const s_wd = (uint32_t*)(smem + PF_OFF_WD);  // [wave][plane 5][2][lane 64]
-    PfX* const s_x = (PfX*)(smem + PF_OFF_X);              // [wave][lane 64]
+    uint8_t* const sK = smem + PF_OFF_K;     // K planes of the current tile
+    uint8_t* const sV0 = smem + PF_OFF_V0;   // V planes, even tiles
+    uint8_t* const sV1 = smem + PF_OFF_V1;   // V planes, odd tiles
+    uint8_t* const sM0 = smem + PF_OFF_M0;   // tile metadata, even tiles
+    uint8_t* const sM1 = smem + PF_OFF_M1;   // tile metadata, odd tiles
+    uint8_t* const sQ = smem + PF_OFF_Q;     // q digits of the block's rows
+    double* const sT1 = (double*)(smem + PF_OFF_T);  // T1 * 2^23, then T2
+    double* const sT2 = sT1 + 256;
+    uint32_t* const sWD = (uint32_t*)(smem + PF_OFF_WD);  // weight digits [wave][plane 5][2][lane]
+    PfX* const sX = (PfX*)(smem + PF_OFF_X);              // pair exchange [wave][lane]
+    int& s_kend = *(int*)(smem + PF_OFF_KEND);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = w / SPLIT, hh = w % SPLIT;
@@ -509,16 +550,20 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     const int64_t b = seg / Hkv;
     const int hk = seg % Hkv;
     const int T = P.g.num_tokens;
-    uint32_t* const wd_w = s_wd + w * 640 + lane;               // this wave's digit planes (SPLIT 2)
-    const uint32_t* const wd_r = s_wd + (w & ~1) * 640 + lane;  // the pair's, in key-group order
+    constexpr int WDS = 5 * NKT * 64;  // digit dwords per wave: [plane 5][NKT][lane 64]
+    uint32_t* const wd_w = sWD + w * WDS + lane;                    // this wave's digit planes
+    const uint32_t* const wd_r = sWD + (rg * SPLIT) * WDS + lane;  // the row group's, by key group
     // per-lane scratch: fp64 sums of completed epochs, then the final quotients
     double* const scr = P.pfscr + (((int64_t)blockIdx.x * NWB + w) * 64 + lane) * (8 * NCT);
 
     if (tid == 0) s_kend = 0;
     if (tid < 256) {
-        T1s[tid] = u64_as_f64(EA_T1_BITS[tid]) * 8388608.0;  // 2^23: exact
-        T2[tid] = u64_as_f64(EA_T2_BITS[tid]);
+        sT1[tid] = u64_as_f64(EA_T1_BITS[tid]) * 8388608.0;  // 2^23: exact
+        sT2[tid] = u64_as_f64(EA_T2_BITS[tid]);
     }
+    // step 0 runs the P.V of "tile -1" on zero weight digits and adds the zero EV of sM1
+    for (int c = tid; c < NWB * WDS; c += 64 * NWB) sWD[c] = 0u;
+    if (tid < 128) ((PfTileMeta*)sM1)->EV[tid] = 0.0;
     // ---- this lane's row in the score layout
     const int lr = rbk * RPB + rg * 16 + j;
     const bool rvalid = lr < P.r_seg;
@@ -533,6 +578,8 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     int ve = kvl;
     if (tmk) ve = max(ve, tbase + 64 - (int)__clzll(tmk));
     ve = min(ve, slen);
+    // keys below kvmin are visible to every row of the wave (and of its partner)
+    const int kvmin = wave_min_i(rvalid ? min(kvl, slen) : INT_MAX);
     __syncthreads();  // s_kend initialised
     {
         const int kw = wave_max_i(ve);
@@ -546,20 +593,19 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const int lrr = min(rbk * RPB + r, P.r_seg - 1);
         int tt;
         const int64_t gr = seg_row(P, b, hk, lrr, &tt);
-        *(uint4*)(smem + PF_OFF_Q + r * 512 + ((q16 ^ (r & 7)) << 4)) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
+        *(uint4*)(sQ + r * 512 + ((q16 ^ (r & 7)) << 4)) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
     }
     // this lane's q digits (B operand of the score MFMA): row j, dims 64 h + 16 g .. + 15, plane s:
-    // chunk 8 s + 4 h + g of the row, swizzled
-    const uint8_t* const qlds = smem + PF_OFF_Q + (rg * 16 + j) * 512;
-    // (8 s + 4 h + g) ^ (j & 7) = 8 s + ((4 h + g) ^ (j & 7)): one base per h, plane s at + 128 s
+    // chunk 8 s + 4 h + g of the row, swizzled; (8 s + 4 h + g) ^ (j & 7) = 8 s + ((4 h + g) ^ (j & 7))
+    const uint8_t* const qlds = sQ + (rg * 16 + j) * 512;
     const uint8_t* const qb[2] = {qlds + ((g ^ (j & 7)) << 4), qlds + (((4 + g) ^ (j & 7)) << 4)};
     // K operand: key 16 kt + j, chunk (4 h + g) ^ (j & 7), plane t at + 8192 t, key group at + 2048 kt
-    const uint8_t* const kb[2] = {smem + PF_OFF_K + j * 128 + ((g ^ (j & 7)) << 4),
-                                  smem + PF_OFF_K + j * 128 + (((4 + g) ^ (j & 7)) << 4)};
+    const uint8_t* const kb[2] = {sK + j * 128 + ((g ^ (j & 7)) << 4), sK + j * 128 + (((4 + g) ^ (j & 7)) << 4)};
     const PfQMeta qm = ((const PfQMeta*)P.pfqm)[grow];
     const bool needq = __ballot(rvalid && (qm.flags & 1)) != 0;
-    // |a| times the fold error factor 6.01 u and sum_i A_q,i: the score bound is this * A_k
-    const double adq = fabs(qm.a) * 6.01 * 0x1p-53 * qm.qA;
+    // the score bound per pair is adq * kA 2^lk: |a| times the fold error factor 6.01 u times
+    // sum_i A_q,i, with 2^-48 of slack for the roundings of this product and of adq * kAs
+    const double adq = fabs(qm.a) * (6.01 * 0x1p-53) * qm.qA * (1.0 + 0x1p-48);
     const double aqL = fabs(qm.a) * 0.5 * (double)((qm.flags >> 8) & 0xFF);
     const double aqX = fabs(qm.a) * 0.5 * (qm.qX + 1.0);
     const bool lossy_q = __ballot(rvalid && ((qm.flags >> 8) & 0xFF)) != 0;
@@ -567,36 +613,40 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     int dom = (rvalid && qbad) ? 1 : 0;  // NaN/inf in q: a domain error (docs/SPEC.md)
     int unc = 0;
     int nslow = 0, nunc_s = 0, nunc_w = 0;
-    __syncthreads();  // s_kend final, tables visible
+    __syncthreads();  // s_kend final, tables and q digits visible
     const int kend = s_kend;
     const int ntiles = (kend + 63) >> 6;
+    const double* const T1s = sT1;
+    const double* const T2 = sT2;
 
-    // tile DMA: K planes and metadata into K buffer `buf`, V planes into the V buffer. Per wave:
-    // 4 K instructions (+1 metadata for waves 0..3), 4 V instructions.
+    // tile DMA: per wave NKI instructions of 1 KB for the K (or V) planes, one for the metadata.
+    // Issued through pf_dma (inline asm), so the compiler inserts no waits of its own before the
+    // LDS reads: every read of a DMA'd buffer follows an explicit vmcnt wait for that buffer.
     auto rsrc = [&](int tile) __attribute__((always_inline)) {
-        const uint8_t* src = P.pfkv + ((int64_t)seg * P.pf_ntiles + tile) * EA_PF_TILE_BYTES;
-        return __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, EA_PF_TILE_BYTES, 0x00020000);
+        const uint64_t src = (uint64_t)(P.pfkv + ((int64_t)seg * P.pf_ntiles + tile) * EA_PF_TILE_BYTES);
+        v4i r = {(int)(uint32_t)src, (int)((uint32_t)(src >> 32) & 0xFFFFu), EA_PF_TILE_BYTES, 0x00020000};
+        r.x = __builtin_amdgcn_readfirstlane(r.x);
+        r.y = __builtin_amdgcn_readfirstlane(r.y);
+        return r;
     };
-    // one lane offset for every DMA instruction; the per-instruction offset goes in soffset
-    const int vlane = lane * 16;
-    auto issue_k = [&](int tile) __attribute__((always_inline)) {
-        __amdgpu_buffer_rsrc_t rs = rsrc(tile);
+    const int vlane = lane * 16;  // one lane offset; the per-instruction offset goes in soffset
+    const uint32_t aK = lds_addr(sK), aV0 = lds_addr(sV0), aV1 = lds_addr(sV1), aM0 = lds_addr(sM0),
+                   aM1 = lds_addr(sM1);
+    auto issue_k = [&](int tile, uint32_t mdst) __attribute__((always_inline)) {
+        const v4i rs = rsrc(tile);
 #pragma unroll
         for (int q = 0; q < NKI; ++q) {
             const int off = (q * NWB + w) * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_K + off), 16, vlane, off, 0, 0);
+            pf_dma(rs, aK + off, vlane, off);
         }
-        if (NWB == 4 || w < 4)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_M + (tile & 1) * 4096 + w * 1024),
-                                                     16, vlane, EA_PF_META_OFF + w * 1024, 0, 0);
+        if (w < 4) pf_dma(rs, mdst + w * 1024, vlane, EA_PF_META_OFF + w * 1024);  // 4 KB of metadata
     };
-    auto issue_v = [&](int tile) __attribute__((always_inline)) {
-        __amdgpu_buffer_rsrc_t rs = rsrc(tile);
+    auto issue_v = [&](int tile, uint32_t vdst) __attribute__((always_inline)) {
+        const v4i rs = rsrc(tile);
 #pragma unroll
         for (int q = 0; q < NKI; ++q) {
             const int off = (q * NWB + w) * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + PF_OFF_V + off), 16, vlane, 32768 + off,
-                                                     0, 0);
+            pf_dma(rs, vdst + off, vlane, 32768 + off);
         }
     };
 
@@ -619,292 +669,337 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     bool had_fold = false;  // scr holds the sums of earlier epochs
     uint32_t failbits = 0;
 
-    if (ntiles > 0) {
-        issue_k(0);
-        issue_v(0);
-    }
-    for (int it = 0; it <= ntiles; ++it) {
-        const bool last = it == ntiles;
-        const uint8_t* Kt = smem + PF_OFF_K;
-        const PfTileMeta* TM = (const PfTileMeta*)(smem + PF_OFF_M + (it & 1) * 4096);
-        v4i Mk[NKT], Ek[NKT];
-        int nb = base;
-        bool do_fold;
-        int nf_pair = 0;  // the pair's nfrac (epoch so far)
-        bool k_next = false;
-        if (!last) {
-            tick(7);
-            wait_vm<NKI>();   // K(it) and its metadata landed; V(it) (NKI instructions) may be in flight
-            __syncthreads();  // for every wave
-            tick(0);
-            k_next = it + 1 < ntiles;
-            const int tfl = TM->tfl;
-            const bool lossy = lossy_q || (tfl & 32);
-            uint32_t slowmask = 0;  // pairs the fast path left undecided (cold path below)
-            int gm = INT_MIN;
+    // fp64 value of the int32 P.V accumulators of (channel tile cc, row 4 g + i) in units 2^base,
+    // and the bound of everything the epoch left out: fold roundings (6.02 u sum |acc|), inexact V
+    // elements (EVs), the omitted digit pair (0, 0) (2^20 per tile), weight roundings below the
+    // base (fr_i = 2^29 per key: 2^30 / 2)
+    auto epoch_sum = [&](int cc, int i, double fr_i, double omit, double* en) __attribute__((always_inline)) {
+        double h = (double)pacc[cc][6][i], ha = fabs(h);
 #pragma unroll
-            for (int kk = 0; kk < NKT; ++kk) {
-                const int kt = NKT * hh + kk;
-                const bool wide = needq || ((tfl >> kt) & 1);
-                double x[4];
-                if (wide) score_group<true>(kb, qb, kt, x);
-                else score_group<false>(kb, qb, kt, x);
-                const v4i lsbk4 = *(const v4i*)&TM->lsbk[16 * kt + 4 * g];
-                const v4i kfl4 = *(const v4i*)&TM->kfl[16 * kt + 4 * g];
-                const v4i vl4 = *(const v4i*)&TM->vlsb[16 * kt + 4 * g];
-                const double2 kA01 = *(const double2*)&TM->kA[16 * kt + 4 * g];
-                const double2 kA23 = *(const double2*)&TM->kA[16 * kt + 4 * g + 2];
-                const double kA[4] = {kA01.x, kA01.y, kA23.x, kA23.y};
-                double adx[4];
-                bool vis[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int n = it * 64 + 16 * kt + 4 * g + i;
-                    const int ti = n - tbase;
-                    const bool intree = ((unsigned)ti < 64u) & (((tmk >> (ti & 63)) & 1ull) != 0);
-                    vis[i] = (n < slen) & ((n < kvl) | intree);
-                    adx[i] = adq * kA[i];
-                }
-                if (lossy) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        adx[i] = __fma_rn(aqL, TM->kX[16 * kt + 4 * g + i] + 1.0, __fma_rn((double)(kfl4[i] >> 8), aqX, adx[i]));
-                }
-                int M[4], E[4];
-                bool ok[4];
-                lean_weight4(x, adx, lsbk4, qm.a, T1s, T2, M, E, ok);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool kbad = kfl4[i] & 1;
-                    const bool good = vis[i] & ok[i] & !kbad;
-                    dom |= (vis[i] & kbad) ? 1 : 0;
-                    slowmask |= (vis[i] & !ok[i] & !kbad) ? (1u << (4 * kk + i)) : 0u;
-                    Mk[kk][i] = good ? M[i] : 0;
-                    Ek[kk][i] = E[i];
-                    gm = max(gm, good ? E[i] + vl4[i] : INT_MIN);
-                }
-            }
-            // ---- cold path: exact decision for the pairs the fast path left undecided. The exact
-            // integer score comes from the digit planes in LDS (no memory traffic); only pairs
-            // whose digits are inexact (elements rounded at slicing) read the bf16 inputs.
-            if (__builtin_expect(__ballot(slowmask != 0) != 0, 0)) {
-                if (P.stats && lane == 0) atomicAdd((unsigned long long*)&P.stats[12], 1ull);
-                for (int p = 0; p < 4 * NKT; ++p) {
-                    if (!((slowmask >> p) & 1)) continue;
-                    const int kk = p >> 2, i = p & 3;
-                    const int key = 16 * (NKT * hh + kk) + 4 * g + i;
-                    const int n = it * 64 + key;
-                    const int kf = TM->kfl[key];
-                    uint32_t tbits = 0;
-                    int ls = 3;
-                    ++nslow;
-                    if (!qbad && !((qm.flags >> 8) & 0xFF) && !(kf >> 8)) {
-                        const int8_t* qrow = (const int8_t*)qlds;
-                        const int8_t* krow = (const int8_t*)(Kt + key * 128);
-                        i128 S = 0;
-                        for (int c = 0; c < 128; ++c) {
-                            const int kc = (((c >> 4) ^ (key & 7)) << 4) | (c & 15);
-                            int xq = 0, xk = 0;
-#pragma unroll
-                            for (int sp = 3; sp >= 0; --sp) {
-                                xq = xq * 256 + (int)qrow[(((8 * sp + (c >> 4)) ^ (j & 7)) << 4) | (c & 15)];
-                                xk = xk * 256 + (int)krow[8192 * sp + kc];
-                            }
-                            S += (i128)((int64_t)xq * (int64_t)xk);
-                        }
-                        ls = rn32_prod(P.am, S, P.ae + qm.lsb + TM->lsbk[key], &tbits);
-                    } else if (!qbad) {
-                        const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)tq * P.g.q_tok_stride +
-                                             (int64_t)(hk * P.grp + lrc % P.grp) * P.g.q_head_stride;
-                        const uint16_t* kr = P.k + kv_off(P, b, n, hk, 0);
-                        double ss = 0.0, es = 0.0, ea = 0.0;
-                        for (int c = 0; c < 128; ++c) {
-                            double e0;
-                            ss = two_sum(ss, (double)__uint_as_float((uint32_t)qr[c] << 16) *
-                                                 (double)__uint_as_float((uint32_t)kr[c] << 16), &e0);
-                            es += e0;
-                            ea += fabs(e0);
-                        }
-                        ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1
-                                                                    : logit_cert(P.alpha, ss, es, ea * 0x1p-44, &tbits);
-                        if (ls == 1) tbits = 0;
-                    }
-                    int32_t M = 0, E = 0;
-                    bool live = false;
-                    if (ls == 2) {
-                        dom = 1;
-                    } else if (ls == 3) {
-                        unc = 1;
-                        ++nunc_s;
-                    } else if (table_weight(tbits, T1s, T2, &M, &E)) {
-                        live = true;
-                    } else {
-                        // the 128-bit enclosure of 2^t decides RN24 (ea_device.h weight_wide)
-                        int32_t M2 = 0;
-                        int64_t E2 = 0;
-                        if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
-                            M = M2;
-                            E = (int32_t)E2;
-                            live = true;
-                        } else {
-                            unc = 1;
-                            ++nunc_w;
-                        }
-                    }
-#pragma unroll
-                    for (int q = 0; q < NKT; ++q)
-                        if (q == kk) {
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                if (r == i) {
-                                    Mk[q][r] = live ? M : 0;
-                                    Ek[q][r] = E;
-                                }
-                        }
-                    if (live) gm = max(gm, E + TM->vlsb[key]);
-                }
-            }
-            // ---- the row's largest weight in this tile (both waves of the pair); the base moves
-            // when a weight would exceed 2^38 (G - base > 14 for G = E + vlsb)
-            gm = max(gm, __shfl_xor(gm, 16, 64));
-            gm = max(gm, __shfl_xor(gm, 32, 64));
-            tick(1);
-            if (SPLIT == 2) s_x[w * 64 + lane] = PfX{gm, nfrac, 0.0};
-            __syncthreads();  // every wave is done with the K planes of tile it
-            if (k_next) issue_k(it + 1);
-            nf_pair = nfrac;
-            if (SPLIT == 2) {
-                const PfX o = s_x[(w ^ 1) * 64 + lane];
-                gm = max(gm, o.a);
-                nf_pair += o.b;
-            }
-            const bool need_rb = gm != INT_MIN && (base == INT_MIN || gm > base + 14);
-            nb = need_rb ? gm - 10 : base;
-            do_fold = ep_tiles > 0 && (__ballot(need_rb) != 0 || ep_tiles >= 256);
-            tick(2);
-        } else {
-            // row totals for the final rounding: this wave's 4 lanes of the row, then the partner
-            z += __shfl_xor(z, 16, 64);
-            z += __shfl_xor(z, 32, 64);
-            nv += __shfl_xor(nv, 16, 64);
-            nv += __shfl_xor(nv, 32, 64);
-            dom |= __shfl_xor(dom, 16, 64);
-            dom |= __shfl_xor(dom, 32, 64);
-            unc |= __shfl_xor(unc, 16, 64);
-            unc |= __shfl_xor(unc, 32, 64);
-            nf_pair = nfrac;
-            if (SPLIT == 2) {
-                s_x[w * 64 + lane] = PfX{nv, nfrac | (dom << 24) | (unc << 25), z};
-                __syncthreads();
-                const PfX o = s_x[(w ^ 1) * 64 + lane];
-                nv += o.a;
-                nf_pair += o.b & 0xFFFFFF;
-                dom |= (o.b >> 24) & 1;
-                unc |= (o.b >> 25) & 1;
-                z += o.c;
-            }
-            do_fold = true;
+        for (int k = 5; k >= 0; --k) {
+            const double a = (double)pacc[cc][k][i];
+            h = __fma_rn(h, 256.0, a);
+            ha = __fma_rn(ha, 256.0, fabs(a));
         }
-        if (do_fold) {
-            if (P.stats && lane == 0 && !last) atomicAdd((unsigned long long*)&P.stats[11], 1ull);
-            // fold the int32 P.V accumulators (units 2^base of each row) into fp64 with a bound.
-            // Before the last tile: add into scr, rescaled to the new bases. At the end: the
-            // quotient N/Z and its error radius per (row, channel), certified further below.
-            int nf = nf_pair + __shfl_xor(nf_pair, 16, 64);
-            nf += __shfl_xor(nf, 32, 64);
-            double Zs[4], eZs[4], fr[4];
-            bool live_i[4];
-            int bo[4], bn[4];
+        *en = 6.02 * 0x1p-53 * (ha * 256.0) + EVs[cc] + omit + fr_i;
+        return h * 256.0;
+    };
+    // ---- fold the epoch into the per-lane fp64 sums in scr, rescaled to the new bases nb
+    auto fold = [&](int nf_pair, int nb) __attribute__((always_inline)) {
+        if (P.stats && lane == 0) atomicAdd((unsigned long long*)&P.stats[11], 1ull);
+        int nf = nf_pair + __shfl_xor(nf_pair, 16, 64);
+        nf += __shfl_xor(nf, 32, 64);
+        double fr[4];
+        int bo[4], bn[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            bo[i] = __shfl(base, 4 * g + i, 64);
+            bn[i] = __shfl(nb, 4 * g + i, 64);
+            fr[i] = 0x1p29 * (double)__shfl(nf, 4 * g + i, 64);
+        }
+        nfrac = 0;
+        const double omit = (double)ep_tiles * 0x1p20;  // pair (0, 0): 64 keys x 2^14
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                bo[i] = __shfl(base, 4 * g + i, 64);
-                bn[i] = __shfl(nb, 4 * g + i, 64);
-                fr[i] = 0x1p29 * (double)__shfl(nf, 4 * g + i, 64);  // weight roundings: 2^30 / 2 each
-                Zs[i] = eZs[i] = 0.0;
-                live_i[i] = false;
-                if (last) {
-                    Zs[i] = __shfl(z, 4 * g + i, 64);
-                    const int nvr = __shfl(nv, 4 * g + i, 64);
-                    eZs[i] = (double)(nvr + 8) * PF_U * Zs[i] + (double)(nvr + 64) * 0x1p-1074;
-                    live_i[i] = nvr > 0 && !__shfl(dom | unc, 4 * g + i, 64);
+                double en;
+                double nn = epoch_sum(cc, i, fr[i], omit, &en);
+                double2* sp = (double2*)(scr + 2 * (4 * cc + i));
+                if (had_fold) {
+                    const double2 o = *sp;
+                    nn += o.x;
+                    en += o.y;
                 }
-            }
-            nfrac = 0;
-            const double omit = (double)ep_tiles * 0x1p20;  // pair (0, 0): 64 keys x 2^14
-#pragma unroll
-            for (int cc = 0; cc < NCT; ++cc) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    double h = (double)pacc[cc][6][i], ha = fabs(h);
-#pragma unroll
-                    for (int k = 5; k >= 0; --k) {
-                        const double a = (double)pacc[cc][k][i];
-                        h = __fma_rn(h, 256.0, a);
-                        ha = __fma_rn(ha, 256.0, fabs(a));
-                    }
-                    h *= 256.0;
-                    ha *= 256.0;
-                    double en = 6.02 * 0x1p-53 * ha + EVs[cc] + omit + fr[i];
-                    double nn = h;
-                    double2* sp = (double2*)(scr + 2 * (4 * cc + i));
-                    if (had_fold) {
-                        const double2 o = *sp;
-                        nn += o.x;
-                        en += o.y;
-                    }
-                    en += fabs(nn) * 0x1p-52;
-                    if (!last) {
-                        if (bo[i] != INT_MIN && bn[i] != bo[i]) {
-                            const int dsh = max(bo[i] - bn[i], -1100);
-                            nn = ldexp(nn, dsh);
-                            en = ldexp(en, dsh) + 0x1p-1074;
-                        }
-                        *sp = make_double2(nn, en);
-                    } else {
-                        double q = 0.0, delta = -1.0;  // delta < 0: no output from this entry
-                        const double Z = Zs[i], eZ = eZs[i];
-                        if (live_i[i]) {
-                            if (Z > 2.0 * eZ && isfinite(Z)) {
-                                q = nn / Z;
-                                delta = (en * (1.0 + 0x1p-40) + fabs(q) * eZ) / (Z - eZ) * (1.0 + 0x1p-40) +
-                                        fabs(q) * 0x1p-51 + 0x1p-1070;
-                                if (!isfinite(q) || !isfinite(delta)) delta = __builtin_inf();
-                            } else {
-                                delta = __builtin_inf();
-                            }
-                        }
-                        *sp = make_double2(q, delta);
-                    }
-#pragma unroll
-                    for (int k = 0; k < 7; ++k) pacc[cc][k][i] = 0;
+                en += fabs(nn) * 0x1p-52;
+                if (bo[i] != INT_MIN && bn[i] != bo[i]) {
+                    const int dsh = max(bo[i] - bn[i], -1100);
+                    nn = ldexp(nn, dsh);
+                    en = ldexp(en, dsh) + 0x1p-1074;
                 }
-            }
+                *sp = make_double2(nn, en);
 #pragma unroll
-            for (int cc = 0; cc < NCT; ++cc) EVs[cc] = 0.0;
-            ep_tiles = 0;
-            had_fold = !last;
-            wait_vm<0>();  // the scr stores are complete (keeps the DMA counts below exact)
-            tick(3);
+                for (int k = 0; k < 7; ++k) pacc[cc][k][i] = 0;
+            }
         }
-        if (last) break;
-        // ---- move bases, then this wave's weight digits (A operand of the P.V MFMA) and Z
-        if (nb != base && base != INT_MIN) z = ldexp(z, max(base - nb, -1100));
-        base = nb;
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) EVs[cc] = 0.0;
+        ep_tiles = 0;
+        had_fold = true;
+        wait_vm<0>();  // the scr stores are complete (keeps the DMA counts exact)
+    };
+
+    // ---- P.V of the tile whose digits are in sWD and V planes in vbuf: pacc[cc][s + t - 1] +=
+    // W digits s x V digits t (all pairs but (0, 0)). Channel 16 (NCT hh + cc) + j: the 16-byte
+    // slot swizzle (ch >> 1) & 3 = (j >> 1) & 3 does not depend on cc, so every read is one lane
+    // base plus a constant.
+    auto pv_mfma = [&](const v4i (&Wd)[5], const uint8_t* vbuf, int c0, int c1) __attribute__((always_inline)) {
+        const uint8_t* Vt = vbuf + (16 * NCT * hh + j) * 64 + ((g ^ ((j >> 1) & 3)) << 4);
+#pragma unroll
+        for (int cc = c0; cc < c1; ++cc) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const v4i B = *(const v4i*)(Vt + t * 8192 + cc * 1024);
+#pragma unroll
+                for (int s = 0; s < 5; ++s) {
+                    if (s + t < 1) continue;
+                    pacc[cc][s + t - 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Wd[s], B, pacc[cc][s + t - 1], 0, 0, 0);
+                }
+            }
+        }
+    };
+    auto read_wd = [&](v4i (&Wd)[5]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 5; ++s)
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) Wd[s][kt] = (int)wd_r[(kt / NKT) * WDS + (s * NKT + kt % NKT) * 64];
+    };
+
+    // ---- one pipeline step: scores and weights of tile it, P.V of tile it - 1
+    auto step = [&](auto par, int it) __attribute__((always_inline)) {
+        constexpr int PA = decltype(par)::value;
+        const uint8_t* const sVp = PA ? sV0 : sV1;  // V(it - 1)
+        const uint32_t aVn = PA ? aV0 : aV1;        // V(it + 1) replaces it after B2
+        const PfTileMeta* const TMc = (const PfTileMeta*)(PA ? sM1 : sM0);
+        const PfTileMeta* const TMp = (const PfTileMeta*)(PA ? sM0 : sM1);
+        const uint32_t aMn = PA ? aM0 : aM1;        // metadata of tile it + 1
+        const bool have_p = it > 0, k_next = it + 1 < ntiles;
+        tick(7);
+        wait_vm<NKI>();  // K(it) and its metadata landed; V(it) may be in flight
+        pf_bar();        // B1
+        tick(0);
         v4i Wd[5];
+        read_wd(Wd);  // zero at it = 0
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TMp->EV[16 * (NCT * hh + cc) + j];
+        if (have_p) ++ep_tiles;
+        const int tfl = TMc->tfl;
+        // ---- score MFMAs of tile it
+        v4i sacc[NKT][7];
+#pragma unroll
+        for (int kk = 0; kk < NKT; ++kk)
+#pragma unroll
+            for (int k = 0; k < 7; ++k) sacc[kk][k] = (v4i){0, 0, 0, 0};
+        if (needq || ((tfl >> (NKT * hh)) & ((1 << NKT) - 1))) {
+#pragma unroll
+            for (int kk = 0; kk < NKT; ++kk) score_mfma<true>(kb, qb, NKT * hh + kk, sacc[kk]);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < NKT; ++kk) score_mfma<false>(kb, qb, NKT * hh + kk, sacc[kk]);
+        }
+        tick(1);
+        pf_bar();  // B1.5: every wave has read the K planes of tile it
+        if (k_next) issue_k(it + 1, aMn);
+        // ---- per-pair metadata, score bounds and visibility of tile it
+        v4i lk4[NKT], vl4[NKT];
+        double adel[NKT][4];
 #pragma unroll
         for (int kk = 0; kk < NKT; ++kk) {
             const int kt = NKT * hh + kk;
+            lk4[kk] = *(const v4i*)&TMc->lsbk[16 * kt + 4 * g];
+            vl4[kk] = *(const v4i*)&TMc->vlsb[16 * kt + 4 * g];
+            const double2 kA01 = *(const double2*)&TMc->kA[16 * kt + 4 * g];
+            const double2 kA23 = *(const double2*)&TMc->kA[16 * kt + 4 * g + 2];
+            adel[kk][0] = adq * kA01.x;
+            adel[kk][1] = adq * kA01.y;
+            adel[kk][2] = adq * kA23.x;
+            adel[kk][3] = adq * kA23.y;
+        }
+        if (lossy_q || (tfl & 32)) {
+            // elements rounded at slicing: |q_i - Q_i| <= 2^lsbq / 2 and the same for k
+#pragma unroll
+            for (int kk = 0; kk < NKT; ++kk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = 16 * (NKT * hh + kk) + 4 * g + i;
+                    const double e = __fma_rn(aqL, TMc->kX[key] + 1.0, (double)(TMc->kfl[key] >> 8) * aqX);
+                    adel[kk][i] = (adel[kk][i] + ldexp(e, lk4[kk][i])) * (1.0 + 0x1p-50);
+                }
+        }
+        uint32_t vism = rvalid ? 0xFFu : 0u;  // bit 4 kk + i: pair visible
+        if (!((it + 1) * 64 <= kvmin)) {
+            vism = 0;
+#pragma unroll
+            for (int kk = 0; kk < NKT; ++kk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int n = it * 64 + 16 * (NKT * hh + kk) + 4 * g + i;
+                    const int ti = n - tbase;
+                    const bool intree = ((unsigned)ti < 64u) & (((tmk >> (ti & 63)) & 1ull) != 0);
+                    vism |= ((n < slen) & ((n < kvl) | intree)) ? (1u << (4 * kk + i)) : 0u;
+                }
+        }
+        if (tfl & 16) {
+            // NaN/inf in a key's K or V row: a domain error for the rows that see it
+#pragma unroll
+            for (int kk = 0; kk < NKT; ++kk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int bit = 1 << (4 * kk + i);
+                    if (TMc->kfl[16 * (NKT * hh + kk) + 4 * g + i] & 1) {
+                        if (vism & bit) dom = 1;
+                        vism &= ~(uint32_t)bit;
+                    }
+                }
+        }
+        // ---- P.V of tile it - 1 (zero digits at it = 0), certification of tile it: two regions,
+        // each half the channel tiles' MFMAs and one key group's certification, interleaved
+        v4i Mk[NKT], Ek[NKT];
+        uint32_t slowmask = 0;  // pairs the fast path left undecided (cold path below)
+        int gm = INT_MIN;
+#pragma unroll
+        for (int kk = 0; kk < NKT; ++kk) {
+            pv_mfma(Wd, sVp, kk * (NCT / NKT), (kk + 1) * (NCT / NKT));
+            double xs[4];
+            score_fold(sacc[kk], lk4[kk], xs);
+            int M[4], E[4];
+            bool ok[4];
+            cert4(xs, adel[kk], qm.a, T1s, T2, M, E, ok);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool vis = (vism >> (4 * kk + i)) & 1;
+                const bool good = vis & ok[i];
+                slowmask |= (vis & !ok[i]) ? (1u << (4 * kk + i)) : 0u;
+                Mk[kk][i] = good ? M[i] : 0;
+                Ek[kk][i] = E[i];
+                gm = max(gm, good ? E[i] + vl4[kk][i] : INT_MIN);
+            }
+            // interleave: each P.V MFMA followed by VALU work of the certification, so the matrix
+            // core runs while the vector ALU certifies (one wave per SIMD: no other wave fills
+            // the gaps)
+#pragma unroll
+            for (int m = 0; m < 19 * (NCT / NKT); ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, PF_VALU_PER_MFMA, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        tick(2);
+        // ---- cold path: exact decision for the pairs the fast path left undecided. The exact
+        // integer score comes from the tile's digit planes (no bf16 reads); only pairs whose
+        // digits are inexact (elements rounded at slicing) read the bf16 inputs.
+        if (__builtin_expect(__ballot(slowmask != 0) != 0, 0)) {
+            if (P.stats && lane == 0) atomicAdd((unsigned long long*)&P.stats[12], 1ull);
+            const int8_t* Kg = (const int8_t*)(P.pfkv + ((int64_t)seg * P.pf_ntiles + it) * EA_PF_TILE_BYTES);
+            for (int p = 0; p < 4 * NKT; ++p) {
+                if (!((slowmask >> p) & 1)) continue;
+                const int kk = p >> 2, i = p & 3;
+                const int key = 16 * (NKT * hh + kk) + 4 * g + i;
+                const int n = it * 64 + key;
+                const int kf = TMc->kfl[key];
+                uint32_t tbits = 0;
+                int ls = 3;
+                ++nslow;
+                if (!qbad && !((qm.flags >> 8) & 0xFF) && !(kf >> 8)) {
+                    // 16 dims at a time: one 16-byte chunk per digit plane of q (LDS) and K (tile)
+                    const int8_t* krow = Kg + key * 128;
+                    i128 S = 0;
+                    for (int c16 = 0; c16 < 8; ++c16) {
+                        uint4 qc[4], kc[4];
+#pragma unroll
+                        for (int sp = 0; sp < 4; ++sp) {
+                            qc[sp] = *(const uint4*)(qlds + (((8 * sp + c16) ^ (j & 7)) << 4));
+                            kc[sp] = *(const uint4*)(krow + 8192 * sp + ((c16 ^ (key & 7)) << 4));
+                        }
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            int xq = 0, xk = 0;
+#pragma unroll
+                            for (int sp = 3; sp >= 0; --sp) {
+                                const uint32_t wq = (&qc[sp].x)[e >> 2], wk = (&kc[sp].x)[e >> 2];
+                                xq = xq * 256 + (int)(int8_t)(wq >> (8 * (e & 3)));
+                                xk = xk * 256 + (int)(int8_t)(wk >> (8 * (e & 3)));
+                            }
+                            S += (i128)((int64_t)xq * (int64_t)xk);
+                        }
+                    }
+                    ls = rn32_prod(P.am, S, P.ae + qm.lsb + TMc->lsbk[key], &tbits);
+                } else if (!qbad) {
+                    const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)tq * P.g.q_tok_stride +
+                                         (int64_t)(hk * P.grp + lrc % P.grp) * P.g.q_head_stride;
+                    const uint16_t* kr = P.k + kv_off(P, b, n, hk, 0);
+                    double ss = 0.0, es = 0.0, ea = 0.0;
+                    for (int c = 0; c < 128; ++c) {
+                        double e0;
+                        ss = two_sum(ss, (double)__uint_as_float((uint32_t)qr[c] << 16) *
+                                             (double)__uint_as_float((uint32_t)kr[c] << 16), &e0);
+                        es += e0;
+                        ea += fabs(e0);
+                    }
+                    ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1
+                                                                : logit_cert(P.alpha, ss, es, ea * 0x1p-44, &tbits);
+                    if (ls == 1) tbits = 0;
+                }
+                int32_t M = 0, E = 0;
+                bool live = false;
+                if (ls == 2) {
+                    dom = 1;
+                } else if (ls == 3) {
+                    unc = 1;
+                    ++nunc_s;
+                } else if (table_weight(tbits, T1s, T2, &M, &E)) {
+                    live = true;
+                } else {
+                    // the 128-bit enclosure of 2^t decides RN24 (ea_device.h weight_wide)
+                    int32_t M2 = 0;
+                    int64_t E2 = 0;
+                    if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
+                        M = M2;
+                        E = (int32_t)E2;
+                        live = true;
+                    } else {
+                        unc = 1;
+                        ++nunc_w;
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < NKT; ++q)
+                    if (q == kk) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (r == i) {
+                                Mk[q][r] = live ? M : 0;
+                                Ek[q][r] = E;
+                            }
+                    }
+                if (live) gm = max(gm, E + TMc->vlsb[key]);
+            }
+        }
+        tick(3);
+        // ---- the row's largest weight in this tile (both waves of the pair); the base moves
+        // when a weight would exceed 2^38 (G - base > 14 for G = E + vlsb)
+        gm = max(gm, __shfl_xor(gm, 16, 64));
+        gm = max(gm, __shfl_xor(gm, 32, 64));
+        sX[w * 64 + lane] = PfX{gm, nfrac, 0.0};
+        pf_bar();  // B2: every wave is done with V(it - 1) and its tile metadata
+        if (k_next) issue_v(it + 1, aVn);
+        int nf_pair = nfrac;  // the row group's keys (all SPLIT waves)
+#pragma unroll
+        for (int o = 1; o < SPLIT; ++o) {
+            const PfX x = sX[(rg * SPLIT + (hh + o) % SPLIT) * 64 + lane];
+            gm = max(gm, x.a);
+            nf_pair += x.b;
+        }
+        const bool need_rb = gm != INT_MIN && (base == INT_MIN || gm > base + 14);
+        const int nb = need_rb ? gm - 10 : base;
+        tick(4);
+        if (ep_tiles > 0 && (__ballot(need_rb) != 0 || ep_tiles >= 256)) fold(nf_pair, nb);
+        tick(5);
+        // ---- move bases, then this wave's weight digits (A operand of the P.V MFMA) and Z
+        if (nb != base && base != INT_MIN) z = ldexp(z, max(base - nb, -1100));
+        base = nb;
+#pragma unroll
+        for (int kk = 0; kk < NKT; ++kk) {
             uint32_t L[4], H[4];
-            const v4i vl4 = *(const v4i*)&TM->vlsb[16 * kt + 4 * g];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int Mp = Mk[kk][i];
                 const int sc = Ek[kk][i] - base;
                 const double md = (double)Mp;
-                const double wsc = ldexp(md, sc + vl4[i]);  // <= 2^38
-                z += ldexp(md, sc);                         // md = 0 for masked pairs
+                const double wsc = ldexp(md, sc + vl4[kk][i]);  // <= 2^38
+                z += ldexp(md, sc);                             // md = 0 for masked pairs
                 nv += Mp ? 1 : 0;
-                nfrac += (Mp && sc + vl4[i] < 0) ? 1 : 0;
+                nfrac += (Mp && sc + vl4[kk][i] < 0) ? 1 : 0;
                 const uint64_t yb = f64_as_u64(wsc + PF_C40);
                 L[i] = (uint32_t)yb;
                 H[i] = (uint32_t)(yb >> 32);
@@ -915,76 +1010,112 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             const uint32_t b23 = __builtin_amdgcn_perm(L[3], L[2], 0x07030602u);
             const uint32_t e01 = __builtin_amdgcn_perm(H[1], H[0], 0x05010400u);
             const uint32_t e23 = __builtin_amdgcn_perm(H[3], H[2], 0x05010400u);
-            const uint32_t d0 = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
-            const uint32_t d1 = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
-            const uint32_t d2 = __builtin_amdgcn_perm(b23, b01, 0x05040100u) ^ 0x80808080u;
-            const uint32_t d3 = __builtin_amdgcn_perm(b23, b01, 0x07060302u) ^ 0x80808080u;
-            const uint32_t d4 = __builtin_amdgcn_perm(e23, e01, 0x05040100u) ^ 0x80808080u;
-            if (SPLIT == 2) {
-                uint32_t* wd = wd_w + kk * 64;
-                wd[0 * 128] = d0;
-                wd[1 * 128] = d1;
-                wd[2 * 128] = d2;
-                wd[3 * 128] = d3;
-                wd[4 * 128] = d4;
-            } else {
-                Wd[0][kt] = (int)d0;
-                Wd[1][kt] = (int)d1;
-                Wd[2][kt] = (int)d2;
-                Wd[3][kt] = (int)d3;
-                Wd[4][kt] = (int)d4;
-            }
+            uint32_t* wd = wd_w + kk * 64;
+            wd[0 * 64 * NKT] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
+            wd[1 * 64 * NKT] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
+            wd[2 * 64 * NKT] = __builtin_amdgcn_perm(b23, b01, 0x05040100u) ^ 0x80808080u;
+            wd[3 * 64 * NKT] = __builtin_amdgcn_perm(b23, b01, 0x07060302u) ^ 0x80808080u;
+            wd[4 * 64 * NKT] = __builtin_amdgcn_perm(e23, e01, 0x05040100u) ^ 0x80808080u;
         }
-        tick(4);
-        // V(it) landed (only K(it+1) may still be in flight), the pair's digits are in LDS
-        if (k_next) {
-            if (NWB == 4 || w < 4) wait_vm<NKI + 1>();
-            else wait_vm<NKI>();
-        } else {
-            wait_vm<0>();
-        }
-        __syncthreads();
-        tick(5);
-        if (SPLIT == 2) {
+        tick(6);
+    };
+
+    wait_vm<0>();  // the prologue's global loads: from here on vmcnt counts DMAs (and folds)
+    if (ntiles > 0) {
+        issue_k(0, aM0);
+        issue_v(0, aV0);
+    }
+    for (int it = 0; it < ntiles; it += 2) {
+        step(PfPar<0>{}, it);
+        if (it + 1 < ntiles) step(PfPar<1>{}, it + 1);
+    }
+    // ---- drain: P.V of the last tile
+    if (ntiles > 0) {
+        wait_vm<0>();
+        pf_bar();
+        const bool odd = (ntiles - 1) & 1;
+        v4i Wd[5];
+        read_wd(Wd);
+        const PfTileMeta* TMp = (const PfTileMeta*)(odd ? sM1 : sM0);
 #pragma unroll
-            for (int s = 0; s < 5; ++s)
+        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TMp->EV[16 * (NCT * hh + cc) + j];
+        ++ep_tiles;
+        pv_mfma(Wd, odd ? sV1 : sV0, 0, NCT);
+    }
+    // ---- row totals for the final rounding: this wave's 4 lanes of the row, then the partner
+    z += __shfl_xor(z, 16, 64);
+    z += __shfl_xor(z, 32, 64);
+    nv += __shfl_xor(nv, 16, 64);
+    nv += __shfl_xor(nv, 32, 64);
+    dom |= __shfl_xor(dom, 16, 64);
+    dom |= __shfl_xor(dom, 32, 64);
+    unc |= __shfl_xor(unc, 16, 64);
+    unc |= __shfl_xor(unc, 32, 64);
+    sX[w * 64 + lane] = PfX{nv, nfrac | (dom << 24) | (unc << 25), z};
+    pf_bar();
+    int nf_pair = nfrac;
+    {
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt) Wd[s][kt] = (int)wd_r[(kt >> 1) * 640 + (s * 2 + (kt & 1)) * 64];
+        for (int o = 1; o < SPLIT; ++o) {
+            const PfX x = sX[(rg * SPLIT + (hh + o) % SPLIT) * 64 + lane];
+            nv += x.a;
+            nf_pair += x.b & 0xFFFFFF;
+            dom |= (x.b >> 24) & 1;
+            unc |= (x.b >> 25) & 1;
+            z += x.c;
         }
-        // ---- P.V: pacc[cc][s + t - 1] += W digits s x V digits t (all pairs but (0, 0))
-        // channel 16 (NCT hh + cc) + j: the 16-byte slot swizzle (ch >> 1) & 3 = (j >> 1) & 3 does
-        // not depend on cc, so every read is one lane base plus a constant
-        const uint8_t* Vt = smem + PF_OFF_V + (16 * NCT * hh + j) * 64 + ((g ^ ((j >> 1) & 3)) << 4);
+    }
+    // ---- the last epoch plus the earlier ones, then RN(N/Z) per (row, channel), certified:
+    // q = N * RN(1/Z) (two roundings: below 2^-51.9 |q|, inside the 2^-51 |q| term) and
+    // delta >= |N/Z - q| from the N bound en and the Z bound eZ
+    if (ntiles > 0) {
+        double2 prev[4 * NCT];
+#pragma unroll
+        for (int e = 0; e < 4 * NCT; ++e) prev[e] = had_fold ? *(const double2*)(scr + 2 * e) : make_double2(0.0, 0.0);
+        int nf = nf_pair + __shfl_xor(nf_pair, 16, 64);
+        nf += __shfl_xor(nf, 32, 64);
+        double fr[4], Zr[4], eZr[4], rz[4], rze[4];
+        bool skip[4], live[4];  // skip: empty row, domain error or undecided pair (no output here)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            fr[i] = 0x1p29 * (double)__shfl(nf, 4 * g + i, 64);
+            Zr[i] = __shfl(z, 4 * g + i, 64);
+            const int nvr = __shfl(nv, 4 * g + i, 64);
+            eZr[i] = (double)(nvr + 8) * PF_U * Zr[i] + (double)(nvr + 64) * 0x1p-1074;
+            skip[i] = !(nvr > 0 && !__shfl(dom | unc, 4 * g + i, 64));
+            const bool zok = Zr[i] > 2.0 * eZr[i] && isfinite(Zr[i]);
+            rz[i] = zok ? 1.0 / Zr[i] : 0.0;
+            rze[i] = zok ? 1.0 / (Zr[i] - eZr[i]) : 0.0;
+            live[i] = !skip[i] && zok;
+        }
+        // (q, delta) per entry through LDS (the K and V buffers are idle: no DMA is in flight),
+        // then one rolled loop certifies them: the rounding code runs once per wave and stays
+        // small in the instruction cache
+        double2* const qd = (double2*)smem + tid;  // entry e at qd[64 NWB e]
+        const double omit = (double)ep_tiles * 0x1p20;
 #pragma unroll
         for (int cc = 0; cc < NCT; ++cc) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const v4i B = *(const v4i*)(Vt + t * 8192 + cc * 1024);
-#pragma unroll
-                for (int s = 0; s < 5; ++s) {
-                    if (s + t < 1) continue;
-                    pacc[cc][s + t - 1] =
-                        __builtin_amdgcn_mfma_i32_16x16x64_i8(Wd[s], B, pacc[cc][s + t - 1], 0, 0, 0);
-                }
+            for (int i = 0; i < 4; ++i) {
+                double en;
+                const double nn = epoch_sum(cc, i, fr[i], omit, &en) + prev[4 * cc + i].x;
+                en += prev[4 * cc + i].y;
+                en += fabs(nn) * 0x1p-52;
+                const double q = nn * rz[i];
+                double delta = (en * (1.0 + 0x1p-40) + fabs(q) * eZr[i]) * rze[i] * (1.0 + 0x1p-40) +
+                               fabs(q) * 0x1p-51 + 0x1p-1070;
+                if (!isfinite(q) || !isfinite(delta) || !live[i]) delta = __builtin_inf();
+                if (skip[i]) delta = -1.0;  // no output from this entry
+                qd[64 * NWB * (4 * cc + i)] = make_double2(q, delta);
             }
         }
-#pragma unroll
-        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TM->EV[16 * (NCT * hh + cc) + j];
-        ++ep_tiles;
-        tick(6);
-        __syncthreads();  // every wave is done with the V buffer and the digit exchange
-        if (it + 1 < ntiles) issue_v(it + 1);
-    }
-
-    // ---- certified final rounding, one (row, channel) at a time
-    if (ntiles > 0) {
 #pragma unroll 1
         for (int e = 0; e < 4 * NCT; ++e) {
             const int cc = e >> 2, i = e & 3;
-            const double2 qd2 = *(const double2*)(scr + 2 * e);
-            if (!(qd2.y >= 0.0)) continue;
+            const double2 v = qd[64 * NWB * e];
+            if (!(v.y >= 0.0)) continue;
             uint32_t bits = 0;
-            if (!certify_round(qd2.x, qd2.y, P.out_fp32, &bits)) {
+            if (!certify_round(v.x, v.y, P.out_fp32, &bits)) {
                 failbits |= 1u << (8 * i + cc);
                 continue;
             }
@@ -998,6 +1129,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             }
         }
     }
+    tick(7);
     if (TIMERS && lane == 0) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
@@ -1013,8 +1145,6 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     }
     if (ntiles == 0) {
         // no key visible to any row of the block: every row is empty (+0) or a q domain error
-        dom |= __shfl_xor(dom, 16, 64);
-        dom |= __shfl_xor(dom, 32, 64);
         nv = 0;
         unc = 0;
     }
@@ -1026,12 +1156,11 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             const uint64_t bal = __ballot(((failbits >> (8 * i)) & 0xFF) != 0);
             if (((bal >> (16 * g)) & 0xFFFFull) != 0) fb |= 1u << i;
         }
-        if (SPLIT == 2) {
-            __syncthreads();  // s_x reuse
-            s_x[w * 64 + lane].a = (int)fb;
-            __syncthreads();
-            fb |= (uint32_t)s_x[(w ^ 1) * 64 + lane].a;
-        }
+        pf_bar();  // sX reuse
+        sX[w * 64 + lane].a = (int)fb;
+        pf_bar();
+#pragma unroll
+        for (int o = 1; o < SPLIT; ++o) fb |= (uint32_t)sX[(rg * SPLIT + (hh + o) % SPLIT) * 64 + lane].a;
         failbits = fb;
     }
 #pragma unroll
@@ -1071,9 +1200,10 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
 }
 
 namespace {
-// kernel shape: pair-split waves; 4 waves (32 rows, 1 wave per SIMD, 512 registers) by default,
-// EA_PF_SHAPE=8 selects 8 waves (64 rows, 2 waves per SIMD)
-int pf_rows_per_block() { return (getenv("EA_PF_SHAPE") && getenv("EA_PF_SHAPE")[0] == '8') ? 64 : 32; }
+// kernel shape: 32 rows per block; 8 waves (2 row groups x 4 waves, 2 waves per SIMD, 256
+// registers each) by default, EA_PF_SHAPE=4 selects 4 waves (2 x 2, 1 wave per SIMD)
+constexpr int PF_RPB = 32;
+int pf_waves() { return (getenv("EA_PF_SHAPE") && getenv("EA_PF_SHAPE")[0] == '4') ? 4 : 8; }
 }  // namespace
 
 int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb) {
@@ -1083,7 +1213,7 @@ int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb
     const int64_t r_seg = (int64_t)g.num_tokens * grp;
     if (!force && g.num_tokens < 64) return 0;
     if (r_seg >= (1 << 30) || (int64_t)g.max_seq_len + 64 >= (1 << 30)) return 0;
-    const int rpb = pf_rows_per_block();
+    const int rpb = PF_RPB;
     *ntiles = (g.max_seq_len + 63) / 64;
     *nrb = (int)((r_seg + rpb - 1) / rpb);
     return 1;
@@ -1093,8 +1223,8 @@ int ea::ea_launch_prefill(const Params& P, hipStream_t st) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [] {
-        const void* fns[3] = {(const void*)ea_pf_main<2, 4, false>, (const void*)ea_pf_main<2, 4, true>,
-                              (const void*)ea_pf_main<2, 8, false>};
+        const void* fns[4] = {(const void*)ea_pf_main<4, false>, (const void*)ea_pf_main<4, true>,
+                              (const void*)ea_pf_main<8, false>, (const void*)ea_pf_main<8, true>};
         for (const void* f : fns)
             if (attr_err == hipSuccess)
                 attr_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
@@ -1116,9 +1246,13 @@ int ea::ea_launch_prefill_main(const Params& P, hipStream_t st) {
     Params Pc = P;
     if (P.nseg > 0 && P.pf_nrb > 0) {
         const dim3 grid((unsigned)(P.nseg * P.pf_nrb));
-        if (P.timers) hipLaunchKernelGGL((ea_pf_main<2, 4, true>), grid, dim3(256), PF_LDS, st, Pc);
-        else if (pf_rows_per_block() == 64) hipLaunchKernelGGL((ea_pf_main<2, 8, false>), grid, dim3(512), PF_LDS, st, Pc);
-        else hipLaunchKernelGGL((ea_pf_main<2, 4, false>), grid, dim3(256), PF_LDS, st, Pc);
+        if (pf_waves() == 8) {
+            if (P.timers) hipLaunchKernelGGL((ea_pf_main<8, true>), grid, dim3(512), PF_LDS, st, Pc);
+            else hipLaunchKernelGGL((ea_pf_main<8, false>), grid, dim3(512), PF_LDS, st, Pc);
+        } else {
+            if (P.timers) hipLaunchKernelGGL((ea_pf_main<4, true>), grid, dim3(256), PF_LDS, st, Pc);
+            else hipLaunchKernelGGL((ea_pf_main<4, false>), grid, dim3(256), PF_LDS, st, Pc);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return -100 - (int)e;
     }
