@@ -513,7 +513,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     // phase clocks (TIMERS build): shader cycles summed over waves into P.timers[0..7]:
     // [0] wait for K + barrier, [1] score MFMAs + barrier, [2] P.V + certification,
     // [3] cold path and bad keys, [4] pair exchange, [5] epoch folds, [6] weight digits, [7] rest
-    uint64_t tclk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t tclk[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     uint64_t tprev = TIMERS ? __builtin_amdgcn_s_memtime() : 0;
     auto tick = [&](int ph) __attribute__((always_inline)) {
         if (TIMERS) {
@@ -755,26 +755,81 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             for (int kt = 0; kt < 4; ++kt) Wd[s][kt] = (int)wd_r[(kt / NKT) * WDS + (s * NKT + kt % NKT) * 64];
     };
 
-    // ---- one pipeline step: scores and weights of tile it, P.V of tile it - 1
+    // ---- weights of the previous tile (certified in the previous step) and this wave's row maxima
+    v4i cMk[NKT], cEk[NKT], cvl[NKT];
+    int cgm = INT_MIN;
+    // ---- after B1: the row group's maxima of the previous tile are in sX. Move the base (folding
+    // the epoch first when it moves or is 256 tiles old), add the previous tile's inexact-V
+    // counts, then write the previous tile's weight digits (A operand of the P.V MFMA) to sWD.
+    auto rebase_digits = [&](const PfTileMeta* TMprev) __attribute__((always_inline)) {
+        int gm = cgm;
+        int nf_pair = nfrac;  // the row group's keys (all SPLIT waves) of the epoch
+#pragma unroll
+        for (int o = 1; o < SPLIT; ++o) {
+            const PfX x = sX[(rg * SPLIT + (hh + o) % SPLIT) * 64 + lane];
+            gm = max(gm, x.a);
+            nf_pair += x.b;
+        }
+        // the base moves when a weight would exceed 2^38 (G - base > 14 for G = E + vlsb)
+        const bool need_rb = gm != INT_MIN && (base == INT_MIN || gm > base + 14);
+        const int nb = need_rb ? gm - 10 : base;
+        if (ep_tiles > 0 && (__ballot(need_rb) != 0 || ep_tiles >= 256)) fold(nf_pair, nb);
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TMprev->EV[16 * (NCT * hh + cc) + j];
+        if (nb != base && base != INT_MIN) z = ldexp(z, max(base - nb, -1100));
+        base = nb;
+    #pragma unroll
+            for (int kk = 0; kk < NKT; ++kk) {
+                uint32_t L[4], H[4];
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int Mp = cMk[kk][i];
+                    const int sc = cEk[kk][i] - base;
+                    const double md = (double)Mp;
+                    const double wsc = ldexp(md, sc + cvl[kk][i]);  // <= 2^38
+                    z += ldexp(md, sc);                             // md = 0 for masked pairs
+                    nv += Mp ? 1 : 0;
+                    nfrac += (Mp && sc + cvl[kk][i] < 0) ? 1 : 0;
+                    const uint64_t yb = f64_as_u64(wsc + PF_C40);
+                    L[i] = (uint32_t)yb;
+                    H[i] = (uint32_t)(yb >> 32);
+                }
+                const uint32_t a01 = __builtin_amdgcn_perm(L[1], L[0], 0x05010400u);
+                const uint32_t b01 = __builtin_amdgcn_perm(L[1], L[0], 0x07030602u);
+                const uint32_t a23 = __builtin_amdgcn_perm(L[3], L[2], 0x05010400u);
+                const uint32_t b23 = __builtin_amdgcn_perm(L[3], L[2], 0x07030602u);
+                const uint32_t e01 = __builtin_amdgcn_perm(H[1], H[0], 0x05010400u);
+                const uint32_t e23 = __builtin_amdgcn_perm(H[3], H[2], 0x05010400u);
+                uint32_t* wd = wd_w + kk * 64;
+                wd[0 * 64 * NKT] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
+                wd[1 * 64 * NKT] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
+                wd[2 * 64 * NKT] = __builtin_amdgcn_perm(b23, b01, 0x05040100u) ^ 0x80808080u;
+                wd[3 * 64 * NKT] = __builtin_amdgcn_perm(b23, b01, 0x07060302u) ^ 0x80808080u;
+                wd[4 * 64 * NKT] = __builtin_amdgcn_perm(e23, e01, 0x05040100u) ^ 0x80808080u;
+            }
+    };
+
+    // ---- one pipeline step, tile it:
+    //   B1    K(it) landed; the row group's maxima of tile it-1 are in sX
+    //   R1    base, fold, weight digits of tile it-1 to sWD; V(it) starts loading; score MFMAs
+    //   B1.5  every wave has read the K planes (K(it+1) starts loading) and written its digits
+    //   R2    P.V of tile it-1 beside the certification of tile it; maxima of tile it to sX
     auto step = [&](auto par, int it) __attribute__((always_inline)) {
         constexpr int PA = decltype(par)::value;
         const uint8_t* const sVp = PA ? sV0 : sV1;  // V(it - 1)
-        const uint32_t aVn = PA ? aV0 : aV1;        // V(it + 1) replaces it after B2
+        const uint32_t aVc = PA ? aV1 : aV0;        // V(it) loads into the buffer V(it - 2) used
         const PfTileMeta* const TMc = (const PfTileMeta*)(PA ? sM1 : sM0);
         const PfTileMeta* const TMp = (const PfTileMeta*)(PA ? sM0 : sM1);
         const uint32_t aMn = PA ? aM0 : aM1;        // metadata of tile it + 1
-        const bool have_p = it > 0, k_next = it + 1 < ntiles;
+        const bool k_next = it + 1 < ntiles;
         tick(7);
-        wait_vm<NKI>();  // K(it) and its metadata landed; V(it) may be in flight
-        pf_bar();        // B1
+        wait_vm<0>();  // K(it) and its metadata (issued at B1.5 of the previous step) landed
+        tick(14);
+        pf_bar();      // B1
         tick(0);
-        v4i Wd[5];
-        read_wd(Wd);  // zero at it = 0
-#pragma unroll
-        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TMp->EV[16 * (NCT * hh + cc) + j];
-        if (have_p) ++ep_tiles;
         const int tfl = TMc->tfl;
-        // ---- score MFMAs of tile it
+        // ---- score MFMAs of tile it, then (while they run) the previous tile's digits, then the
+        // fp64 scores
         v4i sacc[NKT][7];
 #pragma unroll
         for (int kk = 0; kk < NKT; ++kk)
@@ -788,15 +843,28 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             for (int kk = 0; kk < NKT; ++kk) score_mfma<false>(kb, qb, NKT * hh + kk, sacc[kk]);
         }
         tick(1);
-        pf_bar();  // B1.5: every wave has read the K planes of tile it
+        if (it > 0) rebase_digits(TMp);
+        issue_v(it, aVc);
+        v4i lk4[NKT];
+        double xs[NKT][4];
+#pragma unroll
+        for (int kk = 0; kk < NKT; ++kk) {
+            lk4[kk] = *(const v4i*)&TMc->lsbk[16 * (NKT * hh + kk) + 4 * g];
+            score_fold(sacc[kk], lk4[kk], xs[kk]);
+        }
+        tick(2);
+        pf_bar();  // B1.5: every wave has read the K planes of tile it and written its digits
         if (k_next) issue_k(it + 1, aMn);
+        v4i Wd[5];
+        read_wd(Wd);  // zero at it = 0
+        if (it > 0) ++ep_tiles;
+        tick(3);
         // ---- per-pair metadata, score bounds and visibility of tile it
-        v4i lk4[NKT], vl4[NKT];
+        v4i vl4[NKT];
         double adel[NKT][4];
 #pragma unroll
         for (int kk = 0; kk < NKT; ++kk) {
             const int kt = NKT * hh + kk;
-            lk4[kk] = *(const v4i*)&TMc->lsbk[16 * kt + 4 * g];
             vl4[kk] = *(const v4i*)&TMc->vlsb[16 * kt + 4 * g];
             const double2 kA01 = *(const double2*)&TMc->kA[16 * kt + 4 * g];
             const double2 kA23 = *(const double2*)&TMc->kA[16 * kt + 4 * g + 2];
@@ -842,19 +910,16 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                     }
                 }
         }
-        // ---- P.V of tile it - 1 (zero digits at it = 0), certification of tile it: two regions,
-        // each half the channel tiles' MFMAs and one key group's certification, interleaved
+        // ---- P.V of tile it - 1 (zero digits at it = 0) beside the certification of tile it
         v4i Mk[NKT], Ek[NKT];
         uint32_t slowmask = 0;  // pairs the fast path left undecided (cold path below)
         int gm = INT_MIN;
 #pragma unroll
         for (int kk = 0; kk < NKT; ++kk) {
             pv_mfma(Wd, sVp, kk * (NCT / NKT), (kk + 1) * (NCT / NKT));
-            double xs[4];
-            score_fold(sacc[kk], lk4[kk], xs);
             int M[4], E[4];
             bool ok[4];
-            cert4(xs, adel[kk], qm.a, T1s, T2, M, E, ok);
+            cert4(xs[kk], adel[kk], qm.a, T1s, T2, M, E, ok);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bool vis = (vism >> (4 * kk + i)) & 1;
@@ -874,7 +939,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        tick(2);
+        tick(4);
         // ---- cold path: exact decision for the pairs the fast path left undecided. The exact
         // integer score comes from the tile's digit planes (no bf16 reads); only pairs whose
         // digits are inexact (elements rounded at slicing) read the bf16 inputs.
@@ -891,9 +956,15 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 int ls = 3;
                 ++nslow;
                 if (!qbad && !((qm.flags >> 8) & 0xFF) && !(kf >> 8)) {
-                    // 16 dims at a time: one 16-byte chunk per digit plane of q (LDS) and K (tile)
-                    const int8_t* krow = Kg + key * 128;
-                    i128 S = 0;
+                    // exact score from the digit planes: D_st = sum_i q_s,i k_t,i by v_dot4 (|D| <=
+                    // 128 x 2^14), equal weights s + t summed in int32 (<= 4 x 2^21), then
+                    // S = sum_k acc_k 256^k in 128 bits
+                    const uint8_t* krow = (const uint8_t*)Kg + key * 128;
+                    int D[4][4];
+#pragma unroll
+                    for (int sq = 0; sq < 4; ++sq)
+#pragma unroll
+                        for (int tk = 0; tk < 4; ++tk) D[sq][tk] = 0;
                     for (int c16 = 0; c16 < 8; ++c16) {
                         uint4 qc[4], kc[4];
 #pragma unroll
@@ -902,16 +973,24 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                             kc[sp] = *(const uint4*)(krow + 8192 * sp + ((c16 ^ (key & 7)) << 4));
                         }
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) {
-                            int xq = 0, xk = 0;
+                        for (int sq = 0; sq < 4; ++sq)
 #pragma unroll
-                            for (int sp = 3; sp >= 0; --sp) {
-                                const uint32_t wq = (&qc[sp].x)[e >> 2], wk = (&kc[sp].x)[e >> 2];
-                                xq = xq * 256 + (int)(int8_t)(wq >> (8 * (e & 3)));
-                                xk = xk * 256 + (int)(int8_t)(wk >> (8 * (e & 3)));
+                            for (int tk = 0; tk < 4; ++tk) {
+                                int d = D[sq][tk];
+                                d = __builtin_amdgcn_sdot4((int)qc[sq].x, (int)kc[tk].x, d, false);
+                                d = __builtin_amdgcn_sdot4((int)qc[sq].y, (int)kc[tk].y, d, false);
+                                d = __builtin_amdgcn_sdot4((int)qc[sq].z, (int)kc[tk].z, d, false);
+                                D[sq][tk] = __builtin_amdgcn_sdot4((int)qc[sq].w, (int)kc[tk].w, d, false);
                             }
-                            S += (i128)((int64_t)xq * (int64_t)xk);
-                        }
+                    }
+                    i128 S = 0;
+#pragma unroll
+                    for (int k = 6; k >= 0; --k) {
+                        int acc = 0;
+#pragma unroll
+                        for (int sq = 0; sq < 4; ++sq)
+                            if (k - sq >= 0 && k - sq < 4) acc += D[sq][k - sq];
+                        S = S * 256 + (i128)acc;
                     }
                     ls = rn32_prod(P.am, S, P.ae + qm.lsb + TMc->lsbk[key], &tbits);
                 } else if (!qbad) {
@@ -965,83 +1044,42 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 if (live) gm = max(gm, E + TMc->vlsb[key]);
             }
         }
-        tick(3);
-        // ---- the row's largest weight in this tile (both waves of the pair); the base moves
-        // when a weight would exceed 2^38 (G - base > 14 for G = E + vlsb)
+        tick(5);
+        // ---- the row's largest weight in this tile (this wave's 4 lanes of the row), for the
+        // row group's exchange after the next B1
         gm = max(gm, __shfl_xor(gm, 16, 64));
         gm = max(gm, __shfl_xor(gm, 32, 64));
         sX[w * 64 + lane] = PfX{gm, nfrac, 0.0};
-        pf_bar();  // B2: every wave is done with V(it - 1) and its tile metadata
-        if (k_next) issue_v(it + 1, aVn);
-        int nf_pair = nfrac;  // the row group's keys (all SPLIT waves)
-#pragma unroll
-        for (int o = 1; o < SPLIT; ++o) {
-            const PfX x = sX[(rg * SPLIT + (hh + o) % SPLIT) * 64 + lane];
-            gm = max(gm, x.a);
-            nf_pair += x.b;
-        }
-        const bool need_rb = gm != INT_MIN && (base == INT_MIN || gm > base + 14);
-        const int nb = need_rb ? gm - 10 : base;
-        tick(4);
-        if (ep_tiles > 0 && (__ballot(need_rb) != 0 || ep_tiles >= 256)) fold(nf_pair, nb);
-        tick(5);
-        // ---- move bases, then this wave's weight digits (A operand of the P.V MFMA) and Z
-        if (nb != base && base != INT_MIN) z = ldexp(z, max(base - nb, -1100));
-        base = nb;
+        cgm = gm;
 #pragma unroll
         for (int kk = 0; kk < NKT; ++kk) {
-            uint32_t L[4], H[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int Mp = Mk[kk][i];
-                const int sc = Ek[kk][i] - base;
-                const double md = (double)Mp;
-                const double wsc = ldexp(md, sc + vl4[kk][i]);  // <= 2^38
-                z += ldexp(md, sc);                             // md = 0 for masked pairs
-                nv += Mp ? 1 : 0;
-                nfrac += (Mp && sc + vl4[kk][i] < 0) ? 1 : 0;
-                const uint64_t yb = f64_as_u64(wsc + PF_C40);
-                L[i] = (uint32_t)yb;
-                H[i] = (uint32_t)(yb >> 32);
-            }
-            const uint32_t a01 = __builtin_amdgcn_perm(L[1], L[0], 0x05010400u);
-            const uint32_t b01 = __builtin_amdgcn_perm(L[1], L[0], 0x07030602u);
-            const uint32_t a23 = __builtin_amdgcn_perm(L[3], L[2], 0x05010400u);
-            const uint32_t b23 = __builtin_amdgcn_perm(L[3], L[2], 0x07030602u);
-            const uint32_t e01 = __builtin_amdgcn_perm(H[1], H[0], 0x05010400u);
-            const uint32_t e23 = __builtin_amdgcn_perm(H[3], H[2], 0x05010400u);
-            uint32_t* wd = wd_w + kk * 64;
-            wd[0 * 64 * NKT] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
-            wd[1 * 64 * NKT] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
-            wd[2 * 64 * NKT] = __builtin_amdgcn_perm(b23, b01, 0x05040100u) ^ 0x80808080u;
-            wd[3 * 64 * NKT] = __builtin_amdgcn_perm(b23, b01, 0x07060302u) ^ 0x80808080u;
-            wd[4 * 64 * NKT] = __builtin_amdgcn_perm(e23, e01, 0x05040100u) ^ 0x80808080u;
+            cMk[kk] = Mk[kk];
+            cEk[kk] = Ek[kk];
+            cvl[kk] = vl4[kk];
         }
         tick(6);
     };
 
     wait_vm<0>();  // the prologue's global loads: from here on vmcnt counts DMAs (and folds)
-    if (ntiles > 0) {
-        issue_k(0, aM0);
-        issue_v(0, aV0);
-    }
+    if (ntiles > 0) issue_k(0, aM0);
     for (int it = 0; it < ntiles; it += 2) {
         step(PfPar<0>{}, it);
         if (it + 1 < ntiles) step(PfPar<1>{}, it + 1);
     }
-    // ---- drain: P.V of the last tile
+    tick(7);
+    // ---- drain: digits and P.V of the last tile
     if (ntiles > 0) {
         wait_vm<0>();
         pf_bar();
         const bool odd = (ntiles - 1) & 1;
+        rebase_digits((const PfTileMeta*)(odd ? sM1 : sM0));
+        pf_bar();
         v4i Wd[5];
         read_wd(Wd);
-        const PfTileMeta* TMp = (const PfTileMeta*)(odd ? sM1 : sM0);
-#pragma unroll
-        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TMp->EV[16 * (NCT * hh + cc) + j];
         ++ep_tiles;
         pv_mfma(Wd, odd ? sV1 : sV0, 0, NCT);
     }
+    tick(9);
     // ---- row totals for the final rounding: this wave's 4 lanes of the row, then the partner
     z += __shfl_xor(z, 16, 64);
     z += __shfl_xor(z, 32, 64);
@@ -1065,6 +1103,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             z += x.c;
         }
     }
+    tick(10);
     // ---- the last epoch plus the earlier ones, then RN(N/Z) per (row, channel), certified:
     // q = N * RN(1/Z) (two roundings: below 2^-51.9 |q|, inside the 2^-51 |q| term) and
     // delta >= |N/Z - q| from the N bound en and the Z bound eZ
@@ -1092,6 +1131,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         // then one rolled loop certifies them: the rounding code runs once per wave and stays
         // small in the instruction cache
         double2* const qd = (double2*)smem + tid;  // entry e at qd[64 NWB e]
+        tick(11);
         const double omit = (double)ep_tiles * 0x1p20;
 #pragma unroll
         for (int cc = 0; cc < NCT; ++cc) {
@@ -1109,6 +1149,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 qd[64 * NWB * (4 * cc + i)] = make_double2(q, delta);
             }
         }
+        tick(12);
 #pragma unroll 1
         for (int e = 0; e < 4 * NCT; ++e) {
             const int cc = e >> 2, i = e & 3;
@@ -1129,10 +1170,12 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             }
         }
     }
-    tick(7);
+    tick(13);
     if (TIMERS && lane == 0) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
+#pragma unroll
+        for (int i = 9; i < 15; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
         atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)ntiles);
     }
     if (P.stats) {
