@@ -655,11 +655,16 @@ __device__ __forceinline__ i128 floor_shift128(i128 m, int64_t sh, int* lost) {
     return v;
 }
 
+#define EA_T2_THREADS 512
+#define EA_T2_WAVES (EA_T2_THREADS / 64)
 struct T2Smem {
     double T1[256], T2[256];
     int32_t qm[EA_MAXD], qe[EA_MAXD];
-    uint64_t red_hi[EA_THREADS], red_lo[EA_THREADS];
-    int64_t red_i[EA_THREADS];
+    uint64_t red_hi[EA_T2_THREADS], red_lo[EA_T2_THREADS];
+    int64_t red_i[EA_T2_THREADS];
+    // per wave and channel: the N pass's partial maxima, then its 128-bit sums and lost counts
+    int64_t nrw[EA_T2_WAVES][EA_MAXDV];
+    uint64_t ahi[EA_T2_WAVES][EA_MAXDV], alo[EA_T2_WAVES][EA_MAXDV], aer[EA_T2_WAVES][EA_MAXDV];
     int32_t flag;
 };
 
@@ -669,7 +674,7 @@ __device__ void block_reduce_i128(T2Smem& S, i128* v, uint64_t* err) {
     S.red_lo[tid] = (uint64_t)(u128)*v;
     S.red_i[tid] = (int64_t)*err;
     __syncthreads();
-    for (int s = EA_THREADS / 2; s > 0; s >>= 1) {
+    for (int s = EA_T2_THREADS / 2; s > 0; s >>= 1) {
         if (tid < s) {
             u128 a = ((u128)S.red_hi[tid] << 64) | S.red_lo[tid];
             u128 c = ((u128)S.red_hi[tid + s] << 64) | S.red_lo[tid + s];
@@ -689,7 +694,7 @@ __device__ int block_max_i64(T2Smem& S, int64_t x, int64_t* out) {
     int tid = threadIdx.x;
     S.red_i[tid] = x;
     __syncthreads();
-    for (int s = EA_THREADS / 2; s > 0; s >>= 1) {
+    for (int s = EA_T2_THREADS / 2; s > 0; s >>= 1) {
         if (tid < s) S.red_i[tid] = max(S.red_i[tid], S.red_i[tid + s]);
         __syncthreads();
     }
@@ -698,10 +703,10 @@ __device__ int block_max_i64(T2Smem& S, int64_t x, int64_t* out) {
     return 0;
 }
 
-__global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
+__global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
     __shared__ T2Smem S;
     const int tid = threadIdx.x;
-    for (int i = tid; i < 256; i += EA_THREADS) {
+    for (int i = tid; i < 256; i += EA_T2_THREADS) {
         S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
         S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
     }
@@ -723,7 +728,7 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
         const int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
         if (tid == 0) S.flag = 0;
         const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
-        for (int i = tid; i < d; i += EA_THREADS) {
+        for (int i = tid; i < d; i += EA_T2_THREADS) {
             uint32_t x = qr[i];
             int f = (x >> 7) & 0xFF;
             int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
@@ -734,35 +739,64 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
         __syncthreads();
         int myflag = 0;
         if (nkeys > P.t2_keys) myflag = 1;  // workspace too small: not certified
-        // ---- scores, logits, weights: threads over keys
-        int64_t emax = INT64_MIN;
-        for (int64_t j = tid; j < nkeys && !myflag && S.flag < 2; j += EA_THREADS) {
-            int64_t n;
-            if (j < L) n = j;
-            else {
-                // (j - L)-th set bit of mask
-                uint64_t m = mask;
-                for (int64_t c = j - L; c > 0; --c) m &= m - 1;
-                n = P.tree_base[b] + (__ffsll((long long)m) - 1);
+        // ---- scores, logits, weights. Wave wv takes keys wv, wv + 8, ... in batches of 64: for
+        // each key of the batch the wave reads the K row coalesced (lane ln: dims 2 ln, 2 ln + 1),
+        // finds the window base from the lead exponent (wave max) and sums the floor-shifted
+        // products in 128 bits (wave reduction); lane (key % 64) keeps the sum. Then every lane
+        // decides its key's logit and weight at once.
+        const int wv = tid >> 6, ln = tid & 63;
+        uint64_t tq0 = __builtin_amdgcn_s_memtime();
+        // phase clocks (P.timers set): slots 9..13 = scores, Z, N maxima, N sums, rounding
+        auto t2tick = [&](int slot) __attribute__((always_inline)) {
+            if (P.timers) {
+                const uint64_t t = __builtin_amdgcn_s_memtime();
+                if (tid == 0) atomicAdd((unsigned long long*)&P.timers[slot], (unsigned long long)(t - tq0));
+                tq0 = t;
             }
-            const uint16_t* kr = P.k + kv_off(P, b, n, hk, 0);
-            const uint16_t* vr = P.v + kv_off(P, b, n, hk, 1);
+        };
+        const int64_t tb = P.tree_mask ? P.tree_base[b] : 0;
+        auto key_n = [&](int64_t j) -> int64_t {
+            if (j < L) return j;
+            uint64_t m = mask;
+            for (int64_t cc = j - L; cc > 0; --cc) m &= m - 1;
+            return tb + (__ffsll((long long)m) - 1);
+        };
+        int64_t emax = INT64_MIN;
+        // one key per thread, its K row in registers (16-byte loads when rows are aligned)
+        const bool k16 = (((uintptr_t)P.k | (uintptr_t)(P.g.k_page_stride * 2) | (uintptr_t)(P.g.k_slot_stride * 2) |
+                           (uintptr_t)(P.g.k_head_stride * 2)) & 15) == 0 && d == 128;
+        for (int64_t j = tid; j < nkeys && !myflag && S.flag < 2; j += EA_T2_THREADS) {
+            const uint16_t* kr = P.k + kv_off(P, b, key_n(j), hk, 0);
+            // 16 dims (8 dwords) at a time, read twice: the lead exponent, then the window sum
+            auto chunk = [&](int c16, uint32_t (&kw)[8]) __attribute__((always_inline)) {
+                if (k16) {
+                    const uint4 u0 = ((const uint4*)kr)[2 * c16], u1 = ((const uint4*)kr)[2 * c16 + 1];
+                    kw[0] = u0.x; kw[1] = u0.y; kw[2] = u0.z; kw[3] = u0.w;
+                    kw[4] = u1.x; kw[5] = u1.y; kw[6] = u1.z; kw[7] = u1.w;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const int i = 16 * c16 + 2 * c;
+                        kw[c] = (i < d ? (uint32_t)kr[i] : 0u) | ((i + 1 < d ? (uint32_t)kr[i + 1] : 0u) << 16);
+                    }
+                }
+            };
             int lmax = INT_MIN;
             bool bad = false;
-            for (int i = 0; i < d; ++i) {
-                uint32_t x = kr[i];
-                int f = (x >> 7) & 0xFF;
-                if (f == 0xFF) bad = true;
-                int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
-                int p = S.qm[i] * ((x & 0x8000) ? -m : m);
-                if (p) {
-                    int ap = p < 0 ? -p : p;
-                    int lead = S.qe[i] + (f ? f : 1) - 134 + (31 - __clz(ap));
-                    lmax = max(lmax, lead);
+            for (int c16 = 0; c16 < EA_MAXD / 16; ++c16) {
+                uint32_t kw[8];
+                chunk(c16, kw);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int i = 16 * c16 + e;
+                    const uint32_t x = (kw[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
+                    const int f = (x >> 7) & 0xFF;
+                    bad |= f == 0xFF;
+                    const int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                    const int pr = S.qm[i] * ((x & 0x8000) ? -m : m);
+                    if (pr) lmax = max(lmax, S.qe[i] + (f ? f : 1) - 134 + (31 - __clz(pr < 0 ? -pr : pr)));
                 }
             }
-            for (int i = 0; i < dv; ++i)
-                if (((vr[i] >> 7) & 0xFF) == 0xFF) bad = true;
             if (bad) {
                 atomicMax(&S.flag, 2);
                 break;
@@ -770,22 +804,28 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
             int32_t M = 1 << 23;
             int64_t E = -23;
             if (lmax != INT_MIN && P.am != 0) {
-                int base = lmax + 1 - 120;
+                const int base = lmax + 1 - 120;
                 i128 acc = 0;
                 uint64_t err = 0;
-                for (int i = 0; i < d; ++i) {
-                    uint32_t x = kr[i];
-                    int f = (x >> 7) & 0xFF;
-                    int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
-                    int p = S.qm[i] * ((x & 0x8000) ? -m : m);
-                    if (!p) continue;
-                    int lost;
-                    acc += floor_shift128((i128)p, (int64_t)S.qe[i] + (f ? f : 1) - 134 - base, &lost);
-                    err += (uint64_t)lost;
+                for (int c16 = 0; c16 < EA_MAXD / 16; ++c16) {
+                    uint32_t kw[8];
+                    chunk(c16, kw);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int i = 16 * c16 + e;
+                        const uint32_t x = (kw[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
+                        const int f = (x >> 7) & 0xFF;
+                        const int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                        const int pr = S.qm[i] * ((x & 0x8000) ? -m : m);
+                        if (!pr) continue;
+                        int lost;
+                        acc += floor_shift128((i128)pr, (int64_t)S.qe[i] + (f ? f : 1) - 134 - base, &lost);
+                        err += (uint64_t)lost;
+                    }
                 }
-                uint32_t tlo = 0, thi = 0;
-                int slo = rn32_prod(P.am, acc, P.ae + base, &tlo);
-                int shi = err ? rn32_prod(P.am, acc + (i128)err, P.ae + base, &thi) : slo;
+            uint32_t tlo = 0, thi = 0;
+                const int slo = rn32_prod(P.am, acc, P.ae + base, &tlo);
+                const int shi = err ? rn32_prod(P.am, acc + (i128)err, P.ae + base, &thi) : slo;
                 if (!err) thi = tlo;
                 if (slo == 2 && shi == 2) {
                     atomicMax(&S.flag, 2);  // |alpha s| rounds above fp32 max: domain error
@@ -797,16 +837,12 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
                 }
                 int32_t Mi;
                 int32_t Ei;
-                int ws = weight_f64(tlo, S.T1, S.T2, &Mi, &Ei);
-                if (ws == 0) {
+                if (weight_f64(tlo, S.T1, S.T2, &Mi, &Ei) == 0) {
                     M = Mi;
                     E = Ei;
-                } else {
-                    int ww = weight_wide(tlo, &M, &E);
-                    if (ww) {
-                        myflag = 1;
-                        break;
-                    }
+                } else if (weight_wide(tlo, &M, &E)) {
+                    myflag = 1;
+                    break;
                 }
             }
             Mw[j] = M;
@@ -817,6 +853,7 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
         __syncthreads();
         int64_t R;
         block_max_i64(S, emax, &R);
+        t2tick(9);
         int fl = S.flag;
         if (fl == 0 && nkeys > 0) {
             int key_log2 = 0;
@@ -825,70 +862,131 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
             // Z
             i128 z = 0;
             uint64_t ze = 0;
-            for (int64_t j = tid; j < nkeys; j += EA_THREADS) {
+            for (int64_t j = tid; j < nkeys; j += EA_T2_THREADS) {
                 int lost;
                 z += floor_shift128((i128)Mw[j], Ew[j] - (R - F), &lost);
                 ze += (uint64_t)lost;
             }
             block_reduce_i128(S, &z, &ze);
-            // N per channel: threads over channels, loop over keys
-            bool ok = true;
-            for (int c = tid; c < dv; c += EA_THREADS) {
-                int64_t NR = INT64_MIN;
-                for (int64_t j = 0; j < nkeys; ++j) {
-                    int64_t n;
-                    if (j < L) n = j;
-                    else {
-                        uint64_t m = mask;
-                        for (int64_t cc = j - L; cc > 0; --cc) m &= m - 1;
-                        n = P.tree_base[b] + (__ffsll((long long)m) - 1);
-                    }
-                    uint32_t x = P.v[kv_off(P, b, n, hk, 1) + c];
-                    if (!(x & 0x7FFF)) continue;
-                    int f = (x >> 7) & 0xFF;
-                    int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
-                    int64_t Lj = Ew[j] + 24 + (f ? f : 1) - 134 + (31 - __clz(m));
-                    NR = max(NR, Lj);
+            t2tick(10);
+            // N per channel, key-parallel: wave wv takes keys wv, wv + 8, ...; lane ln channels
+            // 2 ln and 2 ln + 1. Pass 1: NR_c = max_j (E_j + 24 + lead(v_jc)); pass 2: the
+            // 128-bit sums of floor(M_j v_jc 2^(E_j + e_jc - base_c)) and their lost counts,
+            // base_c = NR_c - F; partials reduced over the waves through LDS.
+            // batches of 64 keys per wave: lane ln finds key j0 + ln's V row, the row offsets are
+            // broadcast and the batch's V elements loaded together (independent loads in flight)
+            uint32_t vx[16][2];
+            auto load_batch = [&](int64_t j0, int nk) __attribute__((always_inline)) {
+                const int64_t myoff = ln < nk ? kv_off(P, b, key_n(j0 + ln), hk, 1) : 0;
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    const int64_t o = __shfl(myoff, kk, 64);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) vx[kk][h] = (kk < nk && 2 * ln + h < dv) ? (uint32_t)P.v[o + 2 * ln + h] : 0u;
                 }
+            };
+            const int64_t nvb = (nkeys + 16 * EA_T2_WAVES - 1) / (16 * EA_T2_WAVES);
+            int64_t nr[2] = {INT64_MIN, INT64_MIN};
+            bool vbad = false;
+            for (int64_t bt = 0; bt < nvb; ++bt) {
+                const int64_t j0 = (bt * EA_T2_WAVES + wv) * 16;
+                if (j0 >= nkeys) break;
+                const int nk = (int)min((int64_t)16, nkeys - j0);
+                load_batch(j0, nk);
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    if (kk >= nk) continue;
+                    const int64_t e = Ew[j0 + kk] + 24;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                    const uint32_t x = vx[kk][h];
+                    if (!(x & 0x7FFF)) continue;
+                    const int f = (x >> 7) & 0xFF;
+                    if (f == 0xFF) vbad = true;
+                    const int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                    nr[h] = max(nr[h], e + (f ? f : 1) - 134 + (31 - __clz(m)));
+                    }
+                }
+            }
+            if (vbad) atomicMax(&S.flag, 2);  // NaN/inf in a visible V row: a domain error
+            t2tick(11);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                if (2 * ln + h < EA_MAXDV) S.nrw[wv][2 * ln + h] = nr[h];
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = 2 * ln + h;
+                nr[h] = INT64_MIN;
+                for (int q = 0; q < EA_T2_WAVES; ++q) nr[h] = max(nr[h], S.nrw[q][c]);
+            }
+            i128 acc[2] = {0, 0};
+            uint64_t err[2] = {0, 0};
+            for (int64_t bt = 0; bt < nvb; ++bt) {
+                const int64_t j0 = (bt * EA_T2_WAVES + wv) * 16;
+                if (j0 >= nkeys) break;
+                const int nk = (int)min((int64_t)16, nkeys - j0);
+                load_batch(j0, nk);
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    if (kk >= nk) continue;
+                    const int64_t Ej = Ew[j0 + kk];
+                    const int64_t Mj = Mw[j0 + kk];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t x = vx[kk][h];
+                        if (!(x & 0x7FFF) || nr[h] == INT64_MIN) continue;
+                        const int f = (x >> 7) & 0xFF;
+                        const int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
+                        const int64_t vm = (x & 0x8000) ? -m : m;
+                        int lost;
+                        acc[h] += floor_shift128((i128)(Mj * vm), Ej + (f ? f : 1) - 134 - (nr[h] - F), &lost);
+                        err[h] += (uint64_t)lost;
+                    }
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = 2 * ln + h;
+                if (c < EA_MAXDV) {
+                    S.ahi[wv][c] = (uint64_t)((u128)acc[h] >> 64);
+                    S.alo[wv][c] = (uint64_t)(u128)acc[h];
+                    S.aer[wv][c] = err[h];
+                }
+            }
+            __syncthreads();
+            t2tick(12);
+            bool ok = true;
+            for (int c = tid; c < dv; c += EA_T2_THREADS) {
+                int64_t NR = INT64_MIN;
+                for (int q = 0; q < EA_T2_WAVES; ++q) NR = max(NR, S.nrw[q][c]);
                 uint32_t bits = 0;
                 if (NR != INT64_MIN) {
                     const int64_t base = NR - F;
-                    i128 acc = 0;
+                    u128 accu = 0;
                     uint64_t err = 0;
-                    for (int64_t j = 0; j < nkeys; ++j) {
-                        int64_t n;
-                        if (j < L) n = j;
-                        else {
-                            uint64_t m = mask;
-                            for (int64_t cc = j - L; cc > 0; --cc) m &= m - 1;
-                            n = P.tree_base[b] + (__ffsll((long long)m) - 1);
-                        }
-                        uint32_t x = P.v[kv_off(P, b, n, hk, 1) + c];
-                        if (!(x & 0x7FFF)) continue;
-                        int f = (x >> 7) & 0xFF;
-                        int m = (int)(x & 0x7F) | (f ? 0x80 : 0);
-                        int64_t vm = (x & 0x8000) ? -m : m;
-                        int lost;
-                        acc += floor_shift128((i128)((int64_t)Mw[j] * vm), Ew[j] + (f ? f : 1) - 134 - base, &lost);
-                        err += (uint64_t)lost;
+                    for (int q = 0; q < EA_T2_WAVES; ++q) {
+                        accu += ((u128)S.ahi[q][c] << 64) | S.alo[q][c];
+                        err += S.aer[q][c];
                     }
+                    const i128 acc = (i128)accu;
                     // interval [acc, acc+err] * 2^base over [z, z+ze] * 2^(R-F)
                     i128 Zlo = z, Zhi = z + (i128)ze;
                     i128 Nlo = acc, Nhi = acc + (i128)err;
-                    i128 ln, ld, hn, hd;
+                    i128 ln_, ld, hn, hd;
                     if (Nlo >= 0) {
-                        ln = Nlo; ld = Zhi; hn = Nhi; hd = Zlo;
+                        ln_ = Nlo; ld = Zhi; hn = Nhi; hd = Zlo;
                     } else if (Nhi <= 0) {
-                        ln = Nlo; ld = Zlo; hn = Nhi; hd = Zhi;
+                        ln_ = Nlo; ld = Zlo; hn = Nhi; hd = Zhi;
                     } else {
-                        ln = Nlo; ld = Zlo; hn = Nhi; hd = Zlo;
+                        ln_ = Nlo; ld = Zlo; hn = Nhi; hd = Zlo;
                     }
                     int64_t sh = base - (R - F);
                     int p = P.out_fp32 ? 24 : 8, qmin = P.out_fp32 ? -149 : -133;
                     if (Zlo <= 0 || sh > 100000 || sh < -100000) {
                         ok = false;
                     } else {
-                        rnd rl = round_ratio(ln < 0 ? (u128)(-ln) : (u128)ln, (u128)ld, (int)sh, ln < 0 ? -1 : 1, p, qmin);
+                        rnd rl = round_ratio(ln_ < 0 ? (u128)(-ln_) : (u128)ln_, (u128)ld, (int)sh, ln_ < 0 ? -1 : 1, p, qmin);
                         rnd rh = round_ratio(hn < 0 ? (u128)(-hn) : (u128)hn, (u128)hd, (int)sh, hn < 0 ? -1 : 1, p, qmin);
                         if (!rnd_eq(rl, rh)) ok = false;
                         else bits = rnd_bits(rl, P.out_fp32);
@@ -899,15 +997,16 @@ __global__ void __launch_bounds__(EA_THREADS) ea_tier2(Params P) {
             }
             if (!ok) atomicMax(&S.flag, 1);
             __syncthreads();
+            t2tick(13);
             fl = S.flag;
         } else if (fl == 0) {
-            for (int c = tid; c < dv; c += EA_THREADS) {
+            for (int c = tid; c < dv; c += EA_T2_THREADS) {
                 if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
                 else ((uint16_t*)P.out)[obase + c] = 0;
             }
         }
         if (fl != 0) {
-            for (int c = tid; c < dv; c += EA_THREADS) {
+            for (int c = tid; c < dv; c += EA_T2_THREADS) {
                 if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
                 else ((uint16_t*)P.out)[obase + c] = 0;
             }
@@ -1137,7 +1236,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         if ((rc = mark(2))) return rc;
         if ((rc = mark(3))) return rc;
         if (o->tier2) {
-            hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_THREADS), 0, st, P);
+            hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_T2_THREADS), 0, st, P);
             rc = herr(hipGetLastError());
             if (rc) return rc;
         }
@@ -1191,7 +1290,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     if (rc) return rc;
     if ((rc = mark(3))) return rc;
     if (o->tier2) {
-        hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_THREADS), 0, st, P);
+        hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_T2_THREADS), 0, st, P);
         rc = herr(hipGetLastError());
         if (rc) return rc;
     }
