@@ -1,0 +1,217 @@
+// Merge of the KV-split partials of one row and the certified final rounding, shared by the
+// combine kernel (ea_hip.hip) and the decode kernel's last-arriving block (ea_decode.hip).
+#pragma once
+#include "ea_params.h"
+
+namespace ea {
+
+__device__ inline void combine_row(const Params& P, int64_t row, int lane) {
+    const int dv = P.g.head_dim_v;
+    const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
+    const int64_t b = row / ((int64_t)T * Hq);
+    const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
+    const int hk = hq / P.grp, gi = hq % P.grp;
+    const int seg = (int)(b * P.g.num_kv_heads + hk);
+    const int lr = t * P.grp + gi;
+    const int rbk = lr / P.rb;
+    const int ns = P.nsplit;
+
+    if (ns <= 64) {
+        // lane i holds split s_i = merge_order[i] (or i): its scalars load in parallel, R, Z and the
+        // bound come from wave reductions (any summation order gives the same certified bits), and
+        // each lane's per-split channel loads are issued 8 at a time before they are used
+        int si = lane;
+        bool mo_ok = P.merge_order != nullptr;
+        if (mo_ok) {
+            const int m = lane < ns ? P.merge_order[lane] : 0;
+            const uint64_t bit = (lane < ns && m >= 0 && m < ns) ? (1ull << m) : 0ull;
+            uint64_t seen = bit;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) seen |= __shfl_xor(seen, o, 64);
+            mo_ok = seen == (ns == 64 ? ~0ull : ((1ull << ns) - 1));
+            if (mo_ok) si = m;
+        }
+        int n_i = 0, r_i = INT_MIN;
+        double z_i = 0.0;
+        if (lane < ns) {
+            const int64_t o = (int64_t)si * P.rows + row;
+            n_i = P.pn[o];
+            r_i = P.pR[o];
+            z_i = P.pZ[o];
+        }
+        const bool qbad = P.qinfo[row * 5 + 4] != 0;
+        int flag = (__ballot(n_i < 0) != 0 || qbad) ? 1 : 0;
+        const int R = wave_max_i(n_i > 0 ? r_i : INT_MIN);
+        uint16_t* o16 = (uint16_t*)P.out;
+        uint32_t* o32 = (uint32_t*)P.out;
+        const int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
+        if (!flag && R == INT_MIN) {
+            // no visible key: the output is +0 (docs/SPEC.md step 5, empty set)
+            for (int c = lane; c < dv; c += 64) {
+                if (P.out_fp32) o32[obase + c] = 0;
+                else o16[obase + c] = 0;
+            }
+            if (lane == 0) P.flags[row] = 0;
+            return;
+        }
+        const double up = 0x1p-53 * (1.0 + 0x1p-28);
+        const int dsh_i = (n_i > 0 && R != INT_MIN) ? r_i - R : 0;
+        if (__ballot(n_i > 0 && dsh_i < -900) != 0) flag = 1;
+        const double zs_i = n_i > 0 ? ldexp(z_i, max(dsh_i, -1000)) : 0.0;
+        double Z = zs_i, A = zs_i * (double)(n_i + ns + 4);
+        int nterm = n_i > 0 ? n_i : 0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            Z += __shfl_xor(Z, o, 64);
+            A += __shfl_xor(A, o, 64);
+            nterm += __shfl_xor(nterm, o, 64);
+        }
+        const double tiny = (double)(nterm + 64 * ns + 64) * 0x1p-1074;
+        const double eZ = A * up + tiny;
+        if (!(Z > 2.0 * eZ) || !isfinite(Z)) flag = 1;
+        bool ok = !flag;
+        for (int c = lane; c < dv; c += 64) {
+            uint32_t bits = 0;
+            if (!flag) {
+                double N = 0.0;
+                float vmaxf = 0.0f;
+                for (int i0 = 0; i0 < ns; i0 += 8) {
+                    double pn8[8];
+                    float pv8[8];
+                    int sh8[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const int i = i0 + k;
+                        const int s = __shfl(si, i & 63, 64), n = __shfl(n_i, i & 63, 64);
+                        sh8[k] = __shfl(dsh_i, i & 63, 64);
+                        const bool use = i < ns && n > 0;
+                        const int64_t o = (int64_t)s * P.rows + row;
+                        pn8[k] = use ? P.pN[o * dv + c] : 0.0;
+                        pv8[k] = use ? P.pV[(((int64_t)s * P.nseg + seg) * P.nrb + rbk) * dv + c] : 0.0f;
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        N += ldexp(pn8[k], max(sh8[k], -1000));
+                        vmaxf = fmaxf(vmaxf, pv8[k]);
+                        if (!(pv8[k] <= 3.4028235e38f)) vmaxf = __builtin_inff();
+                    }
+                }
+                const double eN = A * up * (double)vmaxf + tiny;
+                const double q = N / Z;
+                const double aq = fabs(q);
+                const double delta = (eN + aq * eZ) / (Z - eZ) * (1.0 + 0x1p-40) + aq * 0x1p-51 + 0x1p-1070;
+                if (!isfinite(q) || !isfinite(delta) || !certify_round(q, delta, P.out_fp32, &bits)) ok = false;
+            }
+            if (P.out_fp32) o32[obase + c] = bits;
+            else o16[obase + c] = (uint16_t)bits;
+        }
+        const int bad = wave_max_i(ok ? 0 : 1);
+        if (lane == 0) {
+            P.flags[row] = bad ? 1 : 0;
+            if (P.stats && bad && !flag) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
+            if (bad) {
+                const int slot = atomicAdd(P.wl_cnt, 1);
+                P.wl[slot] = (int32_t)row;
+            }
+            if (P.stats) {
+                atomicAdd((unsigned long long*)&P.stats[0], 1ull);
+                if (bad) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
+            }
+        }
+        return;
+    }
+    // the caller's merge order is used only if it is a permutation of [0, ns); any order gives
+    // the same certified bits, so an invalid one falls back to 0..ns-1
+    bool use_mo = P.merge_order != nullptr && ns <= 64;
+    if (use_mo) {
+        uint64_t seen = 0;
+        for (int i = 0; i < ns; ++i) {
+            int s = P.merge_order[i];
+            if (s < 0 || s >= ns) use_mo = false;
+            else seen |= 1ull << s;
+        }
+        if (seen != (ns == 64 ? ~0ull : ((1ull << ns) - 1))) use_mo = false;
+    }
+    int flag = 0;
+    int R = INT_MIN;
+    for (int s = 0; s < ns; ++s) {
+        int64_t o = (int64_t)s * P.rows + row;
+        int n = P.pn[o];
+        if (n < 0) flag = 1;
+        else if (n > 0) R = max(R, P.pR[o]);
+    }
+    if (P.qinfo[row * 5 + 4]) flag = 1;
+    uint16_t* o16 = (uint16_t*)P.out;
+    uint32_t* o32 = (uint32_t*)P.out;
+    int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
+    const double up = 0x1p-53 * (1.0 + 0x1p-28);
+    double Z = 0.0, A = 0.0;
+    int nterm = 0;
+    if (!flag && R != INT_MIN) {
+        for (int i = 0; i < ns; ++i) {
+            int s = use_mo ? P.merge_order[i] : i;
+            int64_t o = (int64_t)s * P.rows + row;
+            int n = P.pn[o];
+            if (n <= 0) continue;
+            int dsh = P.pR[o] - R;
+            if (dsh < -900) flag = 1;
+            double zs = ldexp(P.pZ[o], max(dsh, -1000));
+            Z += zs;
+            A += zs * (double)(n + ns + 4);
+            nterm += n;
+        }
+    }
+    if (!flag && R == INT_MIN) {
+        // no visible key: the output is +0 (docs/SPEC.md step 5, empty set)
+        for (int c = lane; c < dv; c += 64) {
+            if (P.out_fp32) o32[obase + c] = 0;
+            else o16[obase + c] = 0;
+        }
+        if (lane == 0) P.flags[row] = 0;
+        return;
+    }
+    double tiny = (double)(nterm + 64 * ns + 64) * 0x1p-1074;
+    double eZ = A * up + tiny;
+    if (!(Z > 2.0 * eZ) || !isfinite(Z)) flag = 1;
+    bool ok = !flag;
+    for (int c = lane; c < dv; c += 64) {
+        uint32_t bits = 0;
+        if (!flag) {
+            double N = 0.0;
+            float vmaxf = 0.0f;
+            for (int i = 0; i < ns; ++i) {
+                int s = use_mo ? P.merge_order[i] : i;
+                int64_t o = (int64_t)s * P.rows + row;
+                int n = P.pn[o];
+                if (n <= 0) continue;
+                N += ldexp(P.pN[o * dv + c], max(P.pR[o] - R, -1000));
+                float vm = P.pV[(((int64_t)s * P.nseg + seg) * P.nrb + rbk) * dv + c];
+                vmaxf = fmaxf(vmaxf, vm);
+                if (!(vm <= 3.4028235e38f)) vmaxf = __builtin_inff();
+            }
+            double eN = A * up * (double)vmaxf + tiny;
+            double q = N / Z;
+            double aq = fabs(q);
+            double delta = (eN + aq * eZ) / (Z - eZ) * (1.0 + 0x1p-40) + aq * 0x1p-51 + 0x1p-1070;
+            if (!isfinite(q) || !isfinite(delta) || !certify_round(q, delta, P.out_fp32, &bits)) ok = false;
+        }
+        if (P.out_fp32) o32[obase + c] = bits;
+        else o16[obase + c] = (uint16_t)bits;
+    }
+    // all lanes agree
+    int bad = wave_max_i(ok ? 0 : 1);
+    if (lane == 0) {
+        P.flags[row] = bad ? 1 : 0;
+        if (P.stats && bad && !flag) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
+        if (bad) {
+            int slot = atomicAdd(P.wl_cnt, 1);
+            P.wl[slot] = (int32_t)row;
+        }
+        if (P.stats) {
+            atomicAdd((unsigned long long*)&P.stats[0], 1ull);
+            if (bad) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
+        }
+    }
+}
+
+}  // namespace ea

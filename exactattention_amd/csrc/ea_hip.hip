@@ -22,6 +22,7 @@
 #include "../../include/exactattn_hip.h"
 #include "ea_device.h"
 #include "ea_params.h"
+#include "ea_combine.h"
 
 using namespace ea;
 
@@ -528,111 +529,9 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
 //   eZ = u' A + tiny,  eN_c = u' A max_s Vmax_sc + tiny.
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) ea_combine(Params P) {
-    const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= P.rows) return;
-    const int dv = P.g.head_dim_v;
-    const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
-    const int64_t b = row / ((int64_t)T * Hq);
-    const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
-    const int hk = hq / P.grp, gi = hq % P.grp;
-    const int seg = (int)(b * P.g.num_kv_heads + hk);
-    const int lr = t * P.grp + gi;
-    const int rbk = lr / P.rb;
-    const int ns = P.nsplit;
-
-    // the caller's merge order is used only if it is a permutation of [0, ns); any order gives
-    // the same certified bits, so an invalid one falls back to 0..ns-1
-    bool use_mo = P.merge_order != nullptr && ns <= 64;
-    if (use_mo) {
-        uint64_t seen = 0;
-        for (int i = 0; i < ns; ++i) {
-            int s = P.merge_order[i];
-            if (s < 0 || s >= ns) use_mo = false;
-            else seen |= 1ull << s;
-        }
-        if (seen != (ns == 64 ? ~0ull : ((1ull << ns) - 1))) use_mo = false;
-    }
-    int flag = 0;
-    int R = INT_MIN;
-    for (int s = 0; s < ns; ++s) {
-        int64_t o = (int64_t)s * P.rows + row;
-        int n = P.pn[o];
-        if (n < 0) flag = 1;
-        else if (n > 0) R = max(R, P.pR[o]);
-    }
-    if (P.qinfo[row * 5 + 4]) flag = 1;
-    uint16_t* o16 = (uint16_t*)P.out;
-    uint32_t* o32 = (uint32_t*)P.out;
-    int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
-    const double up = 0x1p-53 * (1.0 + 0x1p-28);
-    double Z = 0.0, A = 0.0;
-    int nterm = 0;
-    if (!flag && R != INT_MIN) {
-        for (int i = 0; i < ns; ++i) {
-            int s = use_mo ? P.merge_order[i] : i;
-            int64_t o = (int64_t)s * P.rows + row;
-            int n = P.pn[o];
-            if (n <= 0) continue;
-            int dsh = P.pR[o] - R;
-            if (dsh < -900) flag = 1;
-            double zs = ldexp(P.pZ[o], max(dsh, -1000));
-            Z += zs;
-            A += zs * (double)(n + ns + 4);
-            nterm += n;
-        }
-    }
-    if (!flag && R == INT_MIN) {
-        // no visible key: the output is +0 (docs/SPEC.md step 5, empty set)
-        for (int c = lane; c < dv; c += 64) {
-            if (P.out_fp32) o32[obase + c] = 0;
-            else o16[obase + c] = 0;
-        }
-        if (lane == 0) P.flags[row] = 0;
-        return;
-    }
-    double tiny = (double)(nterm + 64 * ns + 64) * 0x1p-1074;
-    double eZ = A * up + tiny;
-    if (!(Z > 2.0 * eZ) || !isfinite(Z)) flag = 1;
-    bool ok = !flag;
-    for (int c = lane; c < dv; c += 64) {
-        uint32_t bits = 0;
-        if (!flag) {
-            double N = 0.0;
-            float vmaxf = 0.0f;
-            for (int i = 0; i < ns; ++i) {
-                int s = use_mo ? P.merge_order[i] : i;
-                int64_t o = (int64_t)s * P.rows + row;
-                int n = P.pn[o];
-                if (n <= 0) continue;
-                N += ldexp(P.pN[o * dv + c], max(P.pR[o] - R, -1000));
-                float vm = P.pV[(((int64_t)s * P.nseg + seg) * P.nrb + rbk) * dv + c];
-                vmaxf = fmaxf(vmaxf, vm);
-                if (!(vm <= 3.4028235e38f)) vmaxf = __builtin_inff();
-            }
-            double eN = A * up * (double)vmaxf + tiny;
-            double q = N / Z;
-            double aq = fabs(q);
-            double delta = (eN + aq * eZ) / (Z - eZ) * (1.0 + 0x1p-40) + aq * 0x1p-51 + 0x1p-1070;
-            if (!isfinite(q) || !isfinite(delta) || !certify_round(q, delta, P.out_fp32, &bits)) ok = false;
-        }
-        if (P.out_fp32) o32[obase + c] = bits;
-        else o16[obase + c] = (uint16_t)bits;
-    }
-    // all lanes agree
-    int bad = wave_max_i(ok ? 0 : 1);
-    if (lane == 0) {
-        P.flags[row] = bad ? 1 : 0;
-        if (P.stats && bad && !flag) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
-        if (bad) {
-            int slot = atomicAdd(P.wl_cnt, 1);
-            P.wl[slot] = (int32_t)row;
-        }
-        if (P.stats) {
-            atomicAdd((unsigned long long*)&P.stats[0], 1ull);
-            if (bad) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
-        }
-    }
+    combine_row(P, row, threadIdx.x & 63);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -706,6 +605,7 @@ __device__ int block_max_i64(T2Smem& S, int64_t x, int64_t* out) {
 __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
     __shared__ T2Smem S;
     const int tid = threadIdx.x;
+    if ((int)blockIdx.x >= *P.wl_cnt) return;  // no listed row for this block (the usual case)
     for (int i = tid; i < 256; i += EA_T2_THREADS) {
         S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
         S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
