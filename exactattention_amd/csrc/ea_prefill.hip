@@ -49,6 +49,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr double PF_U = 0x1p-53 * (1.0 + 0x1p-28);
+#ifndef PF_EARLY_K
+#define PF_EARLY_K 1
+#endif
 #ifndef PF_VALU_PER_MFMA
 #define PF_VALU_PER_MFMA 5
 #endif
@@ -761,7 +764,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     // ---- after B1: the row group's maxima of the previous tile are in sX. Move the base (folding
     // the epoch first when it moves or is 256 tiles old), add the previous tile's inexact-V
     // counts, then write the previous tile's weight digits (A operand of the P.V MFMA) to sWD.
-    auto rebase_digits = [&](const PfTileMeta* TMprev) __attribute__((always_inline)) {
+    auto rebase_digits = [&](const double (&evp)[NCT]) __attribute__((always_inline)) {
         int gm = cgm;
         int nf_pair = nfrac;  // the row group's keys (all SPLIT waves) of the epoch
 #pragma unroll
@@ -775,7 +778,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const int nb = need_rb ? gm - 10 : base;
         if (ep_tiles > 0 && (__ballot(need_rb) != 0 || ep_tiles >= 256)) fold(nf_pair, nb);
 #pragma unroll
-        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += TMprev->EV[16 * (NCT * hh + cc) + j];
+        for (int cc = 0; cc < NCT; ++cc) EVs[cc] += evp[cc];
         if (nb != base && base != INT_MIN) z = ldexp(z, max(base - nb, -1100));
         base = nb;
     #pragma unroll
@@ -823,7 +826,9 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const uint32_t aMn = PA ? aM0 : aM1;        // metadata of tile it + 1
         const bool k_next = it + 1 < ntiles;
         tick(7);
-        wait_vm<0>();  // K(it) and its metadata (issued at B1.5 of the previous step) landed
+        // every DMA landed: K(it) and its metadata (issued early in the previous step) and V(it - 1)
+        // (issued after them; the P.V of this step reads it and no later wait covers it)
+        wait_vm<0>();
         tick(14);
         pf_bar();      // B1
         tick(0);
@@ -843,7 +848,15 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             for (int kk = 0; kk < NKT; ++kk) score_mfma<false>(kb, qb, NKT * hh + kk, sacc[kk]);
         }
         tick(1);
-        if (it > 0) rebase_digits(TMp);
+        // the previous tile's inexact-V counts, read before its metadata buffer is reloaded
+        double evp[NCT];
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) evp[cc] = TMp->EV[16 * (NCT * hh + cc) + j];
+        if (PF_EARLY_K) {
+            pf_bar();  // every wave has read the K planes of tile it: K(it+1) starts loading now
+            if (k_next) issue_k(it + 1, aMn);
+        }
+        if (it > 0) rebase_digits(evp);
         issue_v(it, aVc);
         v4i lk4[NKT];
         double xs[NKT][4];
@@ -854,7 +867,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         }
         tick(2);
         pf_bar();  // B1.5: every wave has read the K planes of tile it and written its digits
-        if (k_next) issue_k(it + 1, aMn);
+        if (!PF_EARLY_K && k_next) issue_k(it + 1, aMn);
         v4i Wd[5];
         read_wd(Wd);  // zero at it = 0
         if (it > 0) ++ep_tiles;
@@ -1072,7 +1085,11 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         wait_vm<0>();
         pf_bar();
         const bool odd = (ntiles - 1) & 1;
-        rebase_digits((const PfTileMeta*)(odd ? sM1 : sM0));
+        const PfTileMeta* TMl = (const PfTileMeta*)(odd ? sM1 : sM0);
+        double evp[NCT];
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) evp[cc] = TMl->EV[16 * (NCT * hh + cc) + j];
+        rebase_digits(evp);
         pf_bar();
         v4i Wd[5];
         read_wd(Wd);

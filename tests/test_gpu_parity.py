@@ -435,3 +435,25 @@ def test_prefill_c3_golden_hash(gpu):
     assert st["prefill_kernel_rows"] == _rows(p), st
     assert not np.any(flags), st
     assert hashlib.sha256(got.tobytes()).hexdigest() == gold, st
+
+
+def test_prefill_c3_back_to_back(gpu):
+    """C3 launched 12 times in a row with no host synchronisation between steps: the kernel's
+    pipeline (tile DMA into LDS overlapping the MFMA work) must give the same certified rows in
+    every step, so no row may leave the prefill kernel uncertified and the last output still
+    carries the golden hash."""
+    import torch
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    p = configs.c3()
+    ab = configs.alpha_bits()
+    gold = json.load(open(os.path.join(GOLD, "baseline_sha256.json")))["C3"]["sha256"]
+    dp = DeviceProblem(p, "bf16", 0, "cuda:0")
+    steps = 12
+    for _ in range(steps):
+        launch_hip(dp, ab)
+    torch.cuda.synchronize()
+    st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    out = dp.out.cpu().numpy().view(np.uint16)
+    assert st["prefill_kernel_rows"] == steps * _rows(p), st
+    assert st["tier1_flagged"] == 0 and st["uncertified_final"] == 0, st
+    assert hashlib.sha256(out.tobytes()).hexdigest() == gold, st
