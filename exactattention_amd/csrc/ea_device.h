@@ -186,7 +186,9 @@ __device__ __forceinline__ int weight_f64(uint32_t t_bits, const double* T1, con
 // fp32 (RN-even, gradual underflow, +0 for every zero). Returns true and the bits when every
 // point of the interval rounds to the same value.
 // ----------------------------------------------------------------------------------------------
-__device__ __forceinline__ bool certify_round(double x, double r, int fp32, uint32_t* bits) {
+// General case: RN of x from its significand, then both neighbouring rounding midpoints at least
+// 2r away from |x|.
+__device__ __forceinline__ bool certify_round_general(double x, double r, int fp32, uint32_t* bits) {
     const int p = fp32 ? 24 : 8;
     const int qmin = fp32 ? -149 : -133;
     // zero region: |v| <= 2^(qmin-1) rounds to +0 (the boundary is a tie to even zero)
@@ -250,6 +252,36 @@ __device__ __forceinline__ bool certify_round(double x, double r, int fp32, uint
     }
     *bits = (sign << (p - 1 + 8)) | (field << (p - 1)) | frac;
     return true;
+}
+
+// Common case in a few integer operations: the interval lies in the format's normal range and
+// both of its ends round to the same pattern (rounding is monotone, so every point between does).
+// The ends are computed in fp64 on r' = r + |x| 2^-50 + 2^-1070, which covers the rounding of
+// the two additions: fl(|x| - r') <= |x| - r and fl(|x| + r') >= |x| + r whenever |x| - r' > 0.
+// RN-even to p bits on the fp64 encoding: add 2^(S-1) - 1 plus the kept lsb, drop S = 53 - p
+// bits; a carry runs into the exponent field by itself. bf16 and fp32 share fp32's exponent
+// range, normal from 2^-126; ends at or above 2^127 are left to the general case.
+__device__ __forceinline__ bool certify_round_normal(double x, double r, int fp32, uint32_t* bits) {
+    const double ax = fabs(x);
+    const double rr = __fma_rn(ax, 0x1p-50, r) + 0x1p-1070;
+    const double lo = ax - rr, hi = ax + rr;
+    if (!(lo >= 0x1p-126) || !(hi < 0x1p127)) return false;  // also NaN
+    const int S = fp32 ? 29 : 45;
+    const uint64_t bl = f64_as_u64(lo), bh = f64_as_u64(hi);
+    const uint64_t half = (1ull << (S - 1)) - 1;
+    const uint64_t ql = (bl + half + ((bl >> S) & 1)) >> S;
+    const uint64_t qh = (bh + half + ((bh >> S) & 1)) >> S;
+    if (ql != qh) return false;
+    // ql = [fp64 exponent field 11 bits][p - 1 fraction bits]: rebias the exponent 1023 -> 127
+    const uint32_t sign = (uint32_t)(f64_as_u64(x) >> 63);
+    const uint32_t mag = (uint32_t)(ql - ((uint64_t)(1023 - 127) << (52 - S)));
+    *bits = (sign << (fp32 ? 31 : 15)) | mag;
+    return true;
+}
+
+__device__ __forceinline__ bool certify_round(double x, double r, int fp32, uint32_t* bits) {
+    if (certify_round_normal(x, r, fp32, bits)) return true;
+    return certify_round_general(x, r, fp32, bits);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -493,41 +525,50 @@ __device__ inline uint32_t rnd_bits(const rnd& r, int fp32) {
     return (sg << (p - 1 + 8)) | (field << (p - 1)) | frac;
 }
 
-// RN32 of (am * X) * 2^E with X a signed 128-bit integer and |am| < 2^24: the tier-2 logit.
-// status 0 ok, 2 overflow. Zero gives bits 0.
+// (W >> s) mod 2^64 for the 192-bit W = (w2 : w1 : w0) and s >= 0
+__device__ __forceinline__ uint64_t shr192(uint64_t w2, uint64_t w1, uint64_t w0, int s) {
+    if (s >= 192) return 0;
+    if (s >= 128) return w2 >> (s - 128);
+    if (s >= 64) return s == 64 ? w1 : (w1 >> (s - 64)) | (w2 << (128 - s));
+    return s == 0 ? w0 : (w0 >> s) | (w1 << (64 - s));
+}
+// any of bits [0, m) of W set, m >= 0
+__device__ __forceinline__ bool low_bits192(uint64_t w2, uint64_t w1, uint64_t w0, int m) {
+    if (m >= 192) return (w0 | w1 | w2) != 0;
+    if (m >= 128) return (w0 | w1) != 0 || (m > 128 && (w2 & ((1ull << (m - 128)) - 1)) != 0);
+    if (m >= 64) return w0 != 0 || (m > 64 && (w1 & ((1ull << (m - 64)) - 1)) != 0);
+    return m > 0 && (w0 & ((1ull << m) - 1)) != 0;
+}
+
+// RN32 of (am * X) * 2^E with X a signed 128-bit integer and |am| < 2^24: the exact logit.
+// status 0 ok, 2 overflow. Zero gives bits 0. The 152-bit product stays in three 64-bit words;
+// the kept bits, the rounding bit and the sticky bit come from word shifts (no bit loops, no
+// indexed arrays).
 __device__ inline int rn32_prod(int32_t am, i128 X, int E, uint32_t* bits) {
     if (X == 0 || am == 0) {
         *bits = 0;
         return 0;
     }
-    int sign = ((X < 0) != (am < 0)) ? -1 : 1;
-    u128 ax = X < 0 ? (u128)(-X) : (u128)X;
-    uint64_t aa = (uint64_t)(am < 0 ? -(int64_t)am : am);
-    // 152-bit product in three 64-bit words: ax * aa
-    u128 lo = (u128)(uint64_t)ax * aa;
-    u128 hi = (u128)(uint64_t)(ax >> 64) * aa + (lo >> 64);
-    uint64_t w0 = (uint64_t)lo, w1 = (uint64_t)hi, w2 = (uint64_t)(hi >> 64);
-    mw m;
-    mw_zero(m);
-    m.w[0] = (uint32_t)w0; m.w[1] = (uint32_t)(w0 >> 32);
-    m.w[2] = (uint32_t)w1; m.w[3] = (uint32_t)(w1 >> 32);
-    m.w[4] = (uint32_t)w2; m.w[5] = (uint32_t)(w2 >> 32);
-    int bl = mw_bitlen(m);
-    long k = (long)bl - 1 + E;
+    const int sign = ((X < 0) != (am < 0)) ? -1 : 1;
+    const u128 ax = X < 0 ? (u128)(-X) : (u128)X;
+    const uint64_t aa = (uint64_t)(am < 0 ? -(int64_t)am : am);
+    const u128 lo = (u128)(uint64_t)ax * aa;
+    const u128 hi = (u128)(uint64_t)(ax >> 64) * aa + (lo >> 64);
+    const uint64_t w0 = (uint64_t)lo, w1 = (uint64_t)hi, w2 = (uint64_t)(hi >> 64);
+    const int bl = w2 ? 192 - __clzll(w2) : (w1 ? 128 - __clzll(w1) : 64 - __clzll(w0));
+    const long k = (long)bl - 1 + E;  // floor(log2 |am X 2^E|)
     long qe = k - 23;
     if (qe < -149) qe = -149;
-    long lo_bit = qe - E;
-    uint64_t q = 0;
-    int rb = 0, st = 0;
+    const long lo_bit = qe - E;  // position in W of the result's last kept bit
+    uint64_t q;
+    bool rb = false, st = false;
     if (lo_bit <= 0) {
-        // exact: shift left
-        for (int i = bl - 1; i >= 0; --i) q = (q << 1) | ((m.w[i >> 5] >> (i & 31)) & 1);
-        q <<= (-lo_bit);
+        // every bit kept: W < 2^24 and -lo_bit < 24 (qe = k - 23, or the clamp with k < -127)
+        q = w0 << (-lo_bit);
     } else {
-        for (int i = bl - 1; i >= (int)lo_bit; --i) q = (q << 1) | ((m.w[i >> 5] >> (i & 31)) & 1);
-        int rbi = (int)lo_bit - 1;
-        rb = (m.w[rbi >> 5] >> (rbi & 31)) & 1;
-        for (int i = 0; i < rbi && !st; ++i) st |= (m.w[i >> 5] >> (i & 31)) & 1;
+        q = shr192(w2, w1, w0, (int)lo_bit);
+        rb = (shr192(w2, w1, w0, (int)lo_bit - 1) & 1) != 0;
+        st = low_bits192(w2, w1, w0, (int)lo_bit - 1);
     }
     if (rb && (st || (q & 1))) ++q;
     if (q == (1ull << 24)) {

@@ -961,6 +961,16 @@ __global__ void ea_kat_round(int64_t n, const double* x, const double* r, int32_
     bits[i] = bb;
 }
 
+__global__ void ea_kat_rn32_prod(int64_t n, const int32_t* am, const int64_t* x_hi, const uint64_t* x_lo,
+                                 const int32_t* E, uint32_t* bits, int32_t* status) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const i128 X = (i128)(((u128)(uint64_t)x_hi[i] << 64) | x_lo[i]);
+    uint32_t bb = 0;
+    status[i] = rn32_prod(am[i], X, E[i], &bb);
+    bits[i] = bb;
+}
+
 __global__ void ea_kat_round_ratio(int64_t n, const uint64_t* ah, const uint64_t* al, const uint64_t* bh,
                                    const uint64_t* bl, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
                                    int32_t* ov) {
@@ -1302,6 +1312,14 @@ int ea_hip_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, 
     if (n <= 0) return n < 0 ? -1 : 0;
     hipLaunchKernelGGL(ea_kat_round, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n, x, r,
                        fp32, bits, ok);
+    return herr(hipGetLastError());
+}
+
+int ea_hip_kat_rn32_prod(int64_t n, const int32_t* am, const int64_t* x_hi, const uint64_t* x_lo, const int32_t* E,
+                         uint32_t* bits, int32_t* status, ea_stream_t stream) {
+    if (n <= 0) return n < 0 ? -1 : 0;
+    hipLaunchKernelGGL(ea_kat_rn32_prod, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n, am,
+                       x_hi, x_lo, E, bits, status);
     return herr(hipGetLastError());
 }
 

@@ -357,6 +357,108 @@ __device__ __forceinline__ bool table_weight(uint32_t tbits, const double* T1s, 
 }
 
 // ------------------------------------------------------------------------------------------------
+// The exact decision for one pair the fast path left undecided (the prefill kernel's cold path):
+// t = RN32(alpha s) from the exact score, then w = RN24(2^t) from the fp64 tables or, when they
+// cannot decide, the 128-bit enclosure. mode 0: the score from the digit planes, q row qrow (LDS,
+// chunk c at c ^ qsw) and K row krow (the tile in global memory, chunk c at c ^ ksw), with
+// D_st = sum_i q_s,i k_t,i by v_dot4 (|D| <= 128 x 2^14), equal weights s + t summed in int32
+// (<= 4 x 2^21), S = sum_k acc_k 256^k in 128 bits and t = RN32(am S 2^eS); mode 1: from the bf16
+// rows qr, kr (elements rounded at slicing) by TwoSum with a certified logit, the rows read 32
+// elements at a time in 16-byte loads when both are 16-byte aligned (one memory round trip per
+// batch instead of one per element); mode 2: q holds NaN/inf (no score). Returns (status, M, E):
+// 0 w = M 2^E, 2 domain error, 3 score not certified, 4 weight not certified.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int3 pf_cold_pair(int mode, const uint8_t* qrow, int qsw, const uint8_t* krow, int ksw,
+                                          const uint16_t* qr, const uint16_t* kr, int32_t am, int eS, double alpha,
+                                          const double* T1s, const double* T2) {
+    uint32_t tbits = 0;
+    int ls = 3;
+    if (mode == 0) {
+        int D[4][4];
+#pragma unroll
+        for (int sq = 0; sq < 4; ++sq)
+#pragma unroll
+            for (int tk = 0; tk < 4; ++tk) D[sq][tk] = 0;
+        for (int c16 = 0; c16 < 8; ++c16) {
+            uint4 qc[4], kc[4];
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp) {
+                qc[sp] = *(const uint4*)(qrow + (((8 * sp + c16) ^ qsw) << 4));
+                kc[sp] = *(const uint4*)(krow + 8192 * sp + ((c16 ^ ksw) << 4));
+            }
+#pragma unroll
+            for (int sq = 0; sq < 4; ++sq)
+#pragma unroll
+                for (int tk = 0; tk < 4; ++tk) {
+                    int d = D[sq][tk];
+                    d = __builtin_amdgcn_sdot4((int)qc[sq].x, (int)kc[tk].x, d, false);
+                    d = __builtin_amdgcn_sdot4((int)qc[sq].y, (int)kc[tk].y, d, false);
+                    d = __builtin_amdgcn_sdot4((int)qc[sq].z, (int)kc[tk].z, d, false);
+                    D[sq][tk] = __builtin_amdgcn_sdot4((int)qc[sq].w, (int)kc[tk].w, d, false);
+                }
+        }
+        i128 S = 0;
+#pragma unroll
+        for (int k = 6; k >= 0; --k) {
+            int acc = 0;
+#pragma unroll
+            for (int sq = 0; sq < 4; ++sq)
+                if (k - sq >= 0 && k - sq < 4) acc += D[sq][k - sq];
+            S = S * 256 + (i128)acc;
+        }
+        ls = rn32_prod(am, S, eS, &tbits);
+    } else if (mode == 1) {
+        double ss = 0.0, es = 0.0, ea = 0.0;
+        auto acc2 = [&](uint32_t qw, uint32_t kw) __attribute__((always_inline)) {
+            double e0;
+            ss = two_sum(ss, (double)__uint_as_float(qw << 16) * (double)__uint_as_float(kw << 16), &e0);
+            es += e0;
+            ea += fabs(e0);
+            ss = two_sum(ss, (double)__uint_as_float(qw & 0xFFFF0000u) * (double)__uint_as_float(kw & 0xFFFF0000u), &e0);
+            es += e0;
+            ea += fabs(e0);
+        };
+        if ((((uintptr_t)qr | (uintptr_t)kr) & 15) == 0) {
+#pragma unroll 1
+            for (int c0 = 0; c0 < 128; c0 += 32) {
+                uint4 qv[4], kv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    qv[u] = *(const uint4*)(qr + c0 + 8 * u);
+                    kv[u] = *(const uint4*)(kr + c0 + 8 * u);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc2(qv[u].x, kv[u].x);
+                    acc2(qv[u].y, kv[u].y);
+                    acc2(qv[u].z, kv[u].z);
+                    acc2(qv[u].w, kv[u].w);
+                }
+            }
+        } else {
+#pragma unroll 1
+            for (int c = 0; c < 128; ++c) {
+                double e0;
+                ss = two_sum(ss, (double)__uint_as_float((uint32_t)qr[c] << 16) * (double)__uint_as_float((uint32_t)kr[c] << 16),
+                             &e0);
+                es += e0;
+                ea += fabs(e0);
+            }
+        }
+        ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1 : logit_cert(alpha, ss, es, ea * 0x1p-44, &tbits);
+        if (ls == 1) tbits = 0;
+    }
+    int32_t M = 0, E = 0;
+    if (ls == 2) return make_int3(2, M, E);
+    if (ls == 3) return make_int3(3, M, E);
+    if (table_weight(tbits, T1s, T2, &M, &E)) return make_int3(0, M, E);
+    int32_t M2 = 0;
+    int64_t E2 = 0;
+    if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) return make_int3(0, M2, (int32_t)E2);
+    return make_int3(4, M, E);
+}
+
+// ------------------------------------------------------------------------------------------------
 // Branch-free certified t = RN32(alpha s) and w = RN24(2^t) = M 2^E for 4 pairs in lock step
 // (independent chains the scheduler interleaves). xs: fp64 scores in units 2^lsbq; a = alpha 2^lsbq;
 // adel >= (1 + 2^-50) |a| |xs - exact| (the score bound with its rounding slack). p + pe = a xs
@@ -513,9 +615,12 @@ struct PfPar {
 
 template <int NWB, bool TIMERS>
 __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
-    // phase clocks (TIMERS build): shader cycles summed over waves into P.timers[0..7]:
-    // [0] wait for K + barrier, [1] score MFMAs + barrier, [2] P.V + certification,
-    // [3] cold path and bad keys, [4] pair exchange, [5] epoch folds, [6] weight digits, [7] rest
+    // phase clocks (TIMERS build): shader cycles summed over waves into P.timers[i]. Per tile:
+    // [14] DMA wait before the tile barrier, [0] tile barrier, [1] score MFMAs, [2] EV reads, K
+    // issue, rebase and weight digits, V issue, score fold, [3] second barrier and digit reads,
+    // [4] pair metadata, P.V and certification, [5] cold path, [6] pair exchange, [7] the rest.
+    // Per block: [15] prologue, [9] drain, [10] row totals, [11] earlier epochs and reciprocals,
+    // [12] quotients into LDS, [13] certified rounding. [8] counts tiles (lane 0 of each wave).
     uint64_t tclk[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     uint64_t tprev = TIMERS ? __builtin_amdgcn_s_memtime() : 0;
     auto tick = [&](int ph) __attribute__((always_inline)) {
@@ -616,6 +721,9 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     int dom = (rvalid && qbad) ? 1 : 0;  // NaN/inf in q: a domain error (docs/SPEC.md)
     int unc = 0;
     int nslow = 0, nunc_s = 0, nunc_w = 0;
+    // wave-uniform event counts, added to the stats once at the end: an atomic inside the tile loop
+    // would make the next wait for vector memory (vmcnt) also wait for its round trip
+    int nfold = 0, ncold = 0;
     __syncthreads();  // s_kend final, tables and q digits visible
     const int kend = s_kend;
     const int ntiles = (kend + 63) >> 6;
@@ -689,7 +797,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     };
     // ---- fold the epoch into the per-lane fp64 sums in scr, rescaled to the new bases nb
     auto fold = [&](int nf_pair, int nb) __attribute__((always_inline)) {
-        if (P.stats && lane == 0) atomicAdd((unsigned long long*)&P.stats[11], 1ull);
+        ++nfold;
         int nf = nf_pair + __shfl_xor(nf_pair, 16, 64);
         nf += __shfl_xor(nf, 32, 64);
         double fr[4];
@@ -957,7 +1065,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         // integer score comes from the tile's digit planes (no bf16 reads); only pairs whose
         // digits are inexact (elements rounded at slicing) read the bf16 inputs.
         if (__builtin_expect(__ballot(slowmask != 0) != 0, 0)) {
-            if (P.stats && lane == 0) atomicAdd((unsigned long long*)&P.stats[12], 1ull);
+            ++ncold;
             const int8_t* Kg = (const int8_t*)(P.pfkv + ((int64_t)seg * P.pf_ntiles + it) * EA_PF_TILE_BYTES);
             for (int p = 0; p < 4 * NKT; ++p) {
                 if (!((slowmask >> p) & 1)) continue;
@@ -965,84 +1073,29 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 const int key = 16 * (NKT * hh + kk) + 4 * g + i;
                 const int n = it * 64 + key;
                 const int kf = TMc->kfl[key];
-                uint32_t tbits = 0;
-                int ls = 3;
                 ++nslow;
-                if (!qbad && !((qm.flags >> 8) & 0xFF) && !(kf >> 8)) {
-                    // exact score from the digit planes: D_st = sum_i q_s,i k_t,i by v_dot4 (|D| <=
-                    // 128 x 2^14), equal weights s + t summed in int32 (<= 4 x 2^21), then
-                    // S = sum_k acc_k 256^k in 128 bits
-                    const uint8_t* krow = (const uint8_t*)Kg + key * 128;
-                    int D[4][4];
-#pragma unroll
-                    for (int sq = 0; sq < 4; ++sq)
-#pragma unroll
-                        for (int tk = 0; tk < 4; ++tk) D[sq][tk] = 0;
-                    for (int c16 = 0; c16 < 8; ++c16) {
-                        uint4 qc[4], kc[4];
-#pragma unroll
-                        for (int sp = 0; sp < 4; ++sp) {
-                            qc[sp] = *(const uint4*)(qlds + (((8 * sp + c16) ^ (j & 7)) << 4));
-                            kc[sp] = *(const uint4*)(krow + 8192 * sp + ((c16 ^ (key & 7)) << 4));
-                        }
-#pragma unroll
-                        for (int sq = 0; sq < 4; ++sq)
-#pragma unroll
-                            for (int tk = 0; tk < 4; ++tk) {
-                                int d = D[sq][tk];
-                                d = __builtin_amdgcn_sdot4((int)qc[sq].x, (int)kc[tk].x, d, false);
-                                d = __builtin_amdgcn_sdot4((int)qc[sq].y, (int)kc[tk].y, d, false);
-                                d = __builtin_amdgcn_sdot4((int)qc[sq].z, (int)kc[tk].z, d, false);
-                                D[sq][tk] = __builtin_amdgcn_sdot4((int)qc[sq].w, (int)kc[tk].w, d, false);
-                            }
-                    }
-                    i128 S = 0;
-#pragma unroll
-                    for (int k = 6; k >= 0; --k) {
-                        int acc = 0;
-#pragma unroll
-                        for (int sq = 0; sq < 4; ++sq)
-                            if (k - sq >= 0 && k - sq < 4) acc += D[sq][k - sq];
-                        S = S * 256 + (i128)acc;
-                    }
-                    ls = rn32_prod(P.am, S, P.ae + qm.lsb + TMc->lsbk[key], &tbits);
-                } else if (!qbad) {
-                    const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)tq * P.g.q_tok_stride +
-                                         (int64_t)(hk * P.grp + lrc % P.grp) * P.g.q_head_stride;
-                    const uint16_t* kr = P.k + kv_off(P, b, n, hk, 0);
-                    double ss = 0.0, es = 0.0, ea = 0.0;
-                    for (int c = 0; c < 128; ++c) {
-                        double e0;
-                        ss = two_sum(ss, (double)__uint_as_float((uint32_t)qr[c] << 16) *
-                                             (double)__uint_as_float((uint32_t)kr[c] << 16), &e0);
-                        es += e0;
-                        ea += fabs(e0);
-                    }
-                    ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1
-                                                                : logit_cert(P.alpha, ss, es, ea * 0x1p-44, &tbits);
-                    if (ls == 1) tbits = 0;
+                // the pair's exact decision, out of line: from the tile's digit planes when every
+                // element was sliced exactly, else from the bf16 inputs
+                const int mode = qbad ? 2 : ((!((qm.flags >> 8) & 0xFF) && !(kf >> 8)) ? 0 : 1);
+                const uint16_t* qr = nullptr;
+                const uint16_t* kr = nullptr;
+                if (mode == 1) {
+                    qr = P.q + b * P.g.q_seq_stride + (int64_t)tq * P.g.q_tok_stride +
+                         (int64_t)(hk * P.grp + lrc % P.grp) * P.g.q_head_stride;
+                    kr = P.k + kv_off(P, b, n, hk, 0);
                 }
-                int32_t M = 0, E = 0;
-                bool live = false;
-                if (ls == 2) {
-                    dom = 1;
-                } else if (ls == 3) {
+                const int3 cw = pf_cold_pair(mode, qlds, j & 7, (const uint8_t*)Kg + key * 128, key & 7, qr, kr, P.am,
+                                             P.ae + qm.lsb + TMc->lsbk[key], P.alpha, T1s, T2);
+                const bool live = cw.x == 0;
+                const int32_t M = cw.y, E = cw.z;
+                if (cw.x == 2) dom = 1;
+                if (cw.x == 3) {
                     unc = 1;
                     ++nunc_s;
-                } else if (table_weight(tbits, T1s, T2, &M, &E)) {
-                    live = true;
-                } else {
-                    // the 128-bit enclosure of 2^t decides RN24 (ea_device.h weight_wide)
-                    int32_t M2 = 0;
-                    int64_t E2 = 0;
-                    if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
-                        M = M2;
-                        E = (int32_t)E2;
-                        live = true;
-                    } else {
-                        unc = 1;
-                        ++nunc_w;
-                    }
+                }
+                if (cw.x == 4) {
+                    unc = 1;
+                    ++nunc_w;
                 }
 #pragma unroll
                 for (int q = 0; q < NKT; ++q)
@@ -1075,6 +1128,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
 
     wait_vm<0>();  // the prologue's global loads: from here on vmcnt counts DMAs (and folds)
     if (ntiles > 0) issue_k(0, aM0);
+    tick(15);
     for (int it = 0; it < ntiles; it += 2) {
         step(PfPar<0>{}, it);
         if (it + 1 < ntiles) step(PfPar<1>{}, it + 1);
@@ -1192,7 +1246,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
 #pragma unroll
-        for (int i = 9; i < 15; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
+        for (int i = 9; i < 16; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
         atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)ntiles);
     }
     if (P.stats) {
@@ -1201,6 +1255,8 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             if (st5) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)st5);
             if (st6) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)st6);
             if (st8) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)st8);
+            if (nfold) atomicAdd((unsigned long long*)&P.stats[11], (unsigned long long)nfold);
+            if (ncold) atomicAdd((unsigned long long*)&P.stats[12], (unsigned long long)ncold);
         }
     }
     if (ntiles == 0) {

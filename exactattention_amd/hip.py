@@ -76,6 +76,8 @@ def load():
         lib.ea_hip_kat_round.restype = ctypes.c_int
         lib.ea_hip_kat_round_ratio.argtypes = [ctypes.c_int64] + [P] * 6 + [ctypes.c_int32, P, P, P]
         lib.ea_hip_kat_round_ratio.restype = ctypes.c_int
+        lib.ea_hip_kat_rn32_prod.argtypes = [ctypes.c_int64] + [P] * 6 + [P]
+        lib.ea_hip_kat_rn32_prod.restype = ctypes.c_int
         lib.ea_hip_kat_wave_max.argtypes = [ctypes.c_int64, P, P, P]
         lib.ea_hip_kat_wave_max.restype = ctypes.c_int
         lib.ea_hip_version.restype = ctypes.c_char_p

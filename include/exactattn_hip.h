@@ -139,6 +139,13 @@ int ea_hip_kat_wave_max(int64_t nwaves, const int32_t* in, int32_t* out, ea_stre
 int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo, const uint64_t* b_hi,
                            const uint64_t* b_lo, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
                            int32_t* overflow, ea_stream_t stream);
+/* ea_hip_kat_rn32_prod: the exact logit RN32(am * X * 2^E), X a signed 128-bit integer given as
+ * (x_hi signed, x_lo) words, |am| < 2^24 -> fp32 bits, status (0 ok, 2 overflow). The prefill
+ * kernel's cold path and tier 2 round exact scores with it.
+ * Reference counterpart: certified_logit's exact rounding (csrc/exact_attention_cpu.cpp:215) and
+ * RN_fp32(alpha * s) (src/exactattn/reference.py:74-79). */
+int ea_hip_kat_rn32_prod(int64_t n, const int32_t* am, const int64_t* x_hi, const uint64_t* x_lo, const int32_t* E,
+                         uint32_t* bits, int32_t* status, ea_stream_t stream);
 
 /* Library version string. */
 const char* ea_hip_version(void);

@@ -168,6 +168,104 @@ def test_certify_round_kat(gpu):
         assert n_ok > 0.9 * x.size
 
 
+def test_rn32_prod_kat(gpu):
+    """The exact logit RN32(am * X * 2^E) (the prefill cold path and tier 2) against the oracle's
+    round_dyadic: 128-bit X of every length, both signs, exponents from far below the fp32
+    subnormal range to overflow, and products on exact rounding ties."""
+    import torch
+    from exactattention_amd import hip
+    from oracle import exact
+    rng = np.random.default_rng(17)
+    n = 8000
+    am = [int(v) for v in rng.integers(1, 1 << 24, n) * rng.choice([-1, 1], n)]
+    X, E = [], []
+    for i in range(n):
+        bl = int(rng.integers(1, 128))
+        x = int(rng.integers(0, 1 << 62)) << 66 | int(rng.integers(0, 1 << 62)) << 4 | int(rng.integers(0, 16))
+        x = (x >> (128 - bl)) | (1 << (bl - 1))
+        if i % 5 == 0:
+            # odd 13-bit factors: a 25-bit odd product is a tie at 24 bits (about half of them)
+            am[i] = (int(rng.integers(1 << 11, 1 << 12)) * 2 + 1) * (1 if i % 10 else -1)
+            x = (int(rng.integers(1 << 11, 1 << 12)) * 2 + 1) << int(rng.integers(0, 100))
+            X.append(x)
+            E.append(int(rng.integers(-150, 120)) - (abs(am[i]) * x).bit_length() + 1)
+            continue
+        X.append(x if rng.random() < 0.5 else -x)
+        lead = bl + abs(am[i]).bit_length() - 2
+        E.append(int(rng.integers(-200, 140)) - lead)  # floor(log2) from -200 to 139
+    xh = np.array([(x >> 64) for x in X], dtype=np.int64)
+    xl = np.array([x & ((1 << 64) - 1) for x in X], dtype=np.uint64)
+    dev = {k: torch.from_numpy(v).cuda() for k, v in
+           (("am", np.array(am, dtype=np.int32)), ("xh", xh), ("xl", xl.view(np.int64)), ("E", np.array(E, dtype=np.int32)))}
+    bits = torch.zeros(n, dtype=torch.int32, device="cuda")
+    st = torch.zeros(n, dtype=torch.int32, device="cuda")
+    assert hip.load().ea_hip_kat_rn32_prod(n, dev["am"].data_ptr(), dev["xh"].data_ptr(), dev["xl"].data_ptr(),
+                                           dev["E"].data_ptr(), bits.data_ptr(), st.data_ptr(),
+                                           torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    gb, gs = bits.cpu().numpy().view(np.uint32), st.cpu().numpy()
+    kinds = {"normal": 0, "subnormal": 0, "zero": 0, "overflow": 0}
+    for i in range(n):
+        try:
+            m, e = exact.round_dyadic(am[i] * X[i], E[i], exact.FP32)
+        except exact.DomainError:
+            assert gs[i] == 2, (am[i], X[i], E[i])
+            kinds["overflow"] += 1
+            continue
+        assert gs[i] == 0, (am[i], X[i], E[i])
+        want = 0 if m == 0 else exact.encode_fp32(m, e)
+        got = int(gb[i]) & (0x7FFFFFFF if m == 0 else 0xFFFFFFFF)  # the sign of a zero is not part of it
+        assert got == want, (am[i], X[i], E[i], hex(got), hex(want))
+        kinds["zero" if m == 0 else ("subnormal" if (want & 0x7F800000) == 0 else "normal")] += 1
+    assert min(kinds.values()) > 20, kinds
+
+
+def test_certify_round_intervals(gpu):
+    """certify_round on intervals [x - r, x + r] with r > 0, through both its normal-range fast
+    path and the general path (subnormal and zero-region magnitudes, ends near 2^127, intervals
+    on a rounding midpoint): whenever it certifies, both ends round (exactly, as rationals) to the
+    bits it returned, so every point of the interval does."""
+    import torch
+    from fractions import Fraction
+    from exactattention_amd import hip
+    from oracle import exact
+    rng = np.random.default_rng(11)
+    n = 6000
+    for fp32 in (0, 1):
+        p = 24 if fp32 else 8
+        fmt = exact.FP32 if fp32 else exact.BF16
+        enc = exact.encode_fp32 if fp32 else exact.encode_bf16
+        x = rng.standard_normal(n) * np.exp2(rng.uniform(-150, 128, n))
+        r = np.abs(x) * np.exp2(rng.uniform(-60, -p + 1, n))
+        r[::7] = 0.0
+        # points just off a midpoint between two format values
+        mids = np.float32(rng.standard_normal(n // 6) * np.exp2(rng.uniform(-130, 120, n // 6))).astype(np.float64)
+        ulp = np.exp2(np.floor(np.log2(np.abs(mids))) - (p - 1))
+        mids = mids + 0.5 * ulp * np.sign(mids) + rng.uniform(-4, 4, mids.size) * np.abs(mids) * 2.0 ** -52
+        x[: mids.size] = mids
+        r[: mids.size] = np.abs(mids) * 2.0 ** -55
+        xs, rs = torch.from_numpy(x).cuda(), torch.from_numpy(r).cuda()
+        bits = torch.zeros(n, dtype=torch.int32, device="cuda")
+        ok = torch.zeros(n, dtype=torch.int32, device="cuda")
+        assert hip.load().ea_hip_kat_round(n, xs.data_ptr(), rs.data_ptr(), fp32, bits.data_ptr(), ok.data_ptr(),
+                                           torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        gb, gk = bits.cpu().numpy().view(np.uint32), ok.cpu().numpy()
+
+        def rn(v):
+            m, e = exact.round_rational(v.numerator, v.denominator, fmt)
+            return 0 if m == 0 else enc(m, e)
+
+        n_ok = 0
+        for i in range(n):
+            if not gk[i]:
+                continue
+            n_ok += 1
+            lo, hi = Fraction(float(x[i])) - Fraction(float(r[i])), Fraction(float(x[i])) + Fraction(float(r[i]))
+            assert rn(lo) == rn(hi) == int(gb[i]), (float(x[i]), float(r[i]), fp32)
+        assert n_ok > 0.5 * n, n_ok
+
+
 # ---------------------------------------------------------------------------------------------
 # rows against the oracle
 # ---------------------------------------------------------------------------------------------
