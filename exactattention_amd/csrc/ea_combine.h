@@ -1,11 +1,14 @@
-// Merge of the KV-split partials of one row and the certified final rounding, shared by the
-// combine kernel (ea_hip.hip) and the decode kernel's last-arriving block (ea_decode.hip).
+// Merge of the KV-split partials of one row and the certified final rounding (one wave per row;
+// the combine kernel in ea_hip.hip).
 #pragma once
 #include "ea_params.h"
 
 namespace ea {
 
-__device__ inline void combine_row(const Params& P, int64_t row, int lane) {
+// Returns the row's stats events, the same in every lane: bit 0 the row was merged (stats[0]),
+// bit 1 it is flagged (stats[1]), bit 2 only its final rounding failed (stats[7]). The caller
+// adds them up per block.
+__device__ inline int combine_row(const Params& P, int64_t row, int lane) {
     const int dv = P.g.head_dim_v;
     const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
     const int64_t b = row / ((int64_t)T * Hq);
@@ -52,7 +55,7 @@ __device__ inline void combine_row(const Params& P, int64_t row, int lane) {
                 else o16[obase + c] = 0;
             }
             if (lane == 0) P.flags[row] = 0;
-            return;
+            return 0;
         }
         const double up = 0x1p-53 * (1.0 + 0x1p-28);
         const int dsh_i = (n_i > 0 && R != INT_MIN) ? r_i - R : 0;
@@ -108,17 +111,12 @@ __device__ inline void combine_row(const Params& P, int64_t row, int lane) {
         const int bad = wave_max_i(ok ? 0 : 1);
         if (lane == 0) {
             P.flags[row] = bad ? 1 : 0;
-            if (P.stats && bad && !flag) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
             if (bad) {
                 const int slot = atomicAdd(P.wl_cnt, 1);
                 P.wl[slot] = (int32_t)row;
             }
-            if (P.stats) {
-                atomicAdd((unsigned long long*)&P.stats[0], 1ull);
-                if (bad) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
-            }
         }
-        return;
+        return 1 | (bad ? 2 : 0) | ((bad && !flag) ? 4 : 0);
     }
     // the caller's merge order is used only if it is a permutation of [0, ns); any order gives
     // the same certified bits, so an invalid one falls back to 0..ns-1
@@ -168,7 +166,7 @@ __device__ inline void combine_row(const Params& P, int64_t row, int lane) {
             else o16[obase + c] = 0;
         }
         if (lane == 0) P.flags[row] = 0;
-        return;
+        return 0;
     }
     double tiny = (double)(nterm + 64 * ns + 64) * 0x1p-1074;
     double eZ = A * up + tiny;
@@ -202,16 +200,12 @@ __device__ inline void combine_row(const Params& P, int64_t row, int lane) {
     int bad = wave_max_i(ok ? 0 : 1);
     if (lane == 0) {
         P.flags[row] = bad ? 1 : 0;
-        if (P.stats && bad && !flag) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
         if (bad) {
             int slot = atomicAdd(P.wl_cnt, 1);
             P.wl[slot] = (int32_t)row;
         }
-        if (P.stats) {
-            atomicAdd((unsigned long long*)&P.stats[0], 1ull);
-            if (bad) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
-        }
     }
+    return 1 | (bad ? 2 : 0) | ((bad && !flag) ? 4 : 0);
 }
 
 }  // namespace ea

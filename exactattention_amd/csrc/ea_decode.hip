@@ -371,7 +371,8 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
             ns[r] = wave_sum_i(nvis[r]);
         }
         if (lane == 0) {
-            if (P.stats && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)nrow);
+            // the decode kernel takes every row of the problem: one add for the whole grid
+            if (P.stats && item == 0 && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
                 if (r < nrow) {

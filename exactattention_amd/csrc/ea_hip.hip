@@ -529,9 +529,25 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
 //   eZ = u' A + tiny,  eN_c = u' A max_s Vmax_sc + tiny.
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) ea_combine(Params P) {
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= P.rows) return;
-    combine_row(P, row, threadIdx.x & 63);
+    __shared__ int s_ev[4];
+    const int w = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * 4 + w;
+    const int ev = row < P.rows ? combine_row(P, row, threadIdx.x & 63) : 0;
+    if ((threadIdx.x & 63) == 0) s_ev[w] = ev;
+    __syncthreads();
+    // one atomic per counter and block: same-address atomics per row would serialise
+    if (threadIdx.x == 0 && P.stats) {
+        int n0 = 0, n1 = 0, n7 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            n0 += s_ev[i] & 1;
+            n1 += (s_ev[i] >> 1) & 1;
+            n7 += (s_ev[i] >> 2) & 1;
+        }
+        if (n0) atomicAdd((unsigned long long*)&P.stats[0], (unsigned long long)n0);
+        if (n1) atomicAdd((unsigned long long*)&P.stats[1], (unsigned long long)n1);
+        if (n7) atomicAdd((unsigned long long*)&P.stats[7], (unsigned long long)n7);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------

@@ -1279,6 +1279,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         for (int o = 1; o < SPLIT; ++o) fb |= (uint32_t)sX[(rg * SPLIT + (hh + o) % SPLIT) * 64 + lane].a;
         failbits = fb;
     }
+    int c_rows = 0, c_flag = 0, c_dom = 0, c_fin = 0;  // this lane's rows, added per wave below
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int di = __shfl(dom, 4 * g + i, 64), ui = __shfl(unc, 4 * g + i, 64), nvr = __shfl(nv, 4 * g + i, 64);
@@ -1304,13 +1305,26 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 const int slot = atomicAdd(P.wl_cnt, 1);
                 P.wl[slot] = (int32_t)gr;
             }
-            if (P.stats) {
-                atomicAdd((unsigned long long*)&P.stats[0], 1ull);
-                atomicAdd((unsigned long long*)&P.stats[10], 1ull);
-                if (flag) atomicAdd((unsigned long long*)&P.stats[1], 1ull);
-                if (flag == 2) atomicAdd((unsigned long long*)&P.stats[4], 1ull);
-                if (fin) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
+            ++c_rows;
+            c_flag += flag ? 1 : 0;
+            c_dom += flag == 2 ? 1 : 0;
+            c_fin += fin ? 1 : 0;
+        }
+    }
+    // one atomic per counter and wave (same-address atomics per row would serialise)
+    if (P.stats && hh == 0) {
+        c_rows = wave_sum_i(c_rows);
+        c_flag = wave_sum_i(c_flag);
+        c_dom = wave_sum_i(c_dom);
+        c_fin = wave_sum_i(c_fin);
+        if (lane == 0) {
+            if (c_rows) {
+                atomicAdd((unsigned long long*)&P.stats[0], (unsigned long long)c_rows);
+                atomicAdd((unsigned long long*)&P.stats[10], (unsigned long long)c_rows);
             }
+            if (c_flag) atomicAdd((unsigned long long*)&P.stats[1], (unsigned long long)c_flag);
+            if (c_dom) atomicAdd((unsigned long long*)&P.stats[4], (unsigned long long)c_dom);
+            if (c_fin) atomicAdd((unsigned long long*)&P.stats[7], (unsigned long long)c_fin);
         }
     }
 }
