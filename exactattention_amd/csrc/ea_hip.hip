@@ -1150,7 +1150,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     hipStream_t st = (hipStream_t)stream;
     unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
     auto mark = [&](int i) -> int {
-        return o->events ? herr(hipEventRecord((hipEvent_t)o->events[i], st)) : 0;
+        return (o->events && o->events[i]) ? herr(hipEventRecord((hipEvent_t)o->events[i], st)) : 0;
     };
     if ((rc = mark(0))) return rc;
     if (pl.prefill) {

@@ -87,7 +87,8 @@ typedef struct ea_options {
                                tile (waves), [12] prefill waves that ran the exact
                                per-pair path, [13..15] reserved */
     void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep, split,
-                               combine and tier 2, and after tier 2 (per-kernel timing) */
+                               combine and tier 2, and after tier 2 (per-kernel timing); a null
+                               entry is skipped (each record is one more packet in the stream) */
     int64_t* timers;        /* optional device int64[16]: when set, the split kernel runs its
                                phase-clock build and adds shader-clock cycles (s_memtime) summed
                                over waves: [0] prologue, [1] wait for the tile barrier, [2] scores,
