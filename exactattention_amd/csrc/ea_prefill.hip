@@ -1198,10 +1198,27 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             rze[i] = zok ? 1.0 / (Zr[i] - eZr[i]) : 0.0;
             live[i] = !skip[i] && zok;
         }
-        // (q, delta) per entry through LDS (the K and V buffers are idle: no DMA is in flight),
-        // then one rolled loop certifies them: the rounding code runs once per wave and stays
-        // small in the instruction cache
+        // output offsets of this lane's 4 rows (channel j of its first channel tile)
+        int64_t orow[4];
+        bool ovalid[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int lri = rbk * RPB + rg * 16 + 4 * g + i;
+            ovalid[i] = lri < P.r_seg;
+            const int lrv = ovalid[i] ? lri : 0;
+            const int hq = hk * P.grp + lrv % P.grp;
+            orow[i] = b * P.g.o_seq_stride + (int64_t)(lrv / P.grp) * P.g.o_tok_stride +
+                      (int64_t)hq * P.g.o_head_stride + 16 * NCT * hh + j;
+        }
+        auto store_out = [&](int i, int cc, uint32_t bits) __attribute__((always_inline)) {
+            if (P.out_fp32) ((uint32_t*)P.out)[orow[i] + 16 * cc] = bits;
+            else ((uint16_t*)P.out)[orow[i] + 16 * cc] = (uint16_t)bits;
+        };
+        // every entry first tries the normal-range rounding (a few integer operations, no
+        // branches); the entries it cannot decide go through LDS (the K and V buffers are idle:
+        // no DMA is in flight) to one rolled loop of the general test
         double2* const qd = (double2*)smem + tid;  // entry e at qd[64 NWB e]
+        uint32_t slow = 0;
         tick(11);
         const double omit = (double)ep_tiles * 0x1p20;
 #pragma unroll
@@ -1216,28 +1233,28 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 double delta = (en * (1.0 + 0x1p-40) + fabs(q) * eZr[i]) * rze[i] * (1.0 + 0x1p-40) +
                                fabs(q) * 0x1p-51 + 0x1p-1070;
                 if (!isfinite(q) || !isfinite(delta) || !live[i]) delta = __builtin_inf();
-                if (skip[i]) delta = -1.0;  // no output from this entry
-                qd[64 * NWB * (4 * cc + i)] = make_double2(q, delta);
+                uint32_t bits = 0;
+                const bool ok = !skip[i] && certify_round_normal(q, delta, P.out_fp32, &bits);
+                if (ok && ovalid[i]) store_out(i, cc, bits);
+                if (!skip[i] && !ok) {
+                    slow |= 1u << (4 * cc + i);
+                    qd[64 * NWB * (4 * cc + i)] = make_double2(q, delta);
+                }
             }
         }
         tick(12);
+        if (slow) {
 #pragma unroll 1
-        for (int e = 0; e < 4 * NCT; ++e) {
-            const int cc = e >> 2, i = e & 3;
-            const double2 v = qd[64 * NWB * e];
-            if (!(v.y >= 0.0)) continue;
-            uint32_t bits = 0;
-            if (!certify_round(v.x, v.y, P.out_fp32, &bits)) {
-                failbits |= 1u << (8 * i + cc);
-                continue;
-            }
-            const int lri = rbk * RPB + rg * 16 + 4 * g + i;
-            if (lri < P.r_seg) {
-                const int hq = hk * P.grp + lri % P.grp;
-                const int64_t o = b * P.g.o_seq_stride + (int64_t)(lri / P.grp) * P.g.o_tok_stride +
-                                  (int64_t)hq * P.g.o_head_stride + 16 * (NCT * hh + cc) + j;
-                if (P.out_fp32) ((uint32_t*)P.out)[o] = bits;
-                else ((uint16_t*)P.out)[o] = (uint16_t)bits;
+            for (int e = 0; e < 4 * NCT; ++e) {
+                if (!((slow >> e) & 1)) continue;
+                const int cc = e >> 2, i = e & 3;
+                const double2 v = qd[64 * NWB * e];
+                uint32_t bits = 0;
+                if (!certify_round_general(v.x, v.y, P.out_fp32, &bits)) {
+                    failbits |= 1u << (8 * i + cc);
+                    continue;
+                }
+                if (ovalid[i]) store_out(i, cc, bits);
             }
         }
     }
