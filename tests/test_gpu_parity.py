@@ -500,6 +500,62 @@ def test_prefill_paged_gqa_ragged(gpu, force_prefill):
     assert np.array_equal(got, want)
 
 
+def test_prefill_tree_masks_equal_decode(gpu, monkeypatch):
+    """Speculative-tree rows (prefix + 64-bit draft mask) through the prefill kernel give the same
+    bits as the decode path on the same problem."""
+    rng = np.random.default_rng(22)
+    B, P, N, Hq, Hkv, d = 2, 150, 12, 4, 2, 128
+    parents = [configs.draft_tree(rng, N) for _ in range(B)]
+    q = bf16(rng, (B, N, Hq, d))
+    k = bf16(rng, (B, Hkv, P + N, d))
+    v = bf16(rng, (B, Hkv, P + N, d))
+    mask = np.array([[sum(1 << a for a in configs.path_of(parents[b], i)) for i in range(N)] for b in range(B)],
+                    dtype=np.uint64)
+    tree = problem.contiguous(q, k, v, np.full((B, N), P), tree_mask=mask, tree_base=np.full(B, P))
+    ab = default_alpha_bits(d)
+    want, fl_d, st_d = _run(tree, ab, splits=2)
+    assert st_d["prefill_kernel_rows"] == 0 and not np.any(fl_d), st_d
+    monkeypatch.setenv("EA_PREFILL", "1")
+    got, flags, st = _run(tree, ab)
+    assert st["prefill_kernel_rows"] == _rows(tree), st
+    assert not np.any(flags), st
+    assert np.array_equal(got, want)
+
+
+def test_prefill_four_wave_block_matches_oracle(gpu, force_prefill, monkeypatch):
+    """The 4-wave prefill block (EA_PF_SHAPE=4) gives the oracle's bits, like the default 8-wave
+    block."""
+    rng = np.random.default_rng(23)
+    prob = _rand_problem(rng, "normal", "normal", B=2, T=70, Hq=4, Hkv=2, S=300, d=128, dv=128)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    got8, fl8, st8 = _run(prob, ab)
+    monkeypatch.setenv("EA_PF_SHAPE", "4")
+    got4, fl4, st4 = _run(prob, ab)
+    for got, fl, st in ((got8, fl8, st8), (got4, fl4, st4)):
+        assert st["prefill_kernel_rows"] == _rows(prob), st
+        assert not np.any(fl == 1), st
+        assert np.array_equal(got, want), st
+
+
+def test_prefill_rows_longer_than_256_tiles(gpu):
+    """Rows that see 16,837 to 16,900 keys (more than 256 tiles of 64): the per-lane epoch sums
+    fold at least once on age alone, and the rows still equal the oracle."""
+    rng = np.random.default_rng(77)
+    B, T, Hq, Hkv, d, S = 1, 64, 2, 1, 128, 16900
+    q = bf16(rng, (B, T, Hq, d))
+    k = bf16(rng, (B, Hkv, S, d))
+    v = bf16(rng, (B, Hkv, S, d))
+    prob = problem.contiguous(q, k, v, (S - T + 1 + np.arange(T)).reshape(1, T))
+    ab = default_alpha_bits(d)
+    want, _ = _oracle(prob, ab)
+    got, flags, st = _run(prob, ab)
+    assert st["prefill_kernel_rows"] == _rows(prob), st
+    assert st["prefill_epoch_folds"] > 0, st
+    assert not np.any(flags), st
+    assert np.array_equal(got, want)
+
+
 def test_prefill_nonfinite_flags_exactly_the_rows_that_see_them(gpu, force_prefill):
     rng = np.random.default_rng(45)
     T = 80
