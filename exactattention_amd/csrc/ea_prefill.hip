@@ -49,12 +49,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr double PF_U = 0x1p-53 * (1.0 + 0x1p-28);
-#ifndef PF_EARLY_K
-#define PF_EARLY_K 1
-#endif
-#ifndef PF_VALU_PER_MFMA
-#define PF_VALU_PER_MFMA 5
-#endif
 // 1.5 * 2^52 + 0x8080808080: y = Wf + this has the biased digits of Wf in its low 40 bits
 constexpr double PF_C40 = 6755399441055744.0 + (double)0x8080808080ull;
 
@@ -556,23 +550,24 @@ __device__ __forceinline__ void score_fold(const v4i (&acc)[7], const v4i& lk, d
 }
 
 // ------------------------------------------------------------------------------------------------
-// Main kernel. Block = 4 waves over 32 consecutive rows (tokens x query heads of one KV head).
-// Waves 2 rg and 2 rg + 1 share the 16 rows of row group rg; wave half hh = w & 1 takes the
-// scores and weights of key groups kt = 2 hh, 2 hh + 1 of each tile and the P.V sums of channel
-// tiles ct = 4 hh .. 4 hh + 3. Lane (g = lane / 16, j = lane % 16):
+// Main kernel. Block = NWB waves over 32 consecutive rows (tokens x query heads of one KV head):
+// two row groups rg of 16 rows, SPLIT = NWB / 2 waves each. Wave hh of a row group takes the
+// scores and weights of key groups kt = NKT hh .. NKT hh + NKT - 1 of each 64-key tile and the
+// P.V sums of channel tiles ct = NCT hh .. NCT hh + NCT - 1 (NWB = 8: one key group and two
+// channel tiles per wave; NWB = 4: two and four). Lane (g = lane / 16, j = lane % 16):
 //   score layout  row j, keys 16 kt + 4 g + i (i = 0..3)
 //   P.V layout    rows 4 g + i, channels 16 ct + j
-// Software pipeline, one step per tile it:
-//   B1    K(it) and its metadata landed; the pair's weight digits of tile it-1 are in sWD
-//         score MFMAs of tile it (K planes and q digits from LDS)
-//   B1.5  every wave has read the K planes: K(it+1) and its metadata start loading
-//         P.V MFMAs of tile it-1 interleaved with the certification of tile it
-//   B2    pair exchange of row maxima; V(it+1) starts loading into the buffer V(it-1) used;
-//         epoch fold when a base moves; weight digits of tile it to sWD
+// Software pipeline, one step per tile it, two barriers:
+//   B1    K(it), its metadata and V(it-1) landed; the row maxima of tile it-1 are in sX
+//         score MFMAs of tile it (K planes and q digits from LDS); while they run, the base move
+//         (epoch fold when a base moves) and the weight digits of tile it-1 to sWD
+//   B2    every wave has read the K planes of tile it and written its digits: K(it+1) with its
+//         metadata and V(it) start loading; fp64 scores; P.V MFMAs of tile it-1 (digits from
+//         sWD), certification of tile it, cold path; row maxima of tile it to sX
 // V and the metadata are double-buffered (the two parities are two copies of the step). The DMAs
 // are issued as inline asm, so the compiler adds no waits of its own; barriers are s_barrier after
-// lgkmcnt(0) (no vmcnt(0): DMAs stay in flight across them) and the DMA waits explicit vmcnt
-// counts, in issue order: K(it+1) and its metadata at B1.5, V(it+1) at B2.
+// lgkmcnt(0) (no vmcnt(0): DMAs stay in flight across them) and the only DMA wait is the vmcnt(0)
+// before B1.
 // ------------------------------------------------------------------------------------------------
 struct PfX {
     int32_t a, b;
@@ -616,11 +611,11 @@ struct PfPar {
 template <int NWB, bool TIMERS>
 __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     // phase clocks (TIMERS build): shader cycles summed over waves into P.timers[i]. Per tile:
-    // [14] DMA wait before the tile barrier, [0] tile barrier, [1] score MFMAs, [2] EV reads, K
-    // issue, rebase and weight digits, V issue, score fold, [3] second barrier and digit reads,
-    // [4] pair metadata, P.V and certification, [5] cold path, [6] pair exchange, [7] the rest.
-    // Per block: [15] prologue, [9] drain, [10] row totals, [11] earlier epochs and reciprocals,
-    // [12] quotients into LDS, [13] certified rounding. [8] counts tiles (lane 0 of each wave).
+    // [14] DMA wait before B1, [0] B1, [1] EV reads and score MFMAs, [2] base move and weight
+    // digits, [3] B2, DMA issue, fp64 scores and digit reads, [4] pair metadata, P.V and
+    // certification, [5] cold path, [6] pair exchange, [7] the rest. Per block: [15] prologue,
+    // [9] drain, [10] row totals, [11] earlier epochs and reciprocals, [12] normal-range rounding
+    // of every entry, [13] the general test for the rest. [8] counts tiles (lane 0 of each wave).
     uint64_t tclk[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     uint64_t tprev = TIMERS ? __builtin_amdgcn_s_memtime() : 0;
     auto tick = [&](int ph) __attribute__((always_inline)) {
@@ -920,11 +915,8 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             }
     };
 
-    // ---- one pipeline step, tile it:
-    //   B1    K(it) landed; the row group's maxima of tile it-1 are in sX
-    //   R1    base, fold, weight digits of tile it-1 to sWD; V(it) starts loading; score MFMAs
-    //   B1.5  every wave has read the K planes (K(it+1) starts loading) and written its digits
-    //   R2    P.V of tile it-1 beside the certification of tile it; maxima of tile it to sX
+    // ---- one pipeline step, tile it (B1, score MFMAs beside the base move and digits of tile
+    // it-1, B2, DMAs of K(it+1) and V(it), P.V of tile it-1, certification of tile it)
     auto step = [&](auto par, int it) __attribute__((always_inline)) {
         constexpr int PA = decltype(par)::value;
         const uint8_t* const sVp = PA ? sV0 : sV1;  // V(it - 1)
@@ -934,37 +926,41 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const uint32_t aMn = PA ? aM0 : aM1;        // metadata of tile it + 1
         const bool k_next = it + 1 < ntiles;
         tick(7);
-        // every DMA landed: K(it) and its metadata (issued early in the previous step) and V(it - 1)
-        // (issued after them; the P.V of this step reads it and no later wait covers it)
+        // every DMA landed: K(it) and its metadata, and V(it - 1) (the P.V of this step reads it)
         wait_vm<0>();
         tick(14);
         pf_bar();      // B1
         tick(0);
         const int tfl = TMc->tfl;
-        // ---- score MFMAs of tile it, then (while they run) the previous tile's digits, then the
-        // fp64 scores
+        // the previous tile's inexact-V counts, read before its metadata buffer is reloaded
+        double evp[NCT];
+#pragma unroll
+        for (int cc = 0; cc < NCT; ++cc) evp[cc] = TMp->EV[16 * (NCT * hh + cc) + j];
+        // ---- score MFMAs of tile it, then (while they run) the previous tile's base move and
+        // weight digits
         v4i sacc[NKT][7];
 #pragma unroll
         for (int kk = 0; kk < NKT; ++kk)
 #pragma unroll
             for (int k = 0; k < 7; ++k) sacc[kk][k] = (v4i){0, 0, 0, 0};
-        if (needq || ((tfl >> (NKT * hh)) & ((1 << NKT) - 1))) {
+        const bool wide = needq || ((tfl >> (NKT * hh)) & ((1 << NKT) - 1));
+        auto scores = [&]() __attribute__((always_inline)) {
+            if (wide) {
 #pragma unroll
-            for (int kk = 0; kk < NKT; ++kk) score_mfma<true>(kb, qb, NKT * hh + kk, sacc[kk]);
-        } else {
+                for (int kk = 0; kk < NKT; ++kk) score_mfma<true>(kb, qb, NKT * hh + kk, sacc[kk]);
+            } else {
 #pragma unroll
-            for (int kk = 0; kk < NKT; ++kk) score_mfma<false>(kb, qb, NKT * hh + kk, sacc[kk]);
-        }
+                for (int kk = 0; kk < NKT; ++kk) score_mfma<false>(kb, qb, NKT * hh + kk, sacc[kk]);
+            }
+        };
+        scores();
         tick(1);
-        // the previous tile's inexact-V counts, read before its metadata buffer is reloaded
-        double evp[NCT];
-#pragma unroll
-        for (int cc = 0; cc < NCT; ++cc) evp[cc] = TMp->EV[16 * (NCT * hh + cc) + j];
-        if (PF_EARLY_K) {
-            pf_bar();  // every wave has read the K planes of tile it: K(it+1) starts loading now
-            if (k_next) issue_k(it + 1, aMn);
-        }
         if (it > 0) rebase_digits(evp);
+        tick(2);
+        // every wave has read the K planes of tile it and written the weight digits of tile it - 1:
+        // K(it + 1) with its metadata and V(it) start loading
+        pf_bar();
+        if (k_next) issue_k(it + 1, aMn);
         issue_v(it, aVc);
         v4i lk4[NKT];
         double xs[NKT][4];
@@ -973,9 +969,6 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             lk4[kk] = *(const v4i*)&TMc->lsbk[16 * (NKT * hh + kk) + 4 * g];
             score_fold(sacc[kk], lk4[kk], xs[kk]);
         }
-        tick(2);
-        pf_bar();  // B1.5: every wave has read the K planes of tile it and written its digits
-        if (!PF_EARLY_K && k_next) issue_k(it + 1, aMn);
         v4i Wd[5];
         read_wd(Wd);  // zero at it = 0
         if (it > 0) ++ep_tiles;
@@ -1050,15 +1043,6 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 Ek[kk][i] = E[i];
                 gm = max(gm, good ? E[i] + vl4[kk][i] : INT_MIN);
             }
-            // interleave: each P.V MFMA followed by VALU work of the certification, so the matrix
-            // core runs while the vector ALU certifies (one wave per SIMD: no other wave fills
-            // the gaps)
-#pragma unroll
-            for (int m = 0; m < 19 * (NCT / NKT); ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, PF_VALU_PER_MFMA, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
         }
         tick(4);
         // ---- cold path: exact decision for the pairs the fast path left undecided. The exact
