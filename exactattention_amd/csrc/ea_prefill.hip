@@ -596,8 +596,9 @@ constexpr int PF_OFF_V0 = 32768;
 constexpr int PF_OFF_V1 = 65536;
 constexpr int PF_OFF_M0 = 98304;
 constexpr int PF_OFF_M1 = PF_OFF_M0 + 4096;
-constexpr int PF_OFF_Q = PF_OFF_M1 + 4096;  // 32 rows x 512 bytes
-constexpr int PF_OFF_T = PF_OFF_Q + 16384;
+constexpr int PF_QROW = 528;                 // q digit row stride in LDS: 512 bytes + 16 of padding
+constexpr int PF_OFF_Q = PF_OFF_M1 + 4096;  // 32 rows x PF_QROW bytes
+constexpr int PF_OFF_T = PF_OFF_Q + 32 * PF_QROW;
 constexpr int PF_OFF_WD = PF_OFF_T + 4096;  // 5 planes x 4 key groups x 2 row groups x 64 lanes x 4 B
 constexpr int PF_OFF_X = PF_OFF_WD + 10240;  // up to 8 waves x 64 lanes x 16 bytes
 constexpr int PF_OFF_KEND = PF_OFF_X + 8192;
@@ -688,20 +689,20 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const int kw = wave_max_i(ve);
         if (lane == 0) atomicMax(&s_kend, kw);
     }
-    // q digits of the block's rows into LDS: [row][plane 4][128 bytes], 16-byte chunk c of row r
-    // at chunk c ^ (r & 7) (conflict-free reads across the 8 rows of a lane group); rows past the
-    // segment repeat its last row
+    // q digits of the block's rows into LDS: [row][plane 4][128 bytes] with rows PF_QROW = 528
+    // bytes apart, so the 16 rows a 16-lane group reads start 4 banks apart (132 dwords = 4 mod 64)
+    // and a 16-byte read per lane touches every bank once; rows past the segment repeat its last row
     for (int c = tid; c < RPB * 32; c += 64 * NWB) {
         const int r = c >> 5, q16 = c & 31;
         const int lrr = min(rbk * RPB + r, P.r_seg - 1);
         int tt;
         const int64_t gr = seg_row(P, b, hk, lrr, &tt);
-        *(uint4*)(sQ + r * 512 + ((q16 ^ (r & 7)) << 4)) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
+        *(uint4*)(sQ + r * PF_QROW + q16 * 16) = *(const uint4*)(P.pfq + gr * 512 + q16 * 16);
     }
     // this lane's q digits (B operand of the score MFMA): row j, dims 64 h + 16 g .. + 15, plane s:
-    // chunk 8 s + 4 h + g of the row, swizzled; (8 s + 4 h + g) ^ (j & 7) = 8 s + ((4 h + g) ^ (j & 7))
-    const uint8_t* const qlds = sQ + (rg * 16 + j) * 512;
-    const uint8_t* const qb[2] = {qlds + ((g ^ (j & 7)) << 4), qlds + (((4 + g) ^ (j & 7)) << 4)};
+    // chunk 8 s + 4 h + g of the row
+    const uint8_t* const qlds = sQ + (rg * 16 + j) * PF_QROW;
+    const uint8_t* const qb[2] = {qlds + (g << 4), qlds + ((4 + g) << 4)};
     // K operand: key 16 kt + j, chunk (4 h + g) ^ (j & 7), plane t at + 8192 t, key group at + 2048 kt
     const uint8_t* const kb[2] = {sK + j * 128 + ((g ^ (j & 7)) << 4), sK + j * 128 + (((4 + g) ^ (j & 7)) << 4)};
     const PfQMeta qm = ((const PfQMeta*)P.pfqm)[grow];
@@ -1068,7 +1069,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                          (int64_t)(hk * P.grp + lrc % P.grp) * P.g.q_head_stride;
                     kr = P.k + kv_off(P, b, n, hk, 0);
                 }
-                const int3 cw = pf_cold_pair(mode, qlds, j & 7, (const uint8_t*)Kg + key * 128, key & 7, qr, kr, P.am,
+                const int3 cw = pf_cold_pair(mode, qlds, 0, (const uint8_t*)Kg + key * 128, key & 7, qr, kr, P.am,
                                              P.ae + qm.lsb + TMc->lsbk[key], P.alpha, T1s, T2);
                 const bool live = cw.x == 0;
                 const int32_t M = cw.y, E = cw.z;
