@@ -528,25 +528,16 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
 // merging adds depth nsplit, so with A = sum_s 2^(R_s - R) Zhat_s (n_s + nsplit + 4):
 //   eZ = u' A + tiny,  eN_c = u' A max_s Vmax_sc + tiny.
 // ------------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) ea_combine(Params P) {
-    __shared__ int s_ev[4];
-    const int w = threadIdx.x >> 6;
-    const int64_t row = (int64_t)blockIdx.x * 4 + w;
-    const int ev = row < P.rows ? combine_row(P, row, threadIdx.x & 63) : 0;
-    if ((threadIdx.x & 63) == 0) s_ev[w] = ev;
-    __syncthreads();
-    // one atomic per counter and block: same-address atomics per row would serialise
-    if (threadIdx.x == 0 && P.stats) {
-        int n0 = 0, n1 = 0, n7 = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            n0 += s_ev[i] & 1;
-            n1 += (s_ev[i] >> 1) & 1;
-            n7 += (s_ev[i] >> 2) & 1;
-        }
-        if (n0) atomicAdd((unsigned long long*)&P.stats[0], (unsigned long long)n0);
-        if (n1) atomicAdd((unsigned long long*)&P.stats[1], (unsigned long long)n1);
-        if (n7) atomicAdd((unsigned long long*)&P.stats[7], (unsigned long long)n7);
+__global__ void __launch_bounds__(64) ea_combine(Params P) {
+    // one row per 64-thread block: the merge is a chain of dependent loads, so it wants as many
+    // rows in flight as the machine holds. stats[0] counts the step's rows once; the per-row
+    // counters only move for flagged rows (rare), so they never serialise on one address.
+    const int64_t row = blockIdx.x;
+    if (row == 0 && threadIdx.x == 0 && P.stats) atomicAdd((unsigned long long*)&P.stats[0], (unsigned long long)P.rows);
+    const int ev = combine_row(P, row, threadIdx.x);
+    if (threadIdx.x == 0 && P.stats && (ev & 2)) {
+        atomicAdd((unsigned long long*)&P.stats[1], 1ull);
+        if (ev & 4) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
     }
 }
 
@@ -1211,7 +1202,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         return rc;
     }
     if ((rc = mark(2))) return rc;
-    hipLaunchKernelGGL(ea_combine, dim3(rb4), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(ea_combine, dim3((unsigned)pl.rows), dim3(64), 0, st, P);
     rc = herr(hipGetLastError());
     if (rc) return rc;
     if ((rc = mark(3))) return rc;
