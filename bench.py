@@ -207,9 +207,46 @@ def prefill_line(steps: int, warmup: int) -> dict:
                      "cold_pairs": st["slow_path_scores"] / steps},
         "input_gen_s": round(r["gen_s"], 1),
     }
+    line["kv_digits"] = kv_digits_line(r)
     del r
     torch.cuda.empty_cache()
     return line
+
+
+def kv_digits_line(r: dict, reps: int = 20) -> dict:
+    """The KV write path on C3: the digit-tile cache (ea_hip_kv_digits_update) after an append of
+    64 keys per sequence (one tile per KV head) and after all 4096, and one C3 step that reads its
+    K/V tiles from the cache instead of slicing them; the step's bits against the golden hash."""
+    import torch
+    from exactattention_amd.hip import KVDigits, launch_hip
+    dp, ab = r["dp"], r["ab"]
+    S = int(r["prob"]["seq_len"].max())
+    cache = KVDigits(dp, (S + 63) // 64)
+    z = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    e = torch.full((1,), S, dtype=torch.int32, device="cuda:0")
+    b64 = torch.full((1,), S - 64, dtype=torch.int32, device="cuda:0")
+    cache.update(dp, z, e, S)
+    torch.cuda.synchronize()
+    ev = HipEvents(6)
+
+    def timed(fn, i):
+        ev.h.hipEventRecord(ev.ev[2 * i], ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        for _ in range(reps):
+            fn()
+        ev.h.hipEventRecord(ev.ev[2 * i + 1], ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        return ev.ms(2 * i, 2 * i + 1) / reps
+
+    ev.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    full_ms = timed(lambda: cache.update(dp, z, e, S), 0)
+    tile_ms = timed(lambda: cache.update(dp, b64, e, 64), 1)
+    step_ms = timed(lambda: launch_hip(dp, ab, kv_digits=cache), 2)
+    ev.close()
+    out = dp.out.cpu().numpy().view(np.uint16)
+    golden = json.load(open(GOLDEN)).get("C3", {}).get("sha256") if os.path.exists(GOLDEN) else None
+    return {"update_ms_all_4096_keys": round(full_ms, 5), "update_ms_append_64_keys": round(tile_ms, 5),
+            "step_ms_reading_cache": round(step_ms, 5), "step_ms_slicing": round(r["ms_step"], 5),
+            "bit_exact_reading_cache": (hashlib.sha256(out.tobytes()).hexdigest() == golden) if golden else None}
 
 
 def main():

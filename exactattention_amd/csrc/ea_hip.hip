@@ -1061,7 +1061,12 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     if (pl->prefill) {
         pl->off_pfq = off; off = align_up(off + (size_t)R * 512);
         pl->off_pfqm = off; off = align_up(off + (size_t)R * sizeof(PfQMeta));
-        pl->off_pfkv = off; off = align_up(off + (size_t)pl->nseg * pl->pf_ntiles * EA_PF_TILE_BYTES);
+        if (o->kv_digits) {
+            // the caller's digit cache holds the K/V tiles: nothing to slice into the workspace
+            if (o->kv_digits_tiles < pl->pf_ntiles) return -1;
+        } else {
+            pl->off_pfkv = off; off = align_up(off + (size_t)pl->nseg * pl->pf_ntiles * EA_PF_TILE_BYTES);
+        }
         pl->off_pfscr = off; off = align_up(off + (size_t)pl->nseg * pl->pf_nrb * 512 * 32 * 8);
     }
     pl->total = off;
@@ -1135,8 +1140,12 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.pfq = (uint8_t*)(ws + pl.off_pfq);
     P.pfqm = (void*)(ws + pl.off_pfqm);
     P.pfkv = (uint8_t*)(ws + pl.off_pfkv);
+    if (pl.prefill && o->kv_digits) {
+        P.pfkv = (uint8_t*)o->kv_digits;
+        P.pf_kv_cached = 1;
+    }
     P.pfscr = (double*)(ws + pl.off_pfscr);
-    P.pf_ntiles = pl.pf_ntiles;
+    P.pf_ntiles = (pl.prefill && o->kv_digits) ? o->kv_digits_tiles : pl.pf_ntiles;
     P.pf_nrb = pl.pf_nrb;
     hipStream_t st = (hipStream_t)stream;
     unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
@@ -1298,6 +1307,36 @@ done:
 #undef EA_TRY
     if (rc) return rc;
     return herr(e);
+}
+
+size_t ea_hip_kv_digits_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t tiles_per_seq) {
+    if (num_seqs <= 0 || num_kv_heads <= 0 || tiles_per_seq <= 0) return 0;
+    return (size_t)num_seqs * num_kv_heads * tiles_per_seq * EA_PF_TILE_BYTES;
+}
+
+int ea_hip_kv_digits_update(const ea_geometry* g, const ea_buffers* b, const int32_t* key_begin,
+                            const int32_t* key_end, int32_t max_new_keys, void* kv_digits, int32_t tiles_per_seq,
+                            ea_stream_t stream) {
+    if (!g || !b || !b->k || !b->v || !b->seq_len || !key_begin || !key_end || !kv_digits) return -1;
+    if (tiles_per_seq <= 0 || max_new_keys < 0 || g->num_seqs < 0 || g->num_kv_heads <= 0) return -1;
+    if (g->head_dim != 128 || g->head_dim_v != 128) return -1;  // the digit tiles are for d = dv = 128
+    if (g->page_size <= 0 || (g->page_size & (g->page_size - 1))) return -1;
+    if ((int64_t)tiles_per_seq * 64 >= (1 << 30)) return -1;
+    if (max_new_keys == 0 || g->num_seqs == 0) return 0;
+    Params P;
+    memset(&P, 0, sizeof(P));
+    P.g = *g;
+    P.k = b->k; P.v = b->v; P.seq_len = b->seq_len; P.bt = b->block_table; P.bt_off = b->block_table_offset;
+    int ps = 0;
+    while ((1 << ps) < g->page_size) ++ps;
+    P.pshift = ps;
+    P.nseg = g->num_seqs * g->num_kv_heads;
+    P.pfkv = (uint8_t*)kv_digits;
+    P.pf_ntiles = tiles_per_seq;
+    P.kvd_begin = key_begin;
+    P.kvd_end = key_end;
+    P.kvd_span = (int32_t)(((int64_t)max_new_keys + 63) / 64 + 1);  // a key range meets at most this many tiles
+    return ea_launch_kv_digits(P, (hipStream_t)stream);
 }
 
 int ea_hip_kat_weight(int64_t n, const uint32_t* t_bits, int32_t* M, int64_t* E, int32_t* status, int32_t* M2,

@@ -63,6 +63,12 @@ struct Params {
     double* pfscr;    // nseg * pf_nrb * 512 lanes * 32: per-lane sums of completed epochs
     int32_t pf_ntiles;  // 64-key tiles per segment
     int32_t pf_nrb;     // 64-row blocks per segment
+    // digit-tile cache (ea_hip_kv_digits_update): with kvd_begin set, ea_pf_kvslice re-slices the
+    // tiles that hold keys [kvd_begin[b], kvd_end[b]) of each sequence, kvd_span tiles per segment
+    const int32_t* kvd_begin;
+    const int32_t* kvd_end;
+    int32_t kvd_span;
+    int32_t pf_kv_cached;  // 1: pfkv is the caller's digit cache, already sliced
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
@@ -184,6 +190,8 @@ int ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb);
 // Enqueue the slicing kernels (q rows, K/V tiles), then the prefill kernel; 0 or -100 - e.
 int ea_launch_prefill(const Params& P, hipStream_t st);
 int ea_launch_prefill_main(const Params& P, hipStream_t st);
+// Enqueue the re-slicing of the cached digit tiles P.kvd_begin / kvd_end name; 0 or -100 - e.
+int ea_launch_kv_digits(const Params& P, hipStream_t st);
 
 typedef const double __attribute__((address_space(4))) cdouble_t;
 typedef const int32_t __attribute__((address_space(4))) cint_t;

@@ -243,7 +243,18 @@ __global__ void __launch_bounds__(256) ea_pf_kvslice(Params P) {
     __shared__ int s_lc[128];
     __shared__ int s_tfl;
     const int tid = threadIdx.x, q4 = tid & 3, key = tid >> 2;
-    const int seg = blockIdx.x / P.pf_ntiles, tile = blockIdx.x % P.pf_ntiles;
+    int seg, tile;
+    if (P.kvd_begin) {
+        // cache update: block i of a segment re-slices the i-th tile that holds an appended key
+        seg = blockIdx.x / P.kvd_span;
+        const int bs = seg / P.g.num_kv_heads;
+        const int kb = max(P.kvd_begin[bs], 0), ke = P.kvd_end[bs];
+        tile = kb / 64 + (int)(blockIdx.x % P.kvd_span);
+        if (ke <= kb || tile * 64 >= ke || tile >= P.pf_ntiles) return;  // uniform: the whole block
+    } else {
+        seg = blockIdx.x / P.pf_ntiles;
+        tile = blockIdx.x % P.pf_ntiles;
+    }
     const int Hkv = P.g.num_kv_heads;
     const int64_t b = seg / Hkv;
     const int hk = seg % Hkv;
@@ -318,6 +329,7 @@ __global__ void __launch_bounds__(256) ea_pf_kvslice(Params P) {
         int tot = 0;
         for (int c = 0; c < 128; ++c) tot += s_lc[c];
         TM->tfl = s_tfl;
+        TM->pad = 0;
         TM->EVt = 0.5 * (0x1p38 + 1.0) * (double)tot;
     }
 }
@@ -1366,12 +1378,20 @@ int ea::ea_launch_prefill(const Params& P, hipStream_t st) {
     hipLaunchKernelGGL(ea_pf_qslice, dim3((unsigned)((P.rows + 63) / 64)), dim3(256), 0, st, Pc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return -100 - (int)e;
-    if (P.nseg > 0 && P.pf_ntiles > 0) {
+    if (P.nseg > 0 && P.pf_ntiles > 0 && !P.pf_kv_cached) {
         hipLaunchKernelGGL(ea_pf_kvslice, dim3((unsigned)(P.nseg * P.pf_ntiles)), dim3(256), 0, st, Pc);
         e = hipGetLastError();
         if (e != hipSuccess) return -100 - (int)e;
     }
     return 0;
+}
+
+int ea::ea_launch_kv_digits(const Params& P, hipStream_t st) {
+    if (P.nseg <= 0 || P.kvd_span <= 0) return 0;
+    Params Pc = P;
+    hipLaunchKernelGGL(ea_pf_kvslice, dim3((unsigned)(P.nseg * P.kvd_span)), dim3(256), 0, st, Pc);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : -100 - (int)e;
 }
 
 int ea::ea_launch_prefill_main(const Params& P, hipStream_t st) {

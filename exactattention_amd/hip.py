@@ -40,7 +40,8 @@ class Buffers(ctypes.Structure):
 
 class Options(ctypes.Structure):
     _fields_ = [("alpha_bits", ctypes.c_uint32), ("out_fp32", ctypes.c_int32), ("splits", ctypes.c_int32),
-                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P), ("timers", P)]
+                ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P), ("timers", P),
+                ("kv_digits", P), ("kv_digits_tiles", ctypes.c_int32), ("pad1", ctypes.c_int32)]
 
 
 STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
@@ -76,6 +77,11 @@ def load():
         lib.ea_hip_kat_round.restype = ctypes.c_int
         lib.ea_hip_kat_round_ratio.argtypes = [ctypes.c_int64] + [P] * 6 + [ctypes.c_int32, P, P, P]
         lib.ea_hip_kat_round_ratio.restype = ctypes.c_int
+        lib.ea_hip_kv_digits_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+        lib.ea_hip_kv_digits_bytes.restype = ctypes.c_size_t
+        lib.ea_hip_kv_digits_update.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), P, P,
+                                                ctypes.c_int32, P, ctypes.c_int32, P]
+        lib.ea_hip_kv_digits_update.restype = ctypes.c_int
         lib.ea_hip_kat_rn32_prod.argtypes = [ctypes.c_int64] + [P] * 6 + [P]
         lib.ea_hip_kat_rn32_prod.restype = ctypes.c_int
         lib.ea_hip_kat_wave_max.argtypes = [ctypes.c_int64, P, P, P]
@@ -151,9 +157,10 @@ TIMER_PHASES = ["prologue", "tile_barrier", "scores", "score_barrier", "weights"
 
 
 def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True, events=None,
-               timers=None) -> None:
+               timers=None, kv_digits=None) -> None:
     """Enqueue one step on torch's current stream (no sync, no host copies, no allocation).
-    `events`: optional ctypes array of 5 hipEvent_t handles recorded between the kernels."""
+    `events`: optional ctypes array of 5 hipEvent_t handles recorded between the kernels.
+    `kv_digits`: optional KVDigits cache; the int8 prefill path then reads its K/V tiles there."""
     lib = load()
     mo = None
     if merge_order is not None:
@@ -161,10 +168,37 @@ def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool
     o = Options(alpha_bits=alpha_bits, out_fp32=int(dp.out_fp32), splits=dp.splits, tier2=int(tier2),
                 merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr(),
                 events=None if events is None else ctypes.cast(events, P),
-                timers=None if timers is None else timers.data_ptr())
+                timers=None if timers is None else timers.data_ptr(),
+                kv_digits=None if kv_digits is None else kv_digits.buf.data_ptr(),
+                kv_digits_tiles=0 if kv_digits is None else kv_digits.tiles)
     b = dp.buffers()
     _check(lib.ea_hip_attention(ctypes.byref(dp._geom_c), ctypes.byref(b), ctypes.byref(o), dp.workspace.data_ptr(),
                                 dp.ws_bytes, _stream_ptr(dp.torch)), "ea_hip_attention")
+
+
+class KVDigits:
+    """A device digit-tile cache of a problem's K/V (the KV slice format kept across steps):
+    `tiles` 64-key tiles per (sequence, KV head), EA_PF_TILE_BYTES each, laid out as
+    include/exactattn_hip.h describes for ea_hip_kv_digits_update."""
+
+    def __init__(self, dp: DeviceProblem, tiles: int):
+        import torch
+        lib = load()
+        g = dp.geom
+        n = lib.ea_hip_kv_digits_bytes(int(g["num_seqs"]), int(g["num_kv_heads"]), int(tiles))
+        if n == 0:
+            raise ValueError("empty digit cache")
+        self.tiles = int(tiles)
+        self.buf = torch.zeros(n, dtype=torch.uint8, device=dp.out.device)
+
+    def update(self, dp: DeviceProblem, key_begin, key_end, max_new_keys: int) -> None:
+        """Re-slice the tiles that hold keys key_begin[b] .. key_end[b] - 1 of each sequence
+        (device int32 tensors), after they were written to dp's bf16 cache."""
+        lib = load()
+        b = dp.buffers()
+        _check(lib.ea_hip_kv_digits_update(ctypes.byref(dp._geom_c), ctypes.byref(b), key_begin.data_ptr(),
+                                           key_end.data_ptr(), int(max_new_keys), self.buf.data_ptr(), self.tiles,
+                                           _stream_ptr(dp.torch)), "ea_hip_kv_digits_update")
 
 
 def merge_order_tensor(order, nsplit: int, device="cuda"):

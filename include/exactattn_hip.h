@@ -95,6 +95,13 @@ typedef struct ea_options {
                                [3] wait for the score barrier, [4] logits and weights, [5] P.V,
                                [6] epilogue, [7] tiles; the reference's TIMERS build
                                (src/exactattn/triton_kernels.py:747-766) */
+    void* kv_digits;        /* optional: the caller's int8 digit-tile cache of K/V
+                               (ea_hip_kv_digits_update). When set and the step takes the int8
+                               prefill path, its K/V tiles are read there and nothing is sliced;
+                               the other paths read the bf16 cache and ignore it */
+    int32_t kv_digits_tiles; /* tiles per (sequence, KV head) in kv_digits; must be at least
+                               ceil(max_seq_len / 64) */
+    int32_t pad1;
 } ea_options;
 
 /* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
@@ -147,6 +154,26 @@ int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo
  * RN_fp32(alpha * s) (src/exactattn/reference.py:74-79). */
 int ea_hip_kat_rn32_prod(int64_t n, const int32_t* am, const int64_t* x_hi, const uint64_t* x_lo, const int32_t* E,
                          uint32_t* bits, int32_t* status, ea_stream_t stream);
+
+/* The KV slice format as a cache (the write path of a serving loop). For every sequence b and KV
+ * head hk, tiles_per_seq tiles of 64 keys, EA_PF_TILE_BYTES = 69632 bytes each, tile t at byte
+ * ((b * num_kv_heads + hk) * tiles_per_seq + t) * 69632: K and V as four balanced radix-256
+ * int8 digit planes each plus per-key and per-channel metadata (exactattention_amd/csrc/
+ * ea_params.h), the same tiles the prefill path otherwise slices into its workspace every step.
+ * ea_hip_kv_digits_bytes: the cache size.
+ * ea_hip_kv_digits_update: after keys key_begin[b] .. key_end[b] - 1 of each sequence b were
+ *   written to the bf16 cache (and seq_len covers them), re-slice every tile that holds one of
+ *   them, whole (keys at or past seq_len[b] slice as zero, so a tile is sliced again as it fills).
+ *   key_begin, key_end: device int32[num_seqs]; max_new_keys >= every key_end[b] - key_begin[b]
+ *   (sizes the grid); tiles at or past tiles_per_seq are skipped. Returns 0, -1 on bad arguments,
+ *   -100 - e on a HIP error. Enqueue only (no sync).
+ * Reference counterpart: the device slicing of the K/V caches, tc_slices_device /
+ * tc_v_slices_device (src/exactattn/triton_kernels.py:1255-1280), which the reference reruns on
+ * the whole cache at every launch. */
+size_t ea_hip_kv_digits_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t tiles_per_seq);
+int ea_hip_kv_digits_update(const ea_geometry* g, const ea_buffers* b, const int32_t* key_begin,
+                            const int32_t* key_end, int32_t max_new_keys, void* kv_digits, int32_t tiles_per_seq,
+                            ea_stream_t stream);
 
 /* Library version string. */
 const char* ea_hip_version(void);

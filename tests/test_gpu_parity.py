@@ -556,6 +556,102 @@ def test_prefill_rows_longer_than_256_tiles(gpu):
     assert np.array_equal(got, want)
 
 
+# ---------------------------------------------------------------------------------------------
+# the digit-tile cache (the KV slice format kept across steps: ea_hip_kv_digits_update)
+# ---------------------------------------------------------------------------------------------
+
+def _kv_digits_problem(rng, paged_cache):
+    B, T, Hq, Hkv, d, S = 2, 70, 4, 2, 128, 300
+    q = bf16(rng, (B, T, Hq, d))
+    k = bf16(rng, (B, Hkv, S, d), "wide")
+    v = bf16(rng, (B, Hkv, S, d), "outlier")
+    seq = np.array([300, 251])
+    kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    base = problem.contiguous(q, k, v, kv, seq_len=seq)
+    return problem.to_paged(base, 16, np.random.default_rng(5), "NHD") if paged_cache else base
+
+
+@pytest.mark.parametrize("paged_cache", [False, True])
+def test_kv_digits_appends_equal_one_update(gpu, paged_cache):
+    """Slicing a cache in appended chunks (seq_len growing with each append, so partly filled tiles
+    are sliced again) leaves the same bytes as one update over every key."""
+    import torch
+    from exactattention_amd.hip import DeviceProblem, KVDigits
+    prob = _kv_digits_problem(np.random.default_rng(61), paged_cache)
+    dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+    seq = prob["seq_len"].copy()
+    tiles = (int(seq.max()) + 63) // 64
+    one = KVDigits(dp, tiles)
+    zeros = torch.zeros(2, dtype=torch.int32, device="cuda")
+    one.update(dp, zeros, torch.from_numpy(seq.astype(np.int32)).cuda(), int(seq.max()))
+    chunked = KVDigits(dp, tiles)
+    bounds = [0, 100, 170, 229, 300]
+    for a, e in zip(bounds[:-1], bounds[1:]):
+        cur = np.minimum(seq, e).astype(np.int32)
+        dp.t["seq_len"].copy_(torch.from_numpy(cur))
+        kb = torch.from_numpy(np.minimum(seq, a).astype(np.int32)).cuda()
+        chunked.update(dp, kb, dp.t["seq_len"].clone(), e - a)
+    torch.cuda.synchronize()
+    assert torch.equal(one.buf, chunked.buf)
+
+
+@pytest.mark.parametrize("paged_cache", [False, True])
+def test_prefill_reads_kv_digits_cache(gpu, force_prefill, paged_cache):
+    """The prefill kernel reading the caller's digit cache gives the bits it gives when it slices
+    K/V itself, and the oracle's."""
+    import torch
+    from exactattention_amd.hip import DeviceProblem, KVDigits, STATS, launch_hip
+    prob = _kv_digits_problem(np.random.default_rng(62), paged_cache)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    plain, fl, st = _run(prob, ab)
+    assert st["prefill_kernel_rows"] == _rows(prob) and not np.any(fl), st
+    assert np.array_equal(plain, want)
+    dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+    cache = KVDigits(dp, (int(prob["seq_len"].max()) + 63) // 64)
+    cache.update(dp, torch.zeros(2, dtype=torch.int32, device="cuda"), dp.t["seq_len"].clone(),
+                 int(prob["seq_len"].max()))
+    launch_hip(dp, ab, kv_digits=cache)
+    torch.cuda.synchronize()
+    got = dp.out.cpu().numpy().view(np.uint16)
+    st2 = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    assert st2["prefill_kernel_rows"] == _rows(prob), st2
+    assert not np.any(dp.flags.cpu().numpy())
+    assert np.array_equal(got, want)
+
+
+def test_chunked_prefill_from_the_cache_equals_full_prefill(gpu):
+    """A 192-token prefill served as three 64-token chunks: each chunk appends its keys to the
+    digit cache (only the new tiles are sliced) and attends through the cache; every row equals the
+    one-shot causal prefill's."""
+    import torch
+    from exactattention_amd.hip import DeviceProblem, KVDigits, launch_hip
+    rng = np.random.default_rng(63)
+    B, T, Hq, Hkv, d = 1, 192, 4, 2, 128
+    q = bf16(rng, (B, T, Hq, d))
+    k = bf16(rng, (B, Hkv, T, d))
+    v = bf16(rng, (B, Hkv, T, d))
+    ab = default_alpha_bits(d)
+    full = problem.contiguous(q, k, v, (np.arange(T) + 1).reshape(1, T))
+    want, fl, st = _run(full, ab)
+    assert st["prefill_kernel_rows"] == _rows(full) and not np.any(fl), st
+    # the cache lives beside a problem that holds the whole K/V; seq_len grows with each chunk
+    host = DeviceProblem(full, "bf16", 0, "cuda:0")
+    cache = KVDigits(host, T // 64)
+    for c in range(3):
+        a, e = 64 * c, 64 * c + 64
+        host.t["seq_len"].fill_(e)
+        cache.update(host, torch.full((1,), a, dtype=torch.int32, device="cuda"),
+                     torch.full((1,), e, dtype=torch.int32, device="cuda"), 64)
+        chunk = problem.contiguous(q[:, a:e], k, v, (np.arange(a, e) + 1).reshape(1, 64), seq_len=np.array([e]))
+        dp = DeviceProblem(chunk, "bf16", 0, "cuda:0")
+        launch_hip(dp, ab, kv_digits=cache)
+        torch.cuda.synchronize()
+        got = dp.out.cpu().numpy().view(np.uint16)
+        assert not np.any(dp.flags.cpu().numpy()), c
+        assert np.array_equal(got[0], want[0, a:e]), c
+
+
 def test_prefill_nonfinite_flags_exactly_the_rows_that_see_them(gpu, force_prefill):
     rng = np.random.default_rng(45)
     T = 80
