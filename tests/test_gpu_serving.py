@@ -1,0 +1,87 @@
+"""A serving session through exactattention_amd.serving (paged cache, chunked prefill through the
+digit-tile cache, batched decode, speculative tree verification, accepted-path compaction): every
+row against the oracle on the logical, contiguous K/V history."""
+
+import numpy as np
+import pytest
+
+from exactattention_amd import configs, problem
+from exactattention_amd.formats import default_alpha_bits
+from gen import bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_rows(q, K, V, kv_len, alpha_bits, tree_mask=None, tree_base=None):
+    """q (T, Hq, d); K, V (S, Hkv, d) logical history of one sequence."""
+    from oracle import oracle
+    prob = problem.contiguous(q[None], K.transpose(1, 0, 2)[None], V.transpose(1, 0, 2)[None],
+                              np.asarray(kv_len).reshape(1, -1), tree_mask=tree_mask,
+                              tree_base=None if tree_base is None else np.array([tree_base]))
+    out, _ = oracle.attention_geom(prob, alpha_bits, "bf16")
+    return out[0]
+
+
+def test_serving_session_matches_oracle(gpu):
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    rng = np.random.default_rng(71)
+    Hq, Hkv, d = 4, 2, 128
+    ab = default_alpha_bits(d)
+    cache = PagedKVCache(num_pages=80, page_size=16, num_kv_heads=Hkv, head_dim=d, max_seqs=3, max_seq_len=400)
+    be = ExactAttentionBackend(cache, Hq, ab)
+    slots = [cache.add_sequence(), cache.add_sequence()]
+    hist = {s: (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16)) for s in slots}
+
+    def grow(s, k, v):
+        hist[s] = (np.concatenate([hist[s][0], k]), np.concatenate([hist[s][1], v]))
+
+    # chunked prefill: 64 + 64 + 22 tokens for the first sequence, 90 for the second
+    for s, chunks in ((slots[0], (64, 64, 22)), (slots[1], (90,))):
+        for T in chunks:
+            L = len(hist[s][0])
+            q, k, v = bf16(rng, (T, Hq, d)), bf16(rng, (T, Hkv, d)), bf16(rng, (T, Hkv, d))
+            got, fl = be.prefill(s, q, k, v)
+            grow(s, k, v)
+            assert not np.any(fl), (s, T)
+            want = _oracle_rows(q, *hist[s], L + 1 + np.arange(T), ab)
+            assert np.array_equal(got, want), (s, L, T)
+    # three decode steps, both sequences in one call
+    for step in range(3):
+        q, k, v = bf16(rng, (2, Hq, d)), bf16(rng, (2, Hkv, d)), bf16(rng, (2, Hkv, d))
+        got, fl = be.decode(slots, q, k, v)
+        assert not np.any(fl), step
+        for i, s in enumerate(slots):
+            grow(s, k[i:i + 1], v[i:i + 1])
+            want = _oracle_rows(q[i:i + 1], *hist[s], [len(hist[s][0])], ab)
+            assert np.array_equal(got[i], want[0]), (step, s)
+    # speculative verification of 12 draft nodes on the first sequence, then keep a path
+    s = slots[0]
+    L = len(hist[s][0])
+    parents = configs.draft_tree(rng, 12)
+    q, k, v = bf16(rng, (12, Hq, d)), bf16(rng, (12, Hkv, d)), bf16(rng, (12, Hkv, d))
+    got, fl = be.verify_tree(s, q, k, v, parents)
+    assert not np.any(fl)
+    mask = np.array([sum(1 << a for a in configs.path_of(parents, i)) for i in range(12)], dtype=np.uint64)
+    want = _oracle_rows(q, np.concatenate([hist[s][0], k]), np.concatenate([hist[s][1], v]), np.full(12, L), ab,
+                        tree_mask=mask, tree_base=L)
+    assert np.array_equal(got, want)
+    path = configs.path_of(parents, 11)
+    be.accept(s, L, path, k, v)
+    grow(s, k[np.asarray(path)], v[np.asarray(path)])
+    assert cache.length[s] == len(hist[s][0])
+    # one more decode step on both sequences sees the accepted path only
+    q, k, v = bf16(rng, (2, Hq, d)), bf16(rng, (2, Hkv, d)), bf16(rng, (2, Hkv, d))
+    got, fl = be.decode(slots, q, k, v)
+    assert not np.any(fl)
+    for i, s2 in enumerate(slots):
+        grow(s2, k[i:i + 1], v[i:i + 1])
+        want = _oracle_rows(q[i:i + 1], *hist[s2], [len(hist[s2][0])], ab)
+        assert np.array_equal(got[i], want[0]), s2
+    # a 64-token prefill chunk after the truncation reads re-sliced tiles
+    T = 64
+    Lb = len(hist[s][0])
+    q, k, v = bf16(rng, (T, Hq, d)), bf16(rng, (T, Hkv, d)), bf16(rng, (T, Hkv, d))
+    got, fl = be.prefill(s, q, k, v)
+    grow(s, k, v)
+    assert not np.any(fl)
+    assert np.array_equal(got, _oracle_rows(q, *hist[s], Lb + 1 + np.arange(T), ab))
