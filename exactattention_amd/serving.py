@@ -83,28 +83,47 @@ class PagedKVCache:
     def append(self, s: int, k_bits, v_bits) -> None:
         """Append n keys (k_bits, v_bits: (n, Hkv, d) uint16 arrays or int16 device tensors) to slot s,
         then re-slice the digit tiles they touch."""
+        self.append_batch([s], [len(k_bits)], k_bits, v_bits)
+
+    def append_batch(self, seqs, counts, k_bits, v_bits) -> None:
+        """Append counts[i] keys to slot seqs[i] for every i, the keys flattened in that order
+        (k_bits, v_bits: (sum(counts), Hkv, d)); one device scatter for the batch, then one
+        digit re-slice over every slot the batch touched."""
         torch = self.torch
         k_new = _dev16(torch, k_bits, self.dev)
         v_new = _dev16(torch, v_bits, self.dev)
-        n = k_new.shape[0]
-        if n == 0:
+        counts = [int(n) for n in counts]
+        if k_new.shape[0] != sum(counts) or v_new.shape[0] != sum(counts):
+            raise ValueError("k/v must hold sum(counts) keys")
+        if len(set(seqs)) != len(seqs):
+            raise ValueError("a slot may appear once per batch")
+        if sum(counts) == 0:
             return
-        L = self.length[s]
-        if L + n > self.max_seq_len:
-            raise ValueError("sequence longer than the cache's max_seq_len")
-        need = (L + n + self.P - 1) // self.P
-        while len(self.pages[s]) < need:
-            if not self.free:
-                raise RuntimeError("out of pages")
-            self.pages[s].append(self.free.pop())
-        self.block_table[s, :len(self.pages[s])] = torch.tensor(self.pages[s], dtype=torch.int32, device=self.dev)
-        pos = torch.arange(L, L + n, device=self.dev)
-        pg = self.block_table[s][pos // self.P].long()
-        sl = pos % self.P
-        self.k[pg, sl] = k_new
-        self.v[pg, sl] = v_new
-        self.length[s] = L + n
-        self._reslice(s, L, L + n)
+        need = []
+        for s, n in zip(seqs, counts):
+            if self.length[s] + n > self.max_seq_len:
+                raise ValueError("sequence longer than the cache's max_seq_len")
+            need.append(max(0, (self.length[s] + n + self.P - 1) // self.P - len(self.pages[s])))
+        if sum(need) > len(self.free):
+            raise RuntimeError("out of pages")
+        pg, sl, begin, end = [], [], [], []
+        for s, n, m in zip(seqs, counts, need):
+            L = self.length[s]
+            self.pages[s].extend(self.free.pop() for _ in range(m))
+            pos = np.arange(L, L + n)
+            pg.append(np.asarray(self.pages[s], dtype=np.int64)[pos // self.P])
+            sl.append(pos % self.P)
+            begin.append(L)
+            end.append(L + n)
+        for s in seqs:
+            self.block_table[s, :len(self.pages[s])] = torch.tensor(self.pages[s], dtype=torch.int32, device=self.dev)
+        pg_d = torch.from_numpy(np.concatenate(pg)).to(self.dev)
+        sl_d = torch.from_numpy(np.concatenate(sl).astype(np.int64)).to(self.dev)
+        self.k[pg_d, sl_d] = k_new
+        self.v[pg_d, sl_d] = v_new
+        for s, e in zip(seqs, end):
+            self.length[s] = e
+        self._reslice_slots(list(seqs), begin, end)
 
     def truncate(self, s: int, length: int) -> None:
         """Drop the keys at or past `length` (rejected draft nodes); the tile holding the new end is
@@ -117,6 +136,34 @@ class PagedKVCache:
         self.pages[s] = self.pages[s][:keep]
         if length % TILE:
             self._reslice(s, length - 1, length)
+
+    def _reslice_slots(self, seqs, begin, end) -> None:
+        """Re-slice keys begin[i]..end[i]-1 of slot seqs[i]: one update over all slots, where the
+        untouched slots get an empty range (their blocks exit at once)."""
+        if self.digits is None:
+            return
+        torch = self.torch
+        lib = hip.load()
+        kb = np.zeros(self.max_seqs, dtype=np.int32)
+        ke = np.zeros(self.max_seqs, dtype=np.int32)
+        kb[list(seqs)] = begin
+        ke[list(seqs)] = end
+        span = int(max(e - a for a, e in zip(begin, end)))
+        if span <= 0:
+            return
+        g = self._geom1(0, 1, self.Hkv, max(1, max(self.length)))
+        g["num_seqs"] = self.max_seqs
+        gc = hip.geometry(g)
+        seq = torch.tensor(self.length, dtype=torch.int32, device=self.dev)
+        kb_d = torch.from_numpy(kb).to(self.dev)
+        ke_d = torch.from_numpy(ke).to(self.dev)
+        b = hip.Buffers(q=None, k=self.k.data_ptr(), v=self.v.data_ptr(), seq_len=seq.data_ptr(), kv_len=None,
+                        block_table=self.block_table.data_ptr(), block_table_offset=None, tree_mask=None,
+                        tree_base=None, out=None, flags=None)
+        hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(gc), ctypes.byref(b), kb_d.data_ptr(), ke_d.data_ptr(), span,
+                                               ctypes.c_void_p(self.digits.data_ptr()), self.tiles,
+                                               hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
+        self._keep = (seq, kb_d, ke_d)
 
     def _reslice(self, s: int, a: int, e: int) -> None:
         if self.digits is None or e <= a:
@@ -144,21 +191,21 @@ class ExactAttentionBackend:
         self.cache, self.Hq, self.out = cache, num_q_heads, out
         self.alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
 
-    def _run(self, seqs, q, kv_len, tree_mask=None, tree_base=None, digits_slot=None):
-        """One ea_hip_attention call over sequences `seqs` (each row of q is (seq, token, head))."""
+    def _launch(self, seqs, qd, kvl, tree_mask=None, tree_base=None, digits_slot=None):
+        """Enqueue one ea_hip_attention call over sequences `seqs` on torch's current stream.
+        qd: (B, T, Hq, d) int16 device tensor, row (b, t, h) = token t of sequence seqs[b];
+        kvl: (B*T,) int32 device tensor of visible prefix lengths. Returns device (out, flags)."""
         c = self.cache
         torch = c.torch
         lib = hip.load()
-        B, T, Hq, d = q.shape
+        B, T, Hq, d = qd.shape
         lens = [c.length[s] for s in seqs]
         g = c._geom1(seqs[0], T, Hq, max(lens))
         g["num_seqs"] = B
         gc = hip.geometry(g)
-        qd = _dev16(torch, q, c.dev).contiguous()
         out = torch.empty((B, T, Hq, d), dtype=torch.int32 if self.out == "fp32" else torch.int16, device=c.dev)
         flags = torch.empty(B * T * Hq, dtype=torch.uint8, device=c.dev)
         seq = torch.tensor(lens, dtype=torch.int32, device=c.dev)
-        kvl = torch.tensor(np.asarray(kv_len, dtype=np.int32).reshape(-1), device=c.dev)
         off = torch.tensor([s * c.max_pages for s in seqs], dtype=torch.int64, device=c.dev)
         tm = None if tree_mask is None else torch.tensor(np.asarray(tree_mask, dtype=np.uint64).view(np.int64).reshape(-1),
                                                          device=c.dev)
@@ -177,6 +224,18 @@ class ExactAttentionBackend:
                         out=out.data_ptr(), flags=flags.data_ptr())
         hip._check(lib.ea_hip_attention(ctypes.byref(gc), ctypes.byref(b), ctypes.byref(o), ws.data_ptr(), int(nb.value),
                                         hip._stream_ptr(torch)), "ea_hip_attention")
+        # The caching allocator may hand these buffers to later work on this stream only once the
+        # call above has run; keep them referenced until the next launch replaces them.
+        self._keep = (seq, off, tm, tb, ws, kvl, qd)
+        return out, flags
+
+    def _run(self, seqs, q, kv_len, tree_mask=None, tree_base=None, digits_slot=None):
+        """_launch, then the result on the host: (out bits (B, T, Hq, d), flags); flag 2 raises."""
+        c = self.cache
+        torch = c.torch
+        qd = _dev16(torch, q, c.dev).contiguous()
+        kvl = torch.tensor(np.asarray(kv_len, dtype=np.int32).reshape(-1), device=c.dev)
+        out, flags = self._launch(seqs, qd, kvl, tree_mask, tree_base, digits_slot)
         torch.cuda.synchronize()
         res = out.cpu().numpy()
         res = res.view(np.uint32) if self.out == "fp32" else res.view(np.uint16)
@@ -184,6 +243,53 @@ class ExactAttentionBackend:
         if np.any(fl == 2):
             raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
         return res, fl
+
+    def forward(self, query, key, value, seqs, query_lens):
+        """One attention call per layer over a mixed batch, the way vLLM's attention backends are
+        called: `query_lens[i]` new tokens of sequence slot `seqs[i]`, flattened in that order
+        (query (num_tokens, Hq, d), key/value (num_tokens, Hkv, d), bf16 or int16 device tensors).
+        Their K/V are appended to the cache; token j of sequence i attends the cached prefix and
+        tokens 0..j of its chunk (a decode step is a chunk of one token). Enqueued on torch's
+        current stream, no host synchronisation: returns device (out (num_tokens, Hq, d) bf16/fp32
+        bits, flags (num_tokens, Hq) uint8; 0 certified, 1 certified by the exact tier, 2 domain
+        error — check with check_flags)."""
+        c = self.cache
+        torch = c.torch
+        ql = [int(n) for n in query_lens]
+        if len(ql) != len(seqs) or any(n <= 0 for n in ql):
+            raise ValueError("query_lens must give a positive token count per sequence")
+        ntok = sum(ql)
+        if query.shape[0] != ntok or key.shape[0] != ntok or value.shape[0] != ntok:
+            raise ValueError("query/key/value must hold sum(query_lens) tokens")
+        B, T, Hq, d = len(ql), max(ql), query.shape[1], query.shape[2]
+        start = np.concatenate([[0], np.cumsum(ql)])
+        prefix = [c.length[s] for s in seqs]
+        c.append_batch(seqs, ql, key, value)
+        b_of = np.repeat(np.arange(B), ql)
+        j_of = np.arange(ntok) - start[b_of]
+        row = torch.from_numpy(b_of * T + j_of).to(c.dev)
+        kvl_h = np.zeros(B * T, dtype=np.int32)
+        kvl_h[b_of * T + j_of] = np.asarray(prefix)[b_of] + j_of + 1
+        kvl = torch.from_numpy(kvl_h).to(c.dev)
+        q16 = query.view(torch.int16) if query.dtype != torch.int16 else query
+        if T == 1:
+            qd = q16.reshape(B, 1, Hq, d).contiguous()
+        else:
+            qd = torch.zeros((B * T, Hq, d), dtype=torch.int16, device=c.dev)
+            qd.index_copy_(0, row, q16)
+            qd = qd.view(B, T, Hq, d)
+        slots = list(seqs)
+        contiguous = slots == list(range(slots[0], slots[0] + B))
+        out, flags = self._launch(slots, qd, kvl, digits_slot=slots[0] if contiguous else None)
+        if T == 1:
+            return out.view(B, Hq, -1), flags.view(B, Hq)
+        return out.view(B * T, Hq, -1).index_select(0, row), flags.view(B * T, Hq).index_select(0, row)
+
+    @staticmethod
+    def check_flags(flags) -> None:
+        """Synchronise on `flags` (from forward) and raise on a domain error (flag 2)."""
+        if bool((flags == 2).any().item()):
+            raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
 
     def prefill(self, s: int, q, k, v):
         """Append T tokens' K/V to slot s and attend causally: token t sees the prefix and tokens

@@ -85,3 +85,47 @@ def test_serving_session_matches_oracle(gpu):
     grow(s, k, v)
     assert not np.any(fl)
     assert np.array_equal(got, _oracle_rows(q, *hist[s], Lb + 1 + np.arange(T), ab))
+
+
+def test_forward_mixed_batches_match_oracle(gpu):
+    """ExactAttentionBackend.forward on flattened mixed batches: prefill chunks and decode tokens
+    of several sequences in one call (the int8 prefill kernel reading the digit-tile cache when the
+    slots are contiguous, slicing on its own when not), decode-only batches, bf16 tensor inputs."""
+    import torch
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    rng = np.random.default_rng(72)
+    Hq, Hkv, d = 4, 2, 128
+    ab = default_alpha_bits(d)
+    cache = PagedKVCache(num_pages=120, page_size=16, num_kv_heads=Hkv, head_dim=d, max_seqs=4, max_seq_len=512)
+    be = ExactAttentionBackend(cache, Hq, ab)
+    slots = [cache.add_sequence() for _ in range(4)]
+    hist = {s: (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16)) for s in slots}
+    dev = torch.device("cuda")
+
+    def step(seqs, lens, as_bf16=False):
+        n = sum(lens)
+        q, k, v = bf16(rng, (n, Hq, d)), bf16(rng, (n, Hkv, d)), bf16(rng, (n, Hkv, d))
+        conv = (lambda a: torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)) if as_bf16 else \
+            (lambda a: torch.from_numpy(a.view(np.int16)).to(dev))
+        out, fl = be.forward(conv(q), conv(k), conv(v), seqs, lens)
+        be.check_flags(fl)
+        got = out.cpu().numpy().view(np.uint16)
+        assert got.shape == (n, Hq, d) and not fl.any().item(), (seqs, lens)
+        at = 0
+        for s, T in zip(seqs, lens):
+            L = len(hist[s][0])
+            hist[s] = (np.concatenate([hist[s][0], k[at:at + T]]), np.concatenate([hist[s][1], v[at:at + T]]))
+            want = _oracle_rows(q[at:at + T], *hist[s], L + 1 + np.arange(T), ab)
+            assert np.array_equal(got[at:at + T], want), (seqs, lens, s)
+            assert cache.length[s] == L + T
+            at += T
+
+    step([0, 1, 2], [70, 1, 5])           # T = 70: int8 prefill kernel, digits read from the cache
+    step([0, 1, 2], [1, 1, 1])            # decode batch
+    step([2, 0], [66, 3])                 # slots out of order: prefill slices its own tiles
+    step([1, 3], [64, 9], as_bf16=True)   # contiguous again, bf16 tensors, a fresh slot
+    step([0, 1, 2, 3], [1, 1, 1, 1])
+    cache.drop_sequence(1)
+    assert cache.add_sequence() == 1
+    hist[1] = (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16))
+    step([0, 1, 2, 3], [2, 80, 1, 1])     # the re-used slot restarts at key 0

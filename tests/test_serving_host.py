@@ -1,0 +1,88 @@
+"""Host bookkeeping of exactattention_amd.serving.PagedKVCache on the CPU (no digit cache, no HIP
+calls): page allocation from the free list, block tables, batched appends, truncation and slot
+reuse, checked by reading each sequence's logical K/V history back through its block table."""
+
+import numpy as np
+import pytest
+
+from gen import bf16
+
+
+def _history(cache, s):
+    n = cache.length[s]
+    bt = cache.block_table[s].numpy()
+    pos = np.arange(n)
+    pg, sl = bt[pos // cache.P], pos % cache.P
+    k = cache.k.numpy()[pg, sl].view(np.uint16)
+    v = cache.v.numpy()[pg, sl].view(np.uint16)
+    return k, v
+
+
+def test_paged_cache_bookkeeping():
+    from exactattention_amd.serving import PagedKVCache
+    rng = np.random.default_rng(5)
+    Hkv, d = 2, 16
+    c = PagedKVCache(num_pages=20, page_size=8, num_kv_heads=Hkv, head_dim=d, max_seqs=3, max_seq_len=64,
+                     digits=False, device="cpu")
+    a, b = c.add_sequence(), c.add_sequence()
+    want = {a: [np.zeros((0, Hkv, d), np.uint16)] * 2, b: [np.zeros((0, Hkv, d), np.uint16)] * 2}
+    for seqs, counts in (([a], [13]), ([a, b], [3, 17]), ([b, a], [1, 8])):
+        n = sum(counts)
+        k, v = bf16(rng, (n, Hkv, d)), bf16(rng, (n, Hkv, d))
+        c.append_batch(seqs, counts, k, v)
+        at = 0
+        for s, m in zip(seqs, counts):
+            want[s] = [np.concatenate([want[s][0], k[at:at + m]]), np.concatenate([want[s][1], v[at:at + m]])]
+            at += m
+    for s in (a, b):
+        k, v = _history(c, s)
+        assert np.array_equal(k, want[s][0]) and np.array_equal(v, want[s][1])
+        assert len(c.pages[s]) == -(-c.length[s] // c.P)
+    used = len(c.pages[a]) + len(c.pages[b])
+    assert len(c.free) == 20 - used
+    assert not set(c.pages[a]) & set(c.pages[b])
+    # truncation returns whole pages past the new end
+    c.truncate(a, 9)
+    assert c.length[a] == 9 and len(c.pages[a]) == 2 and len(c.free) == 20 - 2 - len(c.pages[b])
+    k, _ = _history(c, a)
+    assert np.array_equal(k, want[a][0][:9])
+    c.append(a, want[a][0][9:12], want[a][1][9:12])
+    assert np.array_equal(_history(c, a)[0], want[a][0][:12])
+    # slot reuse starts empty; pages come back to the free list
+    c.drop_sequence(b)
+    assert c.add_sequence() == b and c.length[b] == 0 and c.pages[b] == []
+    assert len(c.free) == 20 - len(c.pages[a])
+
+
+def test_paged_cache_rejects():
+    from exactattention_amd.serving import PagedKVCache
+    rng = np.random.default_rng(6)
+    with pytest.raises(ValueError):
+        PagedKVCache(num_pages=4, page_size=6, num_kv_heads=1, head_dim=8, max_seqs=1, max_seq_len=8,
+                     digits=False, device="cpu")
+    c = PagedKVCache(num_pages=2, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=12,
+                     digits=False, device="cpu")
+    s = c.add_sequence()
+    with pytest.raises(ValueError):     # past max_seq_len
+        c.append(s, bf16(rng, (13, 1, 8)), bf16(rng, (13, 1, 8)))
+    with pytest.raises(RuntimeError):   # 3 pages needed, 2 exist
+        c.append(s, bf16(rng, (9, 1, 8)), bf16(rng, (9, 1, 8)))
+    with pytest.raises(ValueError):     # a slot twice in one batch
+        c.append_batch([s, s], [1, 1], bf16(rng, (2, 1, 8)), bf16(rng, (2, 1, 8)))
+    with pytest.raises(ValueError):
+        c.truncate(s, c.length[s] + 1)
+    c.add_sequence()
+    with pytest.raises(RuntimeError):
+        c.add_sequence()
+
+
+def test_failed_append_changes_nothing():
+    from exactattention_amd.serving import PagedKVCache
+    rng = np.random.default_rng(7)
+    c = PagedKVCache(num_pages=3, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
+                     digits=False, device="cpu")
+    a, b = c.add_sequence(), c.add_sequence()
+    c.append(a, bf16(rng, (5, 1, 8)), bf16(rng, (5, 1, 8)))
+    with pytest.raises(RuntimeError):   # a needs 1 more page, b 1: only 1 left
+        c.append_batch([a, b], [4, 1], bf16(rng, (5, 1, 8)), bf16(rng, (5, 1, 8)))
+    assert c.length == [5, 0] and len(c.pages[a]) == 2 and c.pages[b] == [] and len(c.free) == 1
