@@ -249,6 +249,67 @@ def kv_digits_line(r: dict, reps: int = 20) -> dict:
             "bit_exact_reading_cache": (hashlib.sha256(out.tobytes()).hexdigest() == golden) if golden else None}
 
 
+def serving_line(prob: dict, ab: int, steps: int, warmup: int = 3) -> dict:
+    """C2 through the serving layer (exactattention_amd.serving): the 32 sequences' first 4095 keys
+    loaded into a PagedKVCache (with its digit-tile cache), then decode steps of one token per
+    sequence through ExactAttentionBackend.forward: the K/V append (device scatter and digit
+    re-slice) plus one certified attention launch, host bookkeeping included. The first step is
+    C2 itself (its bits against the golden hash); later steps grow every sequence by one key."""
+    import torch
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    B, S, P = prob["seq_len"].shape[0], int(prob["seq_len"].max()), prob["geom"]["page_size"]
+    bt = prob["block_table"].astype(np.int64)
+    n = np.arange(S)
+    K = np.stack([prob["k"][bt[b, n // P], n % P] for b in range(B)])   # (B, S, Hkv, d)
+    V = np.stack([prob["v"][bt[b, n // P], n % P] for b in range(B)])
+    q = prob["q"].reshape(B, -1, K.shape[3])
+    Hq, Hkv, d = q.shape[1], K.shape[2], K.shape[3]
+    extra = warmup + steps + 1
+    cache = PagedKVCache(num_pages=B * ((S + extra + P - 1) // P), page_size=P, num_kv_heads=Hkv, head_dim=d,
+                         max_seqs=B, max_seq_len=S + extra, device="cuda:0")
+    be = ExactAttentionBackend(cache, Hq, ab)
+    seqs = [cache.add_sequence() for _ in range(B)]
+    cache.append_batch(seqs, [S - 1] * B, K[:, :S - 1].reshape(-1, Hkv, d), V[:, :S - 1].reshape(-1, Hkv, d))
+    dev = torch.device("cuda:0")
+    qd = torch.from_numpy(q.view(np.int16)).to(dev)
+    kd = torch.from_numpy(np.ascontiguousarray(K[:, S - 1]).view(np.int16)).to(dev)
+    vd = torch.from_numpy(np.ascontiguousarray(V[:, S - 1]).view(np.int16)).to(dev)
+    del K, V
+    ones = [1] * B
+    out, fl = be.forward(qd, kd, vd, seqs, ones)
+    be.check_flags(fl)
+    first = out.cpu().numpy().view(np.uint16)
+    golden = json.load(open(GOLDEN)).get("C2", {}).get("sha256") if os.path.exists(GOLDEN) else None
+    for _ in range(warmup):
+        be.forward(qd, kd, vd, seqs, ones)
+    torch.cuda.synchronize()
+    ev = HipEvents(2)
+    ev.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    t0 = time.perf_counter()
+    ev.h.hipEventRecord(ev.ev[0], stream)
+    for _ in range(steps):
+        out, fl = be.forward(qd, kd, vd, seqs, ones)
+    t_host = time.perf_counter()
+    ev.h.hipEventRecord(ev.ev[1], stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    be.check_flags(fl)
+    gpu_ms = ev.ms(0, 1) / steps
+    ev.close()
+    wall_ms = (t1 - t0) * 1e3 / steps
+    line = {"workload": "C2 decode through serving.ExactAttentionBackend.forward (32 sequences, one token each, "
+                        "K/V append + digit re-slice + attention)",
+            "ms_per_step": round(wall_ms, 5), "gpu_ms_per_step": round(gpu_ms, 5),
+            "host_enqueue_ms_per_step": round((t_host - t0) * 1e3 / steps, 5),
+            "tokens_per_s": round(B / (wall_ms * 1e-3), 1),
+            "kv_len": [S + warmup + 1, S + warmup + steps],
+            "bit_exact_first_step": (hashlib.sha256(first.tobytes()).hexdigest() == golden) if golden else None}
+    del cache, be
+    torch.cuda.empty_cache()
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,7 +318,7 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill measurement")
-    ap.add_argument("--only", choices=("C2", "C3"), default=None,
+    ap.add_argument("--only", choices=("C2", "C3", "serving"), default=None,
                     help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
                     help="after the timed steps, run 5 steps of the phase-clock build and report it")
@@ -283,6 +344,11 @@ def main():
 
     if args.only == "C3":
         print(json.dumps({"prefill": prefill_line(args.steps, args.warmup)}), flush=True)
+        return
+    if args.only == "serving":
+        from exactattention_amd import configs
+        print(json.dumps({"serving": serving_line(configs.c2(), configs.alpha_bits(), args.steps, args.warmup)}),
+              flush=True)
         return
     r = run_config("C2", args.steps, args.warmup, args.splits)
     prob, ab, dp, out, st = r["prob"], r["ab"], r["dp"], r["out"], r["stats"]
@@ -324,6 +390,8 @@ def main():
     torch.cuda.empty_cache()
     if args.only is None and not args.no_prefill:
         line["prefill"] = prefill_line(max(5, min(args.steps, 20)), 2)
+    if args.only is None:
+        line["serving"] = serving_line(prob, ab, max(5, min(args.steps, 20)))
     if args.only is None and not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         cb, cres = cpu_baseline(prob, ab, threads)

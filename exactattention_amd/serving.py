@@ -29,6 +29,59 @@ from .formats import ExactAttentionDomainError, fp32_bits
 TILE = 64  # keys per digit tile
 
 
+class _Stager:
+    """Small host-to-device uploads (indices, lengths, offsets) in one asynchronous copy per call
+    through a ring of pinned buffers. A host buffer is written again only after the event of its
+    last copy has completed, so the host waits only when it runs a whole ring ahead of the GPU.
+    The device buffers are reused in stream order: the copy that refills one is enqueued after the
+    kernels that read its previous contents."""
+
+    def __init__(self, torch, dev, depth: int = 8, nbytes: int = 1 << 16):
+        self.torch, self.dev, self.depth = torch, dev, depth
+        self.cuda = dev.type == "cuda"
+        self.host, self.devb, self.ev = [None] * depth, [None] * depth, [None] * depth
+        self.cap = [0] * depth
+        self.nbytes = nbytes
+        self.i = 0
+
+    def put(self, *arrays):
+        """Device tensors holding copies of the numpy arrays (same dtypes and shapes)."""
+        torch = self.torch
+        arrays = [np.ascontiguousarray(a) for a in arrays]
+        if not self.cuda:
+            return [torch.from_numpy(a.copy()) for a in arrays]
+        offs, at = [], 0
+        for a in arrays:
+            offs.append(at)
+            at += (a.nbytes + 255) // 256 * 256
+        i = self.i
+        self.i = (i + 1) % self.depth
+        if self.ev[i] is not None:
+            self.ev[i].synchronize()
+        if self.cap[i] < at:
+            self.cap[i] = max(at, self.nbytes)
+            self.host[i] = torch.empty(self.cap[i], dtype=torch.uint8, pin_memory=True)
+            self.devb[i] = torch.empty(self.cap[i], dtype=torch.uint8, device=self.dev)
+        h = self.host[i].numpy()
+        for a, o in zip(arrays, offs):
+            h[o:o + a.nbytes] = a.view(np.uint8).reshape(-1)
+        d = self.devb[i]
+        d[:at].copy_(self.host[i][:at], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.ev[i] = ev
+        return [d[o:o + a.nbytes].view(_TORCH_DTYPE[a.dtype.str[1:]]).view(a.shape) for a, o in zip(arrays, offs)]
+
+
+_TORCH_DTYPE = {}
+
+
+def _torch_dtypes(torch):
+    if not _TORCH_DTYPE:
+        _TORCH_DTYPE.update({"i4": torch.int32, "i8": torch.int64, "u1": torch.uint8, "i2": torch.int16})
+    return _TORCH_DTYPE
+
+
 class PagedKVCache:
     def __init__(self, num_pages: int, page_size: int, num_kv_heads: int, head_dim: int, max_seqs: int,
                  max_seq_len: int, digits: bool = True, device: str = "cuda"):
@@ -43,6 +96,9 @@ class PagedKVCache:
         self.k = torch.zeros((num_pages, page_size, num_kv_heads, head_dim), dtype=torch.int16, device=self.dev)
         self.v = torch.zeros_like(self.k)
         self.block_table = torch.zeros((max_seqs, self.max_pages), dtype=torch.int32, device=self.dev)
+        self.bt_host = np.zeros((max_seqs, self.max_pages), dtype=np.int32)
+        _torch_dtypes(torch)
+        self.stage = _Stager(torch, self.dev)
         self.free = list(range(num_pages))[::-1]
         self.pages = [[] for _ in range(max_seqs)]
         self.length = [0] * max_seqs
@@ -89,6 +145,15 @@ class PagedKVCache:
         """Append counts[i] keys to slot seqs[i] for every i, the keys flattened in that order
         (k_bits, v_bits: (sum(counts), Hkv, d)); one device scatter for the batch, then one
         digit re-slice over every slot the batch touched."""
+        plan = self._plan_append(seqs, counts, k_bits, v_bits)
+        if plan is not None:
+            self._apply_append(plan, self.stage.put(*plan["arrays"]))
+
+    def _plan_append(self, seqs, counts, k_bits, v_bits):
+        """Host half of an append: checks, page allocation, block-table mirror and lengths. Returns
+        None for an empty append, else a plan whose "arrays" the caller uploads (in one staged copy
+        with its own arrays appended) and hands, as device tensors in the same order, to
+        _apply_append."""
         torch = self.torch
         k_new = _dev16(torch, k_bits, self.dev)
         v_new = _dev16(torch, v_bits, self.dev)
@@ -98,32 +163,48 @@ class PagedKVCache:
         if len(set(seqs)) != len(seqs):
             raise ValueError("a slot may appear once per batch")
         if sum(counts) == 0:
-            return
-        need = []
-        for s, n in zip(seqs, counts):
-            if self.length[s] + n > self.max_seq_len:
-                raise ValueError("sequence longer than the cache's max_seq_len")
-            need.append(max(0, (self.length[s] + n + self.P - 1) // self.P - len(self.pages[s])))
-        if sum(need) > len(self.free):
+            return None
+        sa = np.asarray(seqs, dtype=np.int64)
+        cnt = np.asarray(counts, dtype=np.int64)
+        L = np.asarray(self.length, dtype=np.int64)[sa]
+        if np.any(L + cnt > self.max_seq_len):
+            raise ValueError("sequence longer than the cache's max_seq_len")
+        have = np.asarray([len(self.pages[s]) for s in seqs], dtype=np.int64)
+        need = np.maximum(0, (L + cnt + self.P - 1) // self.P - have)
+        if int(need.sum()) > len(self.free):
             raise RuntimeError("out of pages")
-        pg, sl, begin, end = [], [], [], []
-        for s, n, m in zip(seqs, counts, need):
-            L = self.length[s]
-            self.pages[s].extend(self.free.pop() for _ in range(m))
-            pos = np.arange(L, L + n)
-            pg.append(np.asarray(self.pages[s], dtype=np.int64)[pos // self.P])
-            sl.append(pos % self.P)
-            begin.append(L)
-            end.append(L + n)
-        for s in seqs:
-            self.block_table[s, :len(self.pages[s])] = torch.tensor(self.pages[s], dtype=torch.int32, device=self.dev)
-        pg_d = torch.from_numpy(np.concatenate(pg)).to(self.dev)
-        sl_d = torch.from_numpy(np.concatenate(sl).astype(np.int64)).to(self.dev)
-        self.k[pg_d, sl_d] = k_new
-        self.v[pg_d, sl_d] = v_new
-        for s, e in zip(seqs, end):
+        grown = []
+        for i in np.flatnonzero(need):
+            s = seqs[i]
+            self.pages[s].extend(self.free.pop() for _ in range(int(need[i])))
+            self.bt_host[s, :len(self.pages[s])] = self.pages[s]
+            grown.append(s)
+        b_of = np.repeat(np.arange(len(seqs)), cnt)
+        pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
+        idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
+        kb = np.zeros(self.max_seqs, dtype=np.int32)
+        ke = np.zeros(self.max_seqs, dtype=np.int32)
+        kb[sa], ke[sa] = L, L + cnt
+        for s, e in zip(seqs, (L + cnt).tolist()):
             self.length[s] = e
-        self._reslice_slots(list(seqs), begin, end)
+        arrays = [idx]
+        if grown:
+            arrays += [np.asarray(grown, dtype=np.int64), self.bt_host[grown]]
+        if self.digits is not None:
+            arrays += [np.asarray(self.length, dtype=np.int32), kb, ke]
+        return {"k": k_new, "v": v_new, "grown": bool(grown), "span": max(counts), "arrays": arrays}
+
+    def _apply_append(self, plan, dev, stream=None) -> None:
+        """Device half of an append: block-table rows, the K/V scatter, the digit re-slice."""
+        idx_d, i = dev[0], 1
+        if plan["grown"]:
+            self.block_table.index_copy_(0, dev[1], dev[2])
+            i = 3
+        H, d = self.Hkv, self.d
+        self.k.view(-1, H, d).index_copy_(0, idx_d, plan["k"].reshape(-1, H, d))
+        self.v.view(-1, H, d).index_copy_(0, idx_d, plan["v"].reshape(-1, H, d))
+        if self.digits is not None:
+            self._reslice_all(dev[i], dev[i + 1], dev[i + 2], plan["span"], stream)
 
     def truncate(self, s: int, length: int) -> None:
         """Drop the keys at or past `length` (rejected draft nodes); the tile holding the new end is
@@ -137,33 +218,20 @@ class PagedKVCache:
         if length % TILE:
             self._reslice(s, length - 1, length)
 
-    def _reslice_slots(self, seqs, begin, end) -> None:
-        """Re-slice keys begin[i]..end[i]-1 of slot seqs[i]: one update over all slots, where the
-        untouched slots get an empty range (their blocks exit at once)."""
-        if self.digits is None:
-            return
+    def _reslice_all(self, seq_d, kb_d, ke_d, span: int, stream=None) -> None:
+        """Re-slice keys kb[s]..ke[s]-1 of every slot s (device int32 vectors over all max_seqs
+        slots, seq_d their lengths): one update, where slots with an empty range exit at once."""
         torch = self.torch
         lib = hip.load()
-        kb = np.zeros(self.max_seqs, dtype=np.int32)
-        ke = np.zeros(self.max_seqs, dtype=np.int32)
-        kb[list(seqs)] = begin
-        ke[list(seqs)] = end
-        span = int(max(e - a for a, e in zip(begin, end)))
-        if span <= 0:
-            return
         g = self._geom1(0, 1, self.Hkv, max(1, max(self.length)))
         g["num_seqs"] = self.max_seqs
         gc = hip.geometry(g)
-        seq = torch.tensor(self.length, dtype=torch.int32, device=self.dev)
-        kb_d = torch.from_numpy(kb).to(self.dev)
-        ke_d = torch.from_numpy(ke).to(self.dev)
-        b = hip.Buffers(q=None, k=self.k.data_ptr(), v=self.v.data_ptr(), seq_len=seq.data_ptr(), kv_len=None,
+        b = hip.Buffers(q=None, k=self.k.data_ptr(), v=self.v.data_ptr(), seq_len=seq_d.data_ptr(), kv_len=None,
                         block_table=self.block_table.data_ptr(), block_table_offset=None, tree_mask=None,
                         tree_base=None, out=None, flags=None)
         hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(gc), ctypes.byref(b), kb_d.data_ptr(), ke_d.data_ptr(), span,
                                                ctypes.c_void_p(self.digits.data_ptr()), self.tiles,
-                                               hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
-        self._keep = (seq, kb_d, ke_d)
+                                               stream or hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
 
     def _reslice(self, s: int, a: int, e: int) -> None:
         if self.digits is None or e <= a:
@@ -171,17 +239,14 @@ class PagedKVCache:
         torch = self.torch
         lib = hip.load()
         g = hip.geometry(self._geom1(s, 1, self.Hkv, self.length[s]))
-        seq = torch.tensor([self.length[s]], dtype=torch.int32, device=self.dev)
-        off = torch.tensor([s * self.max_pages], dtype=torch.int64, device=self.dev)
-        kb = torch.tensor([a], dtype=torch.int32, device=self.dev)
-        ke = torch.tensor([e], dtype=torch.int32, device=self.dev)
+        seq, kb, ke, off = self.stage.put(np.array([self.length[s]], dtype=np.int32), np.array([a], dtype=np.int32),
+                                          np.array([e], dtype=np.int32), np.array([s * self.max_pages], dtype=np.int64))
         b = hip.Buffers(q=None, k=self.k.data_ptr(), v=self.v.data_ptr(), seq_len=seq.data_ptr(), kv_len=None,
                         block_table=self.block_table.data_ptr(), block_table_offset=off.data_ptr(), tree_mask=None,
                         tree_base=None, out=None, flags=None)
         hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(g), ctypes.byref(b), kb.data_ptr(), ke.data_ptr(), e - a,
                                                ctypes.c_void_p(self._digit_base(s)), self.tiles,
                                                hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
-        self._keep = (seq, off, kb, ke)  # alive until the stream has run the update
 
 
 class ExactAttentionBackend:
@@ -190,11 +255,14 @@ class ExactAttentionBackend:
     def __init__(self, cache: PagedKVCache, num_q_heads: int, alpha, out: str = "bf16"):
         self.cache, self.Hq, self.out = cache, num_q_heads, out
         self.alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
+        self.ws = None
 
-    def _launch(self, seqs, qd, kvl, tree_mask=None, tree_base=None, digits_slot=None):
+    def _launch(self, seqs, qd, kvl, tree_mask=None, tree_base=None, digits_slot=None, staged=None, stream=None):
         """Enqueue one ea_hip_attention call over sequences `seqs` on torch's current stream.
         qd: (B, T, Hq, d) int16 device tensor, row (b, t, h) = token t of sequence seqs[b];
-        kvl: (B*T,) int32 device tensor of visible prefix lengths. Returns device (out, flags)."""
+        kvl: (B*T,) int32 device tensor of visible prefix lengths; staged: the device seq_len and
+        block-table offset vectors of `seqs` when the caller uploaded them already. Returns device
+        (out, flags)."""
         c = self.cache
         torch = c.torch
         lib = hip.load()
@@ -205,11 +273,18 @@ class ExactAttentionBackend:
         gc = hip.geometry(g)
         out = torch.empty((B, T, Hq, d), dtype=torch.int32 if self.out == "fp32" else torch.int16, device=c.dev)
         flags = torch.empty(B * T * Hq, dtype=torch.uint8, device=c.dev)
-        seq = torch.tensor(lens, dtype=torch.int32, device=c.dev)
-        off = torch.tensor([s * c.max_pages for s in seqs], dtype=torch.int64, device=c.dev)
-        tm = None if tree_mask is None else torch.tensor(np.asarray(tree_mask, dtype=np.uint64).view(np.int64).reshape(-1),
-                                                         device=c.dev)
-        tb = None if tree_base is None else torch.tensor(np.asarray(tree_base, dtype=np.int32), device=c.dev)
+        tm = tb = None
+        if staged is not None:
+            seq, off = staged
+        else:
+            up = [np.asarray(lens, dtype=np.int32), np.asarray([s * c.max_pages for s in seqs], dtype=np.int64)]
+            if tree_mask is not None:
+                up += [np.asarray(tree_mask, dtype=np.uint64).view(np.int64).reshape(-1),
+                       np.asarray(tree_base, dtype=np.int32)]
+            dv = c.stage.put(*up)
+            seq, off = dv[0], dv[1]
+            if tree_mask is not None:
+                tm, tb = dv[2], dv[3]
         o = hip.Options(alpha_bits=self.alpha_bits, out_fp32=int(self.out == "fp32"), splits=0, tier2=1)
         if digits_slot is not None and c.digits is not None:
             o.kv_digits = ctypes.c_void_p(c._digit_base(digits_slot))
@@ -217,16 +292,15 @@ class ExactAttentionBackend:
         nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
         hip._check(lib.ea_hip_workspace_size(ctypes.byref(gc), ctypes.byref(o), ctypes.byref(nb), ctypes.byref(ns)),
                    "ea_hip_workspace_size")
-        ws = torch.empty(max(int(nb.value), 256), dtype=torch.uint8, device=c.dev)
+        if self.ws is None or self.ws.numel() < int(nb.value):
+            self.ws = torch.empty(max(int(nb.value), 1 << 20), dtype=torch.uint8, device=c.dev)
+        ws = self.ws
         b = hip.Buffers(q=qd.data_ptr(), k=c.k.data_ptr(), v=c.v.data_ptr(), seq_len=seq.data_ptr(),
                         kv_len=kvl.data_ptr(), block_table=c.block_table.data_ptr(), block_table_offset=off.data_ptr(),
                         tree_mask=None if tm is None else tm.data_ptr(), tree_base=None if tb is None else tb.data_ptr(),
                         out=out.data_ptr(), flags=flags.data_ptr())
         hip._check(lib.ea_hip_attention(ctypes.byref(gc), ctypes.byref(b), ctypes.byref(o), ws.data_ptr(), int(nb.value),
-                                        hip._stream_ptr(torch)), "ea_hip_attention")
-        # The caching allocator may hand these buffers to later work on this stream only once the
-        # call above has run; keep them referenced until the next launch replaces them.
-        self._keep = (seq, off, tm, tb, ws, kvl, qd)
+                                        stream or hip._stream_ptr(torch)), "ea_hip_attention")
         return out, flags
 
     def _run(self, seqs, q, kv_len, tree_mask=None, tree_base=None, digits_slot=None):
@@ -234,7 +308,7 @@ class ExactAttentionBackend:
         c = self.cache
         torch = c.torch
         qd = _dev16(torch, q, c.dev).contiguous()
-        kvl = torch.tensor(np.asarray(kv_len, dtype=np.int32).reshape(-1), device=c.dev)
+        (kvl,) = c.stage.put(np.asarray(kv_len, dtype=np.int32).reshape(-1))
         out, flags = self._launch(seqs, qd, kvl, tree_mask, tree_base, digits_slot)
         torch.cuda.synchronize()
         res = out.cpu().numpy()
@@ -264,13 +338,21 @@ class ExactAttentionBackend:
         B, T, Hq, d = len(ql), max(ql), query.shape[1], query.shape[2]
         start = np.concatenate([[0], np.cumsum(ql)])
         prefix = [c.length[s] for s in seqs]
-        c.append_batch(seqs, ql, key, value)
+        plan = c._plan_append(seqs, ql, key, value)
         b_of = np.repeat(np.arange(B), ql)
         j_of = np.arange(ntok) - start[b_of]
-        row = torch.from_numpy(b_of * T + j_of).to(c.dev)
         kvl_h = np.zeros(B * T, dtype=np.int32)
         kvl_h[b_of * T + j_of] = np.asarray(prefix)[b_of] + j_of + 1
-        kvl = torch.from_numpy(kvl_h).to(c.dev)
+        mine = [kvl_h, np.asarray([c.length[s] for s in seqs], dtype=np.int32),
+                np.asarray([s * c.max_pages for s in seqs], dtype=np.int64)]
+        if T > 1:
+            mine.append((b_of * T + j_of).astype(np.int64))
+        n_app = len(plan["arrays"])
+        dev = c.stage.put(*plan["arrays"], *mine)
+        st = hip._stream_ptr(torch)
+        c._apply_append(plan, dev[:n_app], st)
+        kvl, staged = dev[n_app], (dev[n_app + 1], dev[n_app + 2])
+        row = dev[n_app + 3] if T > 1 else None
         q16 = query.view(torch.int16) if query.dtype != torch.int16 else query
         if T == 1:
             qd = q16.reshape(B, 1, Hq, d).contiguous()
@@ -280,7 +362,8 @@ class ExactAttentionBackend:
             qd = qd.view(B, T, Hq, d)
         slots = list(seqs)
         contiguous = slots == list(range(slots[0], slots[0] + B))
-        out, flags = self._launch(slots, qd, kvl, digits_slot=slots[0] if contiguous else None)
+        out, flags = self._launch(slots, qd, kvl, digits_slot=slots[0] if contiguous else None, staged=staged,
+                                  stream=st)
         if T == 1:
             return out.view(B, Hq, -1), flags.view(B, Hq)
         return out.view(B * T, Hq, -1).index_select(0, row), flags.view(B * T, Hq).index_select(0, row)
