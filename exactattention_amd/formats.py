@@ -89,5 +89,30 @@ def default_alpha_bits(d: int) -> int:
         W *= 2
 
 
+@lru_cache(maxsize=None)
+def alpha_bits_for(scaling: float) -> int:
+    """fp32 bits of RN_fp32(scaling / ln 2) for a positive float64 logit scale (an attention
+    module's `scaling`), decided by integer enclosures of ln 2 with doubling precision
+    (scripts/validate_model.py:35-40 rounds an mpmath quotient at 200 bits)."""
+    scaling = float(scaling)
+    if not (scaling > 0.0 and math.isfinite(scaling)):
+        raise ValueError("scaling must be positive and finite")
+    m, e = math.frexp(scaling)
+    M, E = int(m * (1 << 53)), e - 53          # scaling = M * 2^E exactly
+    W = 80
+    while True:
+        L_lo, L_hi = _ln2_interval(W)          # L_lo / 2^W <= ln 2 <= L_hi / 2^W
+        sh = E + W                             # scaling / ln 2 = M 2^(E+W) / L
+        num = M << sh if sh >= 0 else M
+        scale = 1 if sh >= 0 else 1 << -sh
+        lo = _rn32_ratio(num, L_hi * scale)
+        hi = _rn32_ratio(num, L_lo * scale)
+        if lo == hi:
+            if not 0 < (lo >> 23) < 255:
+                raise ValueError("scaling / ln 2 is outside the normal fp32 range")
+            return lo
+        W *= 2
+
+
 def default_alpha(d: int) -> np.float32:
     return np.array([default_alpha_bits(d)], dtype=np.uint32).view(np.float32)[0]

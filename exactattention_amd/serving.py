@@ -24,7 +24,7 @@ import ctypes
 import numpy as np
 
 from . import hip
-from .formats import ExactAttentionDomainError, fp32_bits
+from .formats import ExactAttentionDomainError, alpha_bits_for, fp32_bits
 
 TILE = 64  # keys per digit tile
 
@@ -422,6 +422,71 @@ class ExactAttentionBackend:
         if len(path):
             idx = np.asarray(path)
             self.cache.append(s, np.asarray(k)[idx], np.asarray(v)[idx])
+
+
+_HF_WS = {}
+
+
+def hf_attention(module, query, key, value, attention_mask=None, scaling=None, dropout=0.0, **kwargs):
+    """ExactAttention as a transformers attention function (register it with
+    `transformers.AttentionInterface.register("exact", hf_attention)` or `register_hf()`), the GPU
+    drop-in for the reference demo's `exact_attention` (scripts/spec_decode_demo.py:57-73):
+    query (B, H, ql, D), key/value (B, Hkv, kl, D) bf16 CUDA tensors holding the whole cache,
+    causal with the queries at the end of the key range (query t attends keys 0 .. kl-ql+t);
+    `attention_mask` is not read, as in the reference (batches without padding). alpha =
+    RN_fp32(scaling / ln 2), scaling defaulting to `module.scaling`. One ea_hip_attention launch
+    straight on the tensors' strides (no copies); returns (out (B, ql, H, D) bf16, None). Raises
+    on non-finite input or fp32 logit overflow, like the reference's kernels (this waits for
+    the launch)."""
+    import torch
+    if dropout:
+        raise ValueError("dropout is not part of ExactAttention")
+    if kwargs.get("sliding_window"):
+        raise ValueError("sliding-window attention is not supported")
+    B, H, ql, D = query.shape
+    Hkv, kl = key.shape[1], key.shape[2]
+    if key.shape != value.shape[:3] + (D,) or key.shape[0] != B or key.shape[3] != D:
+        raise ValueError("query/key/value shapes do not match")
+    if ql > kl:
+        raise ValueError("more queries than keys")
+    for t in (query, key, value):
+        if t.dtype != torch.bfloat16 or t.device.type != "cuda" or t.stride(3) != 1:
+            raise ValueError("query/key/value must be bf16 CUDA tensors with a contiguous last dimension")
+    ab = alpha_bits_for(float(scaling if scaling is not None else module.scaling))
+    dev = query.device
+    out = torch.empty((B, ql, H, D), dtype=torch.bfloat16, device=dev)
+    flags = torch.empty(B * ql * H, dtype=torch.uint8, device=dev)
+    lens = torch.full((B,), kl, dtype=torch.int32, device=dev)
+    kvl = (torch.arange(kl - ql + 1, kl + 1, dtype=torch.int32, device=dev)).repeat(B)
+    g = hip.geometry(dict(num_seqs=B, num_tokens=ql, num_q_heads=H, num_kv_heads=Hkv, head_dim=D, head_dim_v=D,
+                          q_seq_stride=query.stride(0), q_tok_stride=query.stride(2), q_head_stride=query.stride(1),
+                          o_seq_stride=ql * H * D, o_tok_stride=H * D, o_head_stride=D,
+                          k_page_stride=key.stride(0), k_slot_stride=key.stride(2), k_head_stride=key.stride(1),
+                          v_page_stride=value.stride(0), v_slot_stride=value.stride(2), v_head_stride=value.stride(1),
+                          page_size=1, block_table_stride=0, max_seq_len=kl))
+    o = hip.Options(alpha_bits=ab, out_fp32=0, splits=0, tier2=1)
+    lib = hip.load()
+    nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
+    hip._check(lib.ea_hip_workspace_size(ctypes.byref(g), ctypes.byref(o), ctypes.byref(nb), ctypes.byref(ns)),
+               "ea_hip_workspace_size")
+    ws = _HF_WS.get(dev)
+    if ws is None or ws.numel() < int(nb.value):
+        ws = _HF_WS[dev] = torch.empty(max(int(nb.value), 1 << 20), dtype=torch.uint8, device=dev)
+    b = hip.Buffers(q=query.data_ptr(), k=key.data_ptr(), v=value.data_ptr(), seq_len=lens.data_ptr(),
+                    kv_len=kvl.data_ptr(), block_table=None, block_table_offset=None, tree_mask=None, tree_base=None,
+                    out=out.data_ptr(), flags=flags.data_ptr())
+    hip._check(lib.ea_hip_attention(ctypes.byref(g), ctypes.byref(b), ctypes.byref(o), ws.data_ptr(), int(nb.value),
+                                    hip._stream_ptr(torch)), "ea_hip_attention")
+    if bool((flags == 2).any().item()):
+        raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
+    return out, None
+
+
+def register_hf(name: str = "exact") -> str:
+    """Register hf_attention with transformers under `name` (attn_implementation=name)."""
+    from transformers import AttentionInterface
+    AttentionInterface.register(name, hf_attention)
+    return name
 
 
 def _dev16(torch, x, dev):

@@ -129,3 +129,82 @@ def test_forward_mixed_batches_match_oracle(gpu):
     assert cache.add_sequence() == 1
     hist[1] = (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16))
     step([0, 1, 2, 3], [2, 80, 1, 1])     # the re-used slot restarts at key 0
+
+
+@pytest.mark.parametrize("B,H,Hkv,ql,kl,transposed", [(2, 4, 2, 5, 70, False), (1, 4, 2, 96, 96, True),
+                                                    (1, 2, 2, 1, 300, False), (3, 4, 1, 64, 130, True)])
+def test_hf_attention_matches_oracle(gpu, B, H, Hkv, ql, kl, transposed):
+    """serving.hf_attention (the transformers attention-function drop-in) against the oracle:
+    queries at the end of the key range, GQA, decode (ql = 1), the int8 prefill path (ql >= 64),
+    and queries given as the transposed (B, ql, H, D) -> (B, H, ql, D) views transformers makes."""
+    import torch
+    from exactattention_amd.formats import alpha_bits_for
+    from exactattention_amd.serving import hf_attention
+    rng = np.random.default_rng(100 + ql)
+    D = 128
+    q, k, v = bf16(rng, (B, ql, H, D)), bf16(rng, (B, Hkv, kl, D)), bf16(rng, (B, Hkv, kl, D))
+    dev = torch.device("cuda")
+    tq = torch.from_numpy(q.view(np.int16)).to(dev).view(torch.bfloat16)
+    tq = tq.transpose(1, 2) if transposed else tq.transpose(1, 2).contiguous()
+    tk = torch.from_numpy(k.view(np.int16)).to(dev).view(torch.bfloat16)
+    tv = torch.from_numpy(v.view(np.int16)).to(dev).view(torch.bfloat16)
+    scaling = D ** -0.5
+
+    class M:
+        pass
+    mod = M()
+    mod.scaling = scaling
+    out, none = hf_attention(mod, tq, tk, tv, None)
+    assert none is None and out.shape == (B, ql, H, D)
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    ab = alpha_bits_for(scaling)
+    for b in range(B):
+        want = _oracle_rows(q[b], k[b].transpose(1, 0, 2), v[b].transpose(1, 0, 2), kl - ql + 1 + np.arange(ql), ab)
+        assert np.array_equal(got[b], want), b
+
+
+def test_hf_model_runs_through_exact_attention(gpu):
+    """A small random-init Qwen3 (2 layers, head_dim 128, GQA 2:1) in bf16 on the GPU with
+    attn_implementation set to the registered hf_attention: a 70-token prompt and 3 cached decode
+    steps. Every attention call's output is checked against the oracle on the same q/K/V, and a
+    second run gives the same logits bit for bit."""
+    import torch
+    from transformers import AttentionInterface, DynamicCache, Qwen3Config, Qwen3ForCausalLM
+    from exactattention_amd.formats import alpha_bits_for
+    from exactattention_amd.serving import hf_attention
+    calls = []
+
+    def checked(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
+        out, _ = hf_attention(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kw)
+        to16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        calls.append((to16(query), to16(key), to16(value), to16(out), scaling if scaling is not None else module.scaling))
+        return out, None
+
+    AttentionInterface.register("exact_checked", checked)
+    cfg = Qwen3Config(vocab_size=97, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=2, num_key_value_heads=1, head_dim=128, max_position_embeddings=256)
+    cfg._attn_implementation = "exact_checked"
+    torch.manual_seed(0)
+    model = Qwen3ForCausalLM(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, 97, (1, 70), generator=torch.Generator().manual_seed(1)).cuda()
+
+    def run():
+        cache = DynamicCache()
+        with torch.no_grad():
+            lg = [model(input_ids=ids, past_key_values=cache, use_cache=True).logits[0, -1]]
+            for _ in range(3):
+                nxt = lg[-1].argmax().view(1, 1)
+                lg.append(model(input_ids=nxt, past_key_values=cache, use_cache=True).logits[0, -1])
+        return torch.stack(lg).float().cpu().numpy()
+
+    a = run()
+    n_calls = len(calls)
+    b = run()
+    assert np.array_equal(a, b) and np.all(np.isfinite(a))
+    assert n_calls == 2 * 4
+    for (q, k, v, out, scaling) in calls[:n_calls]:
+        B, H, ql, D = q.shape
+        kl = k.shape[2]
+        want = _oracle_rows(q[0].transpose(1, 0, 2), k[0].transpose(1, 0, 2), v[0].transpose(1, 0, 2),
+                            kl - ql + 1 + np.arange(ql), alpha_bits_for(scaling))
+        assert np.array_equal(out[0], want), (ql, kl)

@@ -86,3 +86,28 @@ def test_failed_append_changes_nothing():
     with pytest.raises(RuntimeError):   # a needs 1 more page, b 1: only 1 left
         c.append_batch([a, b], [4, 1], bf16(rng, (5, 1, 8)), bf16(rng, (5, 1, 8)))
     assert c.length == [5, 0] and len(c.pages[a]) == 2 and c.pages[b] == [] and len(c.free) == 1
+
+
+def test_alpha_bits_for_scaling():
+    """alpha = RN_fp32(scaling / ln 2): the reference's fixture value for Qwen3 heads (scaling
+    128^-0.5), mpmath at 200 bits (the reference's method) on seeded scalings, and the closed
+    form default_alpha_bits(d) for scaling = 1/sqrt(d) where sqrt(d) is exact."""
+    import os
+    import mpmath
+    from exactattention_amd.formats import alpha_bits_for, default_alpha_bits
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "qwen3_0.6b_heads.npz"))
+    assert alpha_bits_for(128 ** -0.5) == int(z["alpha_0_0"].view(np.uint32)) == int(z["alpha_27_11"].view(np.uint32))
+    for d in (1, 4, 16, 64, 256, 1024):
+        assert alpha_bits_for(1.0 / np.sqrt(d)) == default_alpha_bits(d)
+    rng = np.random.default_rng(9)
+    for x in np.concatenate([rng.uniform(0.01, 4.0, 200), 2.0 ** rng.integers(-60, 60, 20)]):
+        with mpmath.workprec(200):
+            # RN to fp32 decided in mpmath: of the fp32 values around the quotient (irrational, so
+            # never a tie), the nearest
+            q = mpmath.mpf(float(x)) / mpmath.log(2)
+            lo = np.float32(float(q))
+            cand = [np.nextafter(lo, np.float32(0)), lo, np.nextafter(lo, np.float32(np.inf))]
+            want = min(cand, key=lambda c: abs(mpmath.mpf(float(c)) - q))
+        assert alpha_bits_for(float(x)) == int(np.float32(want).view(np.uint32)), x
+    with pytest.raises(ValueError):
+        alpha_bits_for(0.0)
