@@ -33,11 +33,18 @@ namespace {
 
 constexpr int DT = 64;  // keys per tile = lanes
 
+// Rows [0, RA) of a block are certified by wave A, rows [RA, RB) by wave B (from scores and bounds
+// wave A hands over), so the two waves' instruction streams per tile are about equally long.
+template <int RB>
+constexpr int rows_a() { return (RB + 1) / 2; }
+
 template <int RB>
 struct DecodeSmem {
-    uint4 K[2][DT * 16];   // 2 x 16 KB K tiles; reused by the epilogue reduction
-    double w[2][DT][RB];   // weights of a tile, [key][row], double-buffered between the waves
-    double sc[2][RB];      // per-row rescale of the running P.V sums before that tile
+    static constexpr int RA = rows_a<RB>(), RBB = RB - RA > 0 ? RB - RA : 1;
+    uint4 K[2][DT * 16];     // 2 x 16 KB K tiles; reused by the epilogue reduction
+    double w[2][DT][RA];     // wave A's weights of a tile, [key][row], double-buffered between the waves
+    double2 sb[2][DT][RBB];  // (score, error bound) of wave B's rows; wave B overwrites .x with the weight
+    double sc[2][RA];        // rescale of wave A's rows' running P.V sums before that tile
     double T1[256], T2[256];
 };
 
@@ -176,18 +183,103 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
     // Both roles run ntiles + 1 loop iterations with one barrier each (and the prologue barrier):
     // iteration it has wave A publish the weights of tile it, wave B consume those of tile it - 1.
     const int role = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    constexpr int RA = rows_a<RB>();
 
-    if (role == 0) {
-        // ============ wave A: K tiles, scores, certified logits and weights
-        int Rrun[RB];
-        double zacc[RB];
-        int nvis[RB];
+    // Per-row certification state; each wave keeps the rows it certifies (A: [0, RA), B: [RA, RB)).
+    int Rrun[RB];
+    double zacc[RB];
+    int nvis[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        Rrun[r] = INT_MIN;
+        zacc[r] = 0.0;
+        nvis[r] = 0;
+    }
+    // Certified weight of row r at key n = lane's key, from the fp64 score s and its error bound
+    // del: t = RN32(alpha s) certified from the interval (pairs it cannot decide are redone exactly
+    // by `exact`, which returns the TwoSum sum, its error sum and the sum of |errors| of the
+    // products of q row r and key n), w = RN24(2^t). Advances the row's running reference exponent
+    // (a DPP wave max), Z sum, visible count and flag; returns the weight scaled to the reference
+    // exponent, and in *fout the wave-uniform rescale of the row's running sums.
+    auto certify = [&](int r, int n, double s, double del, auto&& exact, double* fout) __attribute__((always_inline)) {
+        const int ti = n - tb;
+        const bool vis = (n < k1) && (n < kvl[r] || (ti >= 0 && ti < 64 && ((tmk[r] >> ti) & 1)));
+        int32_t M = 1 << 23, E = -23;
+        int why = 0;  // 1 score not certified, 2 weight not certified, 3 weight out of range
+        bool slow = false;
+        if (vis && !rflag[r]) {
+            uint32_t tbits = 0;
+            int ls = isfinite(s) ? logit_cert(alpha, s, 0.0, del, &tbits) : 3;
+            if (ls == 3 && isfinite(s)) {
+                // exact path: every product separately, TwoSum-accumulated
+                slow = true;
+                double ss = 0.0, es = 0.0, ea = 0.0;
+                exact(r, n, ss, es, ea);
+                ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1 : logit_cert(alpha, ss, es, ea * 0x1p-44, &tbits);
+            }
+            if (ls == 2 || ls == 3) {
+                why = 1;
+            } else if (ls == 0) {
+                int ws = weight_f64(tbits, S.T1, S.T2, &M, &E);
+                if (ws) {
+                    int32_t M2 = 0;
+                    int64_t E2 = 0;
+                    if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
+                        M = M2;
+                        E = (int32_t)E2;
+                    } else {
+                        why = 2;
+                    }
+                }
+            }
+        }
+        if (P.stats) {
+            const uint64_t b1 = __ballot(why == 1), b2 = __ballot(why == 2), b3 = __ballot(slow);
+            if (lane == 0 && b1) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)__popcll(b1));
+            if (lane == 0 && b2) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)__popcll(b2));
+            if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
+        }
+        const bool live = vis && why == 0;
+        const int tmax = wave_max_dpp(live ? E + 23 : INT_MIN);
+        const int Rnew = max(Rrun[r], tmax);
+        const bool far = live && (E - Rnew < -1000);
+        if (__ballot(why != 0 || far)) rflag[r] = 1;
+        double f = 1.0;  // rescale of the running sums to the new reference exponent
+        if (Rrun[r] != INT_MIN && Rnew != Rrun[r]) {
+            const int dsh = Rrun[r] - Rnew;
+            if (dsh < -900) rflag[r] = 1;
+            f = ldexp(1.0, max(dsh, -1000));
+            zacc[r] *= f;
+        }
+        Rrun[r] = Rnew;
+        double om = (live && !far) ? ldexp((double)M, E - Rnew) : 0.0;
+        if (rflag[r]) om = 0.0;
+        zacc[r] += om;
+        nvis[r] += vis ? 1 : 0;
+        *fout = f;
+        return om;
+    };
+    // q row r's fp64 values (prep kernel), for the exact path
+    auto qrow64 = [&](int r) __attribute__((always_inline)) { return (cdouble_t*)P.q64 + (int64_t)grow[r] * EA_MAXD; };
+
+    // R, Z and the visible count (-1: flagged) of rows [r0, r1) into the split partial
+    auto publish_rows = [&](int r0, int r1) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            Rrun[r] = INT_MIN;
-            zacc[r] = 0.0;
-            nvis[r] = 0;
+            if (r < r0 || r >= r1) continue;
+            const double zs = wave_sum(zacc[r]);
+            const int ns = wave_sum_i(nvis[r]);
+            if (lane == 0 && r < nrow) {
+                const int64_t o = pbase + grow[r];
+                P.pR[o] = Rrun[r];
+                P.pZ[o] = zs;
+                P.pn[o] = rflag[r] ? -1 : ns;
+            }
         }
+    };
+
+    if (role == 0) {
+        // ============ wave A: K tiles, scores, certified logits and weights of rows [0, RA)
         if (ntiles > 0) issue_k(k0, 0);
         __syncthreads();  // tables visible
         for (int it = 0; it <= ntiles; ++it) {
@@ -280,109 +372,49 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
                 }
             }
 
-            // ---- B: lane = key, every row
+            // ---- B: lane = key; rows [0, RA) certified here, the scores and bounds of rows
+            // [RA, RB) handed to wave B
             __builtin_amdgcn_sched_barrier(0);
             const int n = n0 + lane;
+            // exact products of q row r and this lane's key, from the K tile in LDS
+            auto exact_lds = [&](int r, int, double& ss, double& es, double& ea) __attribute__((always_inline)) {
+                cdouble_t* qr = qrow64(r);
+                for (int c = 0; c < 16; ++c) {
+                    const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
+                    const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        double e0, e1;
+                        ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
+                        ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
+                        es += e0 + e1;
+                        ea += fabs(e0) + fabs(e1);
+                    }
+                }
+            };
     #pragma unroll
             for (int r = 0; r < RB; ++r) {
                 __builtin_amdgcn_sched_barrier(0);  // one row at a time (bounded live temporaries)
-                const int ti = n - tb;
-                const bool vis = (n < k1) && (n < kvl[r] || (ti >= 0 && ti < 64 && ((tmk[r] >> ti) & 1)));
-                double s = a0[r] + a1[r];
+                const double s = a0[r] + a1[r];
                 const double bnd = __fma_rn(qn4[grow[r] * 4 + 0], (double)km[0],
                                     __fma_rn(qn4[grow[r] * 4 + 1], (double)km[1],
                                     __fma_rn(qn4[grow[r] * 4 + 2], (double)km[2], qn4[grow[r] * 4 + 3] * (double)km[3])));
-                double del = gam * bnd * (1.0 + 0x1p-40) + 0x1p-1060;
-                int32_t M = 1 << 23, E = -23;
-                int why = 0;  // 1 score not certified, 2 weight not certified, 3 weight out of range
-                bool slow = false;
-                if (vis && !rflag[r]) {
-                    uint32_t tbits = 0;
-                    int ls = isfinite(s) ? logit_cert(alpha, s, 0.0, del, &tbits) : 3;
-                    if (ls == 3 && isfinite(s)) {
-                        // exact path: every product separately, TwoSum-accumulated
-                        slow = true;
-                        cdouble_t* qr = (cdouble_t*)P.q64 + (int64_t)grow[r] * EA_MAXD;
-                        double ss = 0.0, es = 0.0, ea = 0.0;
-                        for (int c = 0; c < 16; ++c) {
-                            const uint4 kv = S.K[buf][lane * 16 + (c ^ (lane & 15))];
-                            const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
-    #pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                double e0, e1;
-                                ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
-                                ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
-                                es += e0 + e1;
-                                ea += fabs(e0) + fabs(e1);
-                            }
-                        }
-                        ls = (ss == 0.0 && es == 0.0 && ea == 0.0) ? 1 : logit_cert(alpha, ss, es, ea * 0x1p-44, &tbits);
-                    }
-                    if (ls == 2 || ls == 3) {
-                        why = 1;
-                    } else if (ls == 0) {
-                        int ws = weight_f64(tbits, S.T1, S.T2, &M, &E);
-                        if (ws) {
-                            int32_t M2 = 0;
-                            int64_t E2 = 0;
-                            if (weight_wide(tbits, &M2, &E2) == 0 && E2 > -(1LL << 30) && E2 < (1LL << 30)) {
-                                M = M2;
-                                E = (int32_t)E2;
-                            } else {
-                                why = 2;
-                            }
-                        }
-                    }
+                const double del = gam * bnd * (1.0 + 0x1p-40) + 0x1p-1060;
+                if (r >= RA) {
+                    S.sb[buf][lane][r - RA] = make_double2(s, del);
+                    continue;
                 }
-                if (P.stats) {
-                    const uint64_t b1 = __ballot(why == 1), b2 = __ballot(why == 2), b3 = __ballot(slow);
-                    if (lane == 0 && b1) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)__popcll(b1));
-                    if (lane == 0 && b2) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)__popcll(b2));
-                    if (lane == 0 && b3) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)__popcll(b3));
-                }
-                const bool live = vis && why == 0;
-                const int tmax = wave_max_dpp(live ? E + 23 : INT_MIN);
-                const int Rnew = max(Rrun[r], tmax);
-                const bool far = live && (E - Rnew < -1000);
-                if (__ballot(why != 0 || far)) rflag[r] = 1;
-                double f = 1.0;  // rescale of the running sums to the new reference exponent
-                if (Rrun[r] != INT_MIN && Rnew != Rrun[r]) {
-                    const int dsh = Rrun[r] - Rnew;
-                    if (dsh < -900) rflag[r] = 1;
-                    f = ldexp(1.0, max(dsh, -1000));
-                    zacc[r] *= f;
-                }
+                double f;
+                const double om = certify(r, n, s, del, exact_lds, &f);
                 if (lane == 0) S.sc[buf][r] = f;
-                Rrun[r] = Rnew;
-                double om = (live && !far) ? ldexp((double)M, E - Rnew) : 0.0;
-                if (rflag[r]) om = 0.0;
-                zacc[r] += om;
-                nvis[r] += vis ? 1 : 0;
                 S.w[buf][lane][r] = om;
             }
                 }
             __syncthreads();  // weights of tile it published; wave B is done with tile it - 1
         }
-        double zs[RB];
-        int ns[RB];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            zs[r] = wave_sum(zacc[r]);
-            ns[r] = wave_sum_i(nvis[r]);
-        }
-        if (lane == 0) {
-            // the decode kernel takes every row of the problem: one add for the whole grid
-            if (P.stats && item == 0 && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
-#pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                if (r < nrow) {
-                    const int64_t o = pbase + grow[r];
-                    P.pR[o] = Rrun[r];
-                    P.pZ[o] = zs[r];
-                    P.pn[o] = rflag[r] ? -1 : ns[r];
-                }
-            }
-        }
+        // the decode kernel takes every row of the problem: one add for the whole grid
+        if (lane == 0 && P.stats && item == 0 && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
+        publish_rows(0, RA);
     } else {
         // ============ wave B: V tiles (double-buffered in VGPRs) and the P.V sums
         double pacc[RB][8];
@@ -399,13 +431,54 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
             issue_v(k0 + DT, vB, 0.0, 0.0);
         }
         // P of tile t with its V in vr; then V(t+2) into vr
+        // exact products of q row r and key n, the key read from the cache (its LDS tile is being
+        // refilled by then); only pairs the fp64 interval cannot decide come here
+        auto exact_global = [&](int r, int n, double& ss, double& es, double& ea) __attribute__((always_inline)) {
+            const int64_t pg = P.bt ? (int64_t)btb[n >> pshift] : (int64_t)b;
+            const int sl = P.bt ? (n & pmask) : n;
+            const uint4* kp = (const uint4*)(kh + pg * kps2 + (int64_t)sl * kss2);
+            cdouble_t* qr = qrow64(r);
+            for (int c = 0; c < 16; ++c) {
+                const uint4 kv = kp[c];
+                const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    double e0, e1;
+                    ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
+                    ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
+                    es += e0 + e1;
+                    ea += fabs(e0) + fabs(e1);
+                }
+            }
+        };
         auto pv = [&](int t, u32x4 (&vr)[16]) __attribute__((always_inline)) {
             const int buf = t & 1;
+            // rows [RA, RB) of tile t: certified here (lane = key) while V(t) is still landing;
+            // the weights replace the scores in LDS for the P.V below
+            if constexpr (RB > RA) {
+                const int n = k0 + t * DT + lane;
+#pragma unroll
+                for (int r = RA; r < RB; ++r) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const double2 sd = S.sb[buf][lane][r - RA];
+                    double f;
+                    const double om = certify(r, n, sd.x, sd.y, exact_global, &f);
+                    if (f != 1.0) {
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) pacc[r][c] *= f;
+                    }
+                    S.sb[buf][lane][r - RA].x = om;
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's weights are in LDS
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
             // V loads complete in issue order: V(t) has landed once only V(t+1)'s 16 instructions
             // may be outstanding
             wait_vm<16>();
 #pragma unroll
-            for (int r = 0; r < RB; ++r) {
+            for (int r = 0; r < RA; ++r) {
                 const double f = S.sc[buf][r];
                 if (f != 1.0) {
 #pragma unroll
@@ -417,7 +490,7 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
                 const int kk = 4 * j + g;
                 double om[RB];
 #pragma unroll
-                for (int r = 0; r < RB; ++r) om[r] = S.w[buf][kk][r];
+                for (int r = 0; r < RB; ++r) om[r] = r < RA ? S.w[buf][kk][r] : S.sb[buf][kk][r - RA].x;
                 const uint32_t vd[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -458,6 +531,7 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
             pv(t, vA);
         }
         __syncthreads();  // barrier ntiles + 1: wave A runs one loop iteration past its last tile
+        publish_rows(RA, RB);
         // reduce the 4 key groups (lanes 16 apart) through LDS; the K buffers are free once the
         // loop's last barrier has passed
         double* red = reinterpret_cast<double*>(&S.K[0][0]);  // [g][r][128]: 4 * RB KB <= 16 KB
