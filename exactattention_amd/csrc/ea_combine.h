@@ -34,6 +34,24 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
             mo_ok = seen == (ns == 64 ? ~0ull : ((1ull << ns) - 1));
             if (mo_ok) si = m;
         }
+        // up to 8 splits in the caller's order: every channel partial of both lane channels is
+        // requested now, in the same round as the split scalars (one load latency per row instead
+        // of three); splits that turn out empty are dropped by selects below
+        const bool pre = ns <= 8 && !mo_ok && dv <= 128;
+        double pfn[2][8];
+        float pfv[2][8];
+        if (pre) {
+#pragma unroll
+            for (int ci = 0; ci < 2; ++ci)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int c = lane + 64 * ci;
+                    const bool in = k < ns && c < dv;
+                    const int64_t o = (int64_t)k * P.rows + row;
+                    pfn[ci][k] = in ? P.pN[o * dv + c] : 0.0;
+                    pfv[ci][k] = in ? P.pV[(((int64_t)k * P.nseg + seg) * P.nrb + rbk) * dv + c] : 0.0f;
+                }
+        }
         int n_i = 0, r_i = INT_MIN;
         double z_i = 0.0;
         if (lane < ns) {
@@ -73,7 +91,46 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
         const double eZ = A * up + tiny;
         if (!(Z > 2.0 * eZ) || !isfinite(Z)) flag = 1;
         bool ok = !flag;
-        for (int c = lane; c < dv; c += 64) {
+        // certified rounding of channel c from its merged sum N and bound vmaxf on |v|
+        auto finish = [&](int c, double N, float vmaxf) __attribute__((always_inline)) {
+            uint32_t bits = 0;
+            const double eN = A * up * (double)vmaxf + tiny;
+            const double q = N / Z;
+            const double aq = fabs(q);
+            const double delta = (eN + aq * eZ) / (Z - eZ) * (1.0 + 0x1p-40) + aq * 0x1p-51 + 0x1p-1070;
+            if (!isfinite(q) || !isfinite(delta) || !certify_round(q, delta, P.out_fp32, &bits)) ok = false;
+            return bits;
+        };
+        if (pre) {
+            int nk[8], shk[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                nk[k] = __shfl(n_i, k, 64);
+                shk[k] = __shfl(dsh_i, k, 64);
+            }
+#pragma unroll
+            for (int ci = 0; ci < 2; ++ci) {
+                const int c = lane + 64 * ci;
+                if (c >= dv) continue;
+                uint32_t bits = 0;
+                if (!flag) {
+                    double N = 0.0;
+                    float vmaxf = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const bool use = k < ns && nk[k] > 0;
+                        N += use ? ldexp(pfn[ci][k], max(shk[k], -1000)) : 0.0;
+                        const float vm = use ? pfv[ci][k] : 0.0f;
+                        vmaxf = fmaxf(vmaxf, vm);
+                        if (!(vm <= 3.4028235e38f)) vmaxf = __builtin_inff();
+                    }
+                    bits = finish(c, N, vmaxf);
+                }
+                if (P.out_fp32) o32[obase + c] = bits;
+                else o16[obase + c] = (uint16_t)bits;
+            }
+        }
+        for (int c = lane; c < dv && !pre; c += 64) {
             uint32_t bits = 0;
             if (!flag) {
                 double N = 0.0;
@@ -99,11 +156,7 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
                         if (!(pv8[k] <= 3.4028235e38f)) vmaxf = __builtin_inff();
                     }
                 }
-                const double eN = A * up * (double)vmaxf + tiny;
-                const double q = N / Z;
-                const double aq = fabs(q);
-                const double delta = (eN + aq * eZ) / (Z - eZ) * (1.0 + 0x1p-40) + aq * 0x1p-51 + 0x1p-1070;
-                if (!isfinite(q) || !isfinite(delta) || !certify_round(q, delta, P.out_fp32, &bits)) ok = false;
+                bits = finish(c, N, vmaxf);
             }
             if (P.out_fp32) o32[obase + c] = bits;
             else o16[obase + c] = (uint16_t)bits;
