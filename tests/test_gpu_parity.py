@@ -687,6 +687,30 @@ def test_prefill_c3_golden_hash(gpu):
     assert hashlib.sha256(got.tobytes()).hexdigest() == gold, st
 
 
+@pytest.fixture(scope="module")
+def c4_problem():
+    return configs.c4()
+
+
+@pytest.mark.parametrize("name,path", [("C1", None), ("C2", None), ("C4", None), ("C4", "0")],
+                         ids=["C1", "C2", "C4", "C4-decode-kernel"])
+def test_config_golden_hash(gpu, monkeypatch, request, name, path):
+    """BASELINE configs C1, C2 and C4 at full size against the committed hashes (the oracle's and
+    the reference C++ kernel's bits). C4 (16-node draft trees, GQA 2: 32 rows per sequence and KV
+    head) runs on the int8 prefill kernel by default and on the decode kernel with EA_PREFILL=0;
+    both give the golden bits. C5 (4.97 GB of K/V, about six minutes of seeded input generation)
+    is checked by hand, not here."""
+    if path is not None:
+        monkeypatch.setenv("EA_PREFILL", path)
+    p = request.getfixturevalue("c4_problem") if name == "C4" else configs.CONFIGS[name]()
+    got, flags, st = _run(p, configs.alpha_bits())
+    gold = json.load(open(os.path.join(GOLD, "baseline_sha256.json")))[name]["sha256"]
+    assert hashlib.sha256(got.tobytes()).hexdigest() == gold, st
+    if name == "C4":
+        assert st["prefill_kernel_rows"] == (_rows(p) if path is None else 0), st
+    assert np.all(flags[flags != 0] == 1), st   # flagged rows (if any) certified by tier 2
+
+
 def test_prefill_c3_back_to_back(gpu):
     """C3 launched 12 times in a row with no host synchronisation between steps: the kernel's
     pipeline (tile DMA into LDS overlapping the MFMA work) must give the same certified rows in
