@@ -111,3 +111,27 @@ def test_alpha_bits_for_scaling():
         assert alpha_bits_for(float(x)) == int(np.float32(want).view(np.uint32)), x
     with pytest.raises(ValueError):
         alpha_bits_for(0.0)
+
+
+def test_hf_attention_rejects_before_device_work():
+    """serving.hf_attention refuses, before any HIP call, what the certified kernels do not
+    define: dropout, sliding windows, non-bf16 or host tensors, mismatched shapes, more queries
+    than keys."""
+    import torch
+    from exactattention_amd.serving import hf_attention
+
+    class M:
+        scaling = 128 ** -0.5
+    q = torch.zeros((1, 2, 3, 128), dtype=torch.bfloat16)
+    k = torch.zeros((1, 1, 5, 128), dtype=torch.bfloat16)
+    for kw in ({"dropout": 0.1}, {"sliding_window": 4}):
+        with pytest.raises(ValueError):
+            hf_attention(M(), q, k, k, None, **kw)
+    with pytest.raises(ValueError):            # host tensors
+        hf_attention(M(), q, k, k, None)
+    with pytest.raises(ValueError):            # fp32 tensors
+        hf_attention(M(), q.float(), k.float(), k.float(), None)
+    with pytest.raises(ValueError):            # head_dim mismatch
+        hf_attention(M(), q, k[..., :64], k[..., :64], None)
+    with pytest.raises(ValueError):            # 3 queries, 2 keys
+        hf_attention(M(), q, k[:, :, :2], k[:, :, :2], None)
