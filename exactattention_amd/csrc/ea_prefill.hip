@@ -151,10 +151,27 @@ __device__ __forceinline__ double quad_sumd(double x) {
 __device__ __forceinline__ void slice32(const uint16_t* src, bool valid, Slice32& S, int* lost = nullptr) {
     int m[32], e[32];
     int bad = 0, lead = INT_MIN;
+    // the 64 bytes as four 16-byte loads when they start on a 16-byte boundary (the usual
+    // cache strides), else element by element
+    uint32_t raw[16];
+    if (valid && ((uintptr_t)src & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 v = ((const uint4*)src)[i];
+            raw[4 * i] = v.x;
+            raw[4 * i + 1] = v.y;
+            raw[4 * i + 2] = v.z;
+            raw[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            raw[i] = valid ? ((uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 16)) : 0u;
+    }
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         int bk;
-        bf16_dec(valid ? (uint32_t)src[k] : 0u, &m[k], &e[k], &bk);
+        bf16_dec((raw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, &m[k], &e[k], &bk);
         bad |= bk;
         if (m[k] && !bk) lead = max(lead, lead_of(m[k], e[k]));
     }
