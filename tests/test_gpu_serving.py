@@ -12,14 +12,14 @@ from gen import bf16
 pytestmark = pytest.mark.gpu
 
 
-def _oracle_rows(q, K, V, kv_len, alpha_bits, tree_mask=None, tree_base=None):
+def _oracle_rows(q, K, V, kv_len, alpha_bits, tree_mask=None, tree_base=None, out="bf16"):
     """q (T, Hq, d); K, V (S, Hkv, d) logical history of one sequence."""
     from oracle import oracle
     prob = problem.contiguous(q[None], K.transpose(1, 0, 2)[None], V.transpose(1, 0, 2)[None],
                               np.asarray(kv_len).reshape(1, -1), tree_mask=tree_mask,
                               tree_base=None if tree_base is None else np.array([tree_base]))
-    out, _ = oracle.attention_geom(prob, alpha_bits, "bf16")
-    return out[0]
+    res, _ = oracle.attention_geom(prob, alpha_bits, out)
+    return res[0]
 
 
 def test_serving_session_matches_oracle(gpu):
@@ -208,3 +208,32 @@ def test_hf_model_runs_through_exact_attention(gpu):
         want = _oracle_rows(q[0].transpose(1, 0, 2), k[0].transpose(1, 0, 2), v[0].transpose(1, 0, 2),
                             kl - ql + 1 + np.arange(ql), alpha_bits_for(scaling))
         assert np.array_equal(out[0], want), (ql, kl)
+
+
+def test_forward_fp32_output_matches_oracle(gpu):
+    """ExactAttentionBackend(out="fp32"): a mixed batch (a 70-token chunk on the prefill kernel,
+    then a decode batch on the decode kernel) gives the oracle's fp32 bits."""
+    import torch
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    rng = np.random.default_rng(73)
+    Hq, Hkv, d = 4, 2, 128
+    ab = default_alpha_bits(d)
+    cache = PagedKVCache(num_pages=40, page_size=16, num_kv_heads=Hkv, head_dim=d, max_seqs=2, max_seq_len=256)
+    be = ExactAttentionBackend(cache, Hq, ab, out="fp32")
+    slots = [cache.add_sequence(), cache.add_sequence()]
+    hist = {s: (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16)) for s in slots}
+    dev = torch.device("cuda")
+    for lens in ([70, 3], [1, 1]):
+        n = sum(lens)
+        q, k, v = bf16(rng, (n, Hq, d)), bf16(rng, (n, Hkv, d)), bf16(rng, (n, Hkv, d))
+        to = lambda a: torch.from_numpy(a.view(np.int16)).to(dev)
+        out, fl = be.forward(to(q), to(k), to(v), slots, lens)
+        be.check_flags(fl)
+        got = out.cpu().numpy().view(np.uint32)
+        at = 0
+        for s, T in zip(slots, lens):
+            L = len(hist[s][0])
+            hist[s] = (np.concatenate([hist[s][0], k[at:at + T]]), np.concatenate([hist[s][1], v[at:at + T]]))
+            want = _oracle_rows(q[at:at + T], *hist[s], L + 1 + np.arange(T), ab, out="fp32")
+            assert np.array_equal(got[at:at + T], want), (lens, s)
+            at += T
