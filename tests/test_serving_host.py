@@ -135,3 +135,20 @@ def test_hf_attention_rejects_before_device_work():
         hf_attention(M(), q, k[..., :64], k[..., :64], None)
     with pytest.raises(ValueError):            # 3 queries, 2 keys
         hf_attention(M(), q, k[:, :, :2], k[:, :, :2], None)
+
+
+def test_forward_rejects_bad_batches_without_touching_the_cache():
+    """ExactAttentionBackend.forward checks the batch description before anything is appended:
+    a length list of the wrong size, a zero-token chunk, or tensors that do not hold
+    sum(query_lens) tokens raise ValueError and leave the cache as it was."""
+    import torch
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    c = PagedKVCache(num_pages=4, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
+                     digits=False, device="cpu")
+    be = ExactAttentionBackend(c, 2, 0x3E0293EE)
+    a, b = c.add_sequence(), c.add_sequence()
+    q, k = torch.zeros((3, 2, 8), dtype=torch.int16), torch.zeros((3, 1, 8), dtype=torch.int16)
+    for seqs, lens in (([a, b], [3]), ([a, b], [3, 0]), ([a, b], [1, 1])):
+        with pytest.raises(ValueError):
+            be.forward(q, k, k, seqs, lens)
+    assert c.length == [0, 0] and c.pages == [[], []] and len(c.free) == 4
