@@ -1147,6 +1147,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     if (pl.prefill && o->kv_digits) {
         P.pfkv = (uint8_t*)o->kv_digits;
         P.pf_kv_cached = 1;
+        P.pf_kv_slot = o->kv_digits_slot;
     }
     P.pfscr = (double*)(ws + pl.off_pfscr);
     P.pf_ntiles = (pl.prefill && o->kv_digits) ? o->kv_digits_tiles : pl.pf_ntiles;

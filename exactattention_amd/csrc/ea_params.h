@@ -69,6 +69,7 @@ struct Params {
     const int32_t* kvd_end;
     int32_t kvd_span;
     int32_t pf_kv_cached;  // 1: pfkv is the caller's digit cache, already sliced
+    const int32_t* pf_kv_slot;  // with pf_kv_cached: cache slot of each sequence (NULL: b)
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {

@@ -682,6 +682,8 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     const int Hkv = P.g.num_kv_heads;
     const int64_t b = seg / Hkv;
     const int hk = seg % Hkv;
+    // the segment's K/V tiles: its own in the workspace, or its slot's in the caller's cache
+    const int64_t kseg = (P.pf_kv_cached && P.pf_kv_slot) ? (int64_t)P.pf_kv_slot[b] * Hkv + hk : (int64_t)seg;
     const int T = P.g.num_tokens;
     constexpr int WDS = 5 * NKT * 64;  // digit dwords per wave: [plane 5][NKT][lane 64]
     uint32_t* const wd_w = sWD + w * WDS + lane;                    // this wave's digit planes
@@ -759,7 +761,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     // Issued through pf_dma (inline asm), so the compiler inserts no waits of its own before the
     // LDS reads: every read of a DMA'd buffer follows an explicit vmcnt wait for that buffer.
     auto rsrc = [&](int tile) __attribute__((always_inline)) {
-        const uint64_t src = (uint64_t)(P.pfkv + ((int64_t)seg * P.pf_ntiles + tile) * EA_PF_TILE_BYTES);
+        const uint64_t src = (uint64_t)(P.pfkv + (kseg * P.pf_ntiles + tile) * EA_PF_TILE_BYTES);
         v4i r = {(int)(uint32_t)src, (int)((uint32_t)(src >> 32) & 0xFFFFu), EA_PF_TILE_BYTES, 0x00020000};
         r.x = __builtin_amdgcn_readfirstlane(r.x);
         r.y = __builtin_amdgcn_readfirstlane(r.y);
@@ -1080,7 +1082,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         // digits are inexact (elements rounded at slicing) read the bf16 inputs.
         if (__builtin_expect(__ballot(slowmask != 0) != 0, 0)) {
             ++ncold;
-            const int8_t* Kg = (const int8_t*)(P.pfkv + ((int64_t)seg * P.pf_ntiles + it) * EA_PF_TILE_BYTES);
+            const int8_t* Kg = (const int8_t*)(P.pfkv + (kseg * P.pf_ntiles + it) * EA_PF_TILE_BYTES);
             for (int p = 0; p < 4 * NKT; ++p) {
                 if (!((slowmask >> p) & 1)) continue;
                 const int kk = p >> 2, i = p & 3;

@@ -41,7 +41,8 @@ class Buffers(ctypes.Structure):
 class Options(ctypes.Structure):
     _fields_ = [("alpha_bits", ctypes.c_uint32), ("out_fp32", ctypes.c_int32), ("splits", ctypes.c_int32),
                 ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P), ("timers", P),
-                ("kv_digits", P), ("kv_digits_tiles", ctypes.c_int32), ("pad1", ctypes.c_int32)]
+                ("kv_digits", P), ("kv_digits_tiles", ctypes.c_int32), ("pad1", ctypes.c_int32),
+                ("kv_digits_slot", P)]
 
 
 EA_PF_TILE_BYTES = 69632  # one 64-key digit tile (ea_params.h)

@@ -275,7 +275,7 @@ class ExactAttentionBackend:
         flags = torch.empty(B * T * Hq, dtype=torch.uint8, device=c.dev)
         tm = tb = None
         if staged is not None:
-            seq, off = staged
+            seq, off = staged[0], staged[1]
         else:
             up = [np.asarray(lens, dtype=np.int32), np.asarray([s * c.max_pages for s in seqs], dtype=np.int64)]
             if tree_mask is not None:
@@ -289,6 +289,10 @@ class ExactAttentionBackend:
         if digits_slot is not None and c.digits is not None:
             o.kv_digits = ctypes.c_void_p(c._digit_base(digits_slot))
             o.kv_digits_tiles = c.tiles
+            if staged is not None and len(staged) > 2:
+                # slot map: sequence b's tiles live at cache slot seqs[b]
+                o.kv_digits = ctypes.c_void_p(c.digits.data_ptr())
+                o.kv_digits_slot = staged[2].data_ptr()
         nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
         hip._check(lib.ea_hip_workspace_size(ctypes.byref(gc), ctypes.byref(o), ctypes.byref(nb), ctypes.byref(ns)),
                    "ea_hip_workspace_size")
@@ -344,15 +348,15 @@ class ExactAttentionBackend:
         kvl_h = np.zeros(B * T, dtype=np.int32)
         kvl_h[b_of * T + j_of] = np.asarray(prefix)[b_of] + j_of + 1
         mine = [kvl_h, np.asarray([c.length[s] for s in seqs], dtype=np.int32),
-                np.asarray([s * c.max_pages for s in seqs], dtype=np.int64)]
+                np.asarray([s * c.max_pages for s in seqs], dtype=np.int64), np.asarray(seqs, dtype=np.int32)]
         if T > 1:
             mine.append((b_of * T + j_of).astype(np.int64))
         n_app = len(plan["arrays"])
         dev = c.stage.put(*plan["arrays"], *mine)
         st = hip._stream_ptr(torch)
         c._apply_append(plan, dev[:n_app], st)
-        kvl, staged = dev[n_app], (dev[n_app + 1], dev[n_app + 2])
-        row = dev[n_app + 3] if T > 1 else None
+        kvl, staged = dev[n_app], (dev[n_app + 1], dev[n_app + 2], dev[n_app + 3])
+        row = dev[n_app + 4] if T > 1 else None
         q16 = query.view(torch.int16) if query.dtype != torch.int16 else query
         if T == 1:
             qd = q16.reshape(B, 1, Hq, d).contiguous()
@@ -361,9 +365,7 @@ class ExactAttentionBackend:
             qd.index_copy_(0, row, q16)
             qd = qd.view(B, T, Hq, d)
         slots = list(seqs)
-        contiguous = slots == list(range(slots[0], slots[0] + B))
-        out, flags = self._launch(slots, qd, kvl, digits_slot=slots[0] if contiguous else None, staged=staged,
-                                  stream=st)
+        out, flags = self._launch(slots, qd, kvl, digits_slot=slots[0], staged=staged, stream=st)
         if T == 1:
             return out.view(B, Hq, -1), flags.view(B, Hq)
         return out.view(B * T, Hq, -1).index_select(0, row), flags.view(B * T, Hq).index_select(0, row)

@@ -102,6 +102,9 @@ typedef struct ea_options {
     int32_t kv_digits_tiles; /* tiles per (sequence, KV head) in kv_digits; must be at least
                                ceil(max_seq_len / 64) */
     int32_t pad1;
+    const int32_t* kv_digits_slot; /* optional, with kv_digits: device array, per sequence b of
+                               the geometry the cache slot holding its tiles (a serving loop's
+                               sequence slot); NULL: slot b */
 } ea_options;
 
 /* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
