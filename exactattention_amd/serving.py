@@ -314,7 +314,7 @@ class ExactAttentionBackend:
         qd = _dev16(torch, q, c.dev).contiguous()
         (kvl,) = c.stage.put(np.asarray(kv_len, dtype=np.int32).reshape(-1))
         out, flags = self._launch(seqs, qd, kvl, tree_mask, tree_base, digits_slot)
-        torch.cuda.synchronize()
+        torch.cuda.current_stream().synchronize()  # the launch stream only, not the whole device
         res = out.cpu().numpy()
         res = res.view(np.uint32) if self.out == "fp32" else res.view(np.uint16)
         fl = flags.cpu().numpy()
