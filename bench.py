@@ -114,7 +114,10 @@ def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     pairs = int(L.sum())
+    model = next((ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")),
+                 "unknown") if os.path.exists("/proc/cpuinfo") else "unknown"
     return {"value": round(algorithmic_bytes(prob) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "cpu_model": model, "host_cpus": os.cpu_count(),
             "sample": f"full C2 step ({pairs} query-key pairs, splits=8, 64-key tiles, int64), median of 3 "
                       f"after 1 warm-up; {pairs / t / 1e6:.2f} M pairs/s; {int((flags != 0).sum())} rows flagged",
             "wall_s": round(t, 3)}, res
@@ -122,6 +125,8 @@ def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
 
 MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, vendor figure (256 CUs, 2.4 GHz)
 PF_TRAFFIC = os.path.join(ROOT, "profiles", "ea_pf_main_C3_traffic.md")
+C4_TRAFFIC = os.path.join(ROOT, "profiles", "ea_pf_main_C4_traffic.md")
+C5_TRAFFIC = os.path.join(ROOT, "profiles", "ea_decode_C5_traffic.md")
 
 
 def prefill_ops(prob: dict) -> int:
@@ -141,23 +146,37 @@ def read_traffic(path: str):
     return None
 
 
-def run_config(name: str, steps: int, warmup: int, splits: int = 0, breakdown_steps: int = 10):
+def run_config(name: str, steps: int, warmup: int, splits: int = 0, breakdown_steps: int = 10, digits: bool = False,
+               prob=None):
     """Generate config `name`, run warm-up steps, check the bits against the golden hash, then time
     `steps` steps. Inside the timed region HIP events (recorded on the launch stream) bracket only
     the main kernel of each step: that kernel's mean duration feeds the roofline. A separate,
     untimed pass of `breakdown_steps` steps records events between every kernel for the
     per-kernel breakdown (each event record is one more packet in the stream, so the timed steps
-    carry only the two the roofline needs)."""
+    carry only the two the roofline needs). digits=True keeps the K/V digit tiles in a KVDigits
+    cache sliced once before the steps (the KV write path's format), which the int8 path reads."""
     import torch
     from exactattention_amd import configs
-    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    from exactattention_amd.hip import STATS, DeviceProblem, KVDigits, launch_hip
     t0 = time.time()
-    prob = configs.CONFIGS[name]()
+    if prob is None:
+        prob = configs.CONFIGS[name]()
     ab = configs.alpha_bits()
     gen_s = time.time() - t0
     dp = DeviceProblem(prob, "bf16", splits, "cuda:0")
+    cache = None
+    slice_ms = None
+    if digits:
+        S = int(prob["seq_len"].max())
+        cache = KVDigits(dp, (S + 63) // 64)
+        z = torch.zeros(dp.geom["num_seqs"], dtype=torch.int32, device="cuda:0")
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        cache.update(dp, z, dp.t["seq_len"], S)
+        torch.cuda.synchronize()
+        slice_ms = (time.perf_counter() - t1) * 1e3
     for _ in range(warmup):
-        launch_hip(dp, ab)
+        launch_hip(dp, ab, kv_digits=cache)
     torch.cuda.synchronize()
     out = dp.out.cpu().numpy().view(np.uint16)
     golden = json.load(open(GOLDEN)).get(name, {}).get("sha256") if os.path.exists(GOLDEN) else None
@@ -168,7 +187,7 @@ def run_config(name: str, steps: int, warmup: int, splits: int = 0, breakdown_st
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        launch_hip(dp, ab, events=slots[i])
+        launch_hip(dp, ab, events=slots[i], kv_digits=cache)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     main_ms = float(np.mean([ev.ms(2 * i, 2 * i + 1) for i in range(steps)]))
@@ -176,12 +195,73 @@ def run_config(name: str, steps: int, warmup: int, splits: int = 0, breakdown_st
     st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
     evb = HipEvents(5 * breakdown_steps)
     for i in range(breakdown_steps):
-        launch_hip(dp, ab, events=ctypes.cast(evb.slot(5 * i), ctypes.POINTER(ctypes.c_void_p)))
+        launch_hip(dp, ab, events=ctypes.cast(evb.slot(5 * i), ctypes.POINTER(ctypes.c_void_p)), kv_digits=cache)
     torch.cuda.synchronize()
     phases = np.array([[evb.ms(5 * i + j, 5 * i + j + 1) for j in range(4)] for i in range(breakdown_steps)])
     evb.close()
     return {"prob": prob, "ab": ab, "dp": dp, "out": out, "gen_s": gen_s, "bit_exact": bit_exact,
-            "ms_step": (t1 - t0) * 1e3 / steps, "main_ms": main_ms, "phases": phases.mean(0), "stats": st}
+            "ms_step": (t1 - t0) * 1e3 / steps, "main_ms": main_ms, "phases": phases.mean(0), "stats": st,
+            "cache": cache, "slice_ms": slice_ms}
+
+
+def tree_line(steps: int, warmup: int) -> dict:
+    """C4 speculative tree verification (8 sequences: an 8192-key prefix and a 16-node draft tree
+    each, 16 query / 8 KV heads): 32 rows per (sequence, KV head) take the int8 prefill kernel
+    with key splits, reading the K/V digit tiles from the cache the KV write path keeps (sliced
+    once, before the steps, and timed separately). Roofline: HBM, over the algorithmic bf16 K+V +
+    q + out bytes; the digit tiles the kernel actually streams are 69,632 B per 64 keys and KV
+    head (2.125x the bf16 bytes), reported beside it."""
+    import torch
+    r = run_config("C4", steps, warmup, digits=True)
+    prob, st, dp = r["prob"], r["stats"], r["dp"]
+    nbytes = algorithmic_bytes(prob)
+    g = prob["geom"]
+    tiles = g["num_seqs"] * g["num_kv_heads"] * ((int(prob["seq_len"].max()) + 63) // 64)
+    main_ms = r["main_ms"]
+    achieved = nbytes / (main_ms * 1e-3) / 1e9
+    sl, mk, cb, t2 = (float(x) for x in r["phases"])
+    line = {"workload": "C4 tree verification (B=8, prefix 8192, 16-node trees, 16 q / 8 KV heads, d=128)",
+            "ms_per_step": round(r["ms_step"], 5), "gbs_step": round(nbytes / (r["ms_step"] * 1e-3) / 1e9, 1),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(C4_TRAFFIC),
+                         "kernel": "ea_pf_main", "kernel_ms": round(main_ms, 5),
+                         "basis": "algorithmic bf16 bytes over the kernel's mean HIP-event duration on its stream"},
+            "digit_tile_gbs": round(tiles * 69632 / (main_ms * 1e-3) / 1e9, 1),
+            "kernels_ms": {"q_slice": round(sl, 5), "ea_pf_main": round(mk, 5), "ea_pf_combine": round(cb, 5),
+                           "tier2": round(t2, 5)},
+            "key_splits": dp.nsplit, "algorithmic_bytes_per_step": nbytes,
+            "kv_digits_slice_ms_all_keys": round(r["slice_ms"], 3),
+            "bit_exact": r["bit_exact"], "fallback_rows_pct": round(100.0 * st["tier1_flagged"] / max(1, st["rows"]), 4),
+            "input_gen_s": round(r["gen_s"], 1)}
+    del r
+    torch.cuda.empty_cache()
+    return line
+
+
+def long_context_line(steps: int, warmup: int) -> dict:
+    """C5 ragged long-context decode (16 sequences of 8K-131K keys, outlier channels in k, page 16)
+    on the fp64 decode kernel: HBM roofline over the algorithmic bytes, bits against the golden
+    hash, fallback rows."""
+    import torch
+    r = run_config("C5", steps, warmup)
+    prob, st, dp = r["prob"], r["stats"], r["dp"]
+    nbytes = algorithmic_bytes(prob)
+    main_ms = r["main_ms"]
+    achieved = nbytes / (main_ms * 1e-3) / 1e9
+    line = {"workload": "C5 ragged decode (B=16, kv 8K-131K, 16 q / 8 KV heads, d=128, page 16)",
+            "ms_per_step": round(r["ms_step"], 5), "gbs_step": round(nbytes / (r["ms_step"] * 1e-3) / 1e9, 1),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(C5_TRAFFIC),
+                         "kernel": "ea_decode", "kernel_ms": round(main_ms, 5),
+                         "basis": "algorithmic bytes over the kernel's mean HIP-event duration on its stream"},
+            "kernels_ms": {k: round(float(r["phases"][j]), 5) for j, k in enumerate(("prep", "split", "combine",
+                                                                                     "tier2"))},
+            "nsplit": dp.nsplit, "algorithmic_bytes_per_step": nbytes,
+            "bit_exact": r["bit_exact"], "fallback_rows_pct": round(100.0 * st["tier1_flagged"] / max(1, st["rows"]), 4),
+            "input_gen_s": round(r["gen_s"], 1)}
+    del r
+    torch.cuda.empty_cache()
+    return line
 
 
 def prefill_line(steps: int, warmup: int) -> dict:
@@ -318,7 +398,7 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill measurement")
-    ap.add_argument("--only", choices=("C2", "C3", "serving"), default=None,
+    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving"), default=None,
                     help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
                     help="after the timed steps, run 5 steps of the phase-clock build and report it")
@@ -345,6 +425,12 @@ def main():
     if args.only == "C3":
         print(json.dumps({"prefill": prefill_line(args.steps, args.warmup)}), flush=True)
         return
+    if args.only == "C4":
+        print(json.dumps({"tree_verify": tree_line(args.steps, args.warmup)}), flush=True)
+        return
+    if args.only == "C5":
+        print(json.dumps({"long_context": long_context_line(args.steps, args.warmup)}), flush=True)
+        return
     if args.only == "serving":
         from exactattention_amd import configs
         print(json.dumps({"serving": serving_line(configs.c2(), configs.alpha_bits(), args.steps, args.warmup)}),
@@ -364,10 +450,15 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "f64", "data": "synthetic",
         "config": {"workload": "C2 batched paged decode", "batch": 32, "q_heads": 16, "kv_heads": 8,
                    "head_dim": 128, "kv_len": 4096, "page_size": 16, "layout": "NHD", "nsplit": dp.nsplit,
+                   "nsplit_note": "auto split count; BASELINE names 8: the bits are identical at 1, 4 and 8 "
+                                  "splits (tests/test_gpu_parity.py test_config_golden_hash)",
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "ea_decode",
-                     "kernel_ms": round(split_ms, 5)},
+                     "kernel_ms": round(split_ms, 5),
+                     "basis": "algorithmic bytes over the decode kernel's mean HIP-event duration on its stream "
+                              "(events include dispatch gaps; the rocprofv3 trace average is in profiles/)",
+                     "traffic_source": "profiles/ea_decode_C2_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"},
         "kernels_ms": {k: round(float(r["phases"][j]), 5) for j, k in enumerate(("prep", "split", "combine",
                                                                                   "tier2"))},
         "bit_exact": r["bit_exact"], "fallback_rows_pct": round(flagged_pct, 4),
@@ -390,6 +481,8 @@ def main():
     torch.cuda.empty_cache()
     if args.only is None and not args.no_prefill:
         line["prefill"] = prefill_line(max(5, min(args.steps, 20)), 2)
+        line["tree_verify"] = tree_line(max(5, min(args.steps, 20)), 2)
+        line["long_context"] = long_context_line(max(5, min(args.steps, 10)), 2)
     if args.only is None:
         line["serving"] = serving_line(prob, ab, max(5, min(args.steps, 20)))
     if args.only is None and not args.no_cpu:

@@ -10,6 +10,8 @@ attention_cpu backends (returns (out, flags)), and `launch_hip` the device-level
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import numpy as np
 
 from . import problem
@@ -34,6 +36,8 @@ __all__ = [
     "default_alpha",
     "float_to_bf16_bits",
     "launch_hip",
+    "trace_row",
+    "RowTrace",
 ]
 
 
@@ -102,6 +106,72 @@ def attention_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> np.ndarra
     v = np.asarray(v_bits, dtype=np.uint16)
     v = v.reshape(k.shape[0], -1) if v.size else np.zeros((k.shape[0], v.shape[-1] if v.ndim else 0), np.uint16)
     return attention(q, k, v, alpha, out=out)[0]
+
+
+@dataclass
+class RowTrace:
+    """Every intermediate of one row (the reference's RowTrace, src/exactattn/reference.py:63-71):
+    exact scores s and weights w as (M, E) = M * 2**E, fp32 logits t as Python floats, the exact
+    denominator Z and per-channel numerators N as (M, E), and the output bits."""
+    s: list
+    t: list
+    w: list
+    Z: tuple
+    N: list
+    out: np.ndarray
+
+
+def _decode(bits: np.ndarray):
+    b = np.asarray(bits, dtype=np.uint16).astype(np.int64)
+    f = (b >> 7) & 0xFF
+    if np.any(f == 0xFF):
+        raise ExactAttentionDomainError("bf16 NaN or infinity in input")
+    m = np.where(f != 0, (b & 0x7F) | 0x80, b & 0x7F) * np.where(b & 0x8000, -1, 1)
+    return m, np.where(f != 0, f - 134, -133)
+
+
+def trace_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> RowTrace:
+    """One row with every intermediate (src/exactattn/reference.py:82-143). The logits, weights
+    and output bits come from the library's host exact tier (ea_exact_row); the exact scores and
+    sums are assembled from them here with Python integers."""
+    from .hip import exact_row
+    if out not in ("bf16", "fp32"):
+        raise ValueError("out must be 'bf16' or 'fp32'")
+    q = np.asarray(q_bits, dtype=np.uint16).reshape(-1)
+    d = q.shape[0]
+    k = np.asarray(k_bits, dtype=np.uint16).reshape(-1, d)
+    n = k.shape[0]
+    v = np.asarray(v_bits, dtype=np.uint16)
+    dv = v.shape[-1] if v.ndim == 2 else 0
+    v = v.reshape(n, dv)
+    res, tb, wm, we = exact_row(q, k, v, _alpha_bits(alpha), out, trace=True)
+    qm, qe = _decode(q)
+    km, ke = _decode(k)
+    vm, ve = _decode(v)
+    s = []
+    for j in range(n):
+        pm, pe = (qm * km[j]).tolist(), (qe + ke[j]).tolist()
+        terms = [(m_, e_) for m_, e_ in zip(pm, pe) if m_]
+        if not terms:
+            s.append((0, 0))
+            continue
+        e0 = min(e_ for _, e_ in terms)
+        s.append((sum(m_ << (e_ - e0) for m_, e_ in terms), e0))
+    t = [float(x) for x in np.asarray(tb, dtype=np.uint32).view(np.float32)]
+    w = [(int(a), int(b)) for a, b in zip(wm, we)]
+    if n == 0:
+        return RowTrace(s, t, w, (0, 0), [(0, 0)] * dv, res if out == "bf16" else res.view(np.float32))
+    e0 = min(e_ for _, e_ in w)
+    Z = (sum(m_ << (e_ - e0) for m_, e_ in w), e0)
+    N = []
+    for c in range(dv):
+        terms = [(w[j][0] * int(vm[j, c]), w[j][1] + int(ve[j, c])) for j in range(n) if vm[j, c]]
+        if not terms:
+            N.append((0, 0))
+            continue
+        b0 = min(e_ for _, e_ in terms)
+        N.append((sum(m_ << (e_ - b0) for m_, e_ in terms), b0))
+    return RowTrace(s, t, w, Z, N, res if out == "bf16" else res.view(np.float32))
 
 
 def launch_hip(*args, **kwargs):

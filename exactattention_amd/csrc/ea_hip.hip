@@ -16,6 +16,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -23,6 +24,7 @@
 #include "ea_device.h"
 #include "ea_params.h"
 #include "ea_combine.h"
+#include "ea_exact.h"
 
 using namespace ea;
 
@@ -930,6 +932,47 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
     }
 }
 
+// Lists every row for tier 2 (ea_options.force_tier2); runs after tier 1, so nothing else appends.
+__global__ void __launch_bounds__(256) ea_list_all(Params P) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < P.rows) P.wl[r] = (int32_t)r;
+    if (r == 0) *P.wl_cnt = (int32_t)P.rows;
+}
+
+// The host exact tier's input for one row: its q row, then the K rows and the V rows of its
+// visible keys (the kv_len prefix, then the tree keys in bit order), packed in dst as
+// [q d][K nkeys x d][V nkeys x dv], one element per thread.
+__global__ void __launch_bounds__(256) ea_gather_row(Params P, int64_t row, int64_t nkeys, uint16_t* dst) {
+    const int d = P.g.head_dim, dv = P.g.head_dim_v, T = P.g.num_tokens, Hq = P.g.num_q_heads;
+    const int64_t b = row / ((int64_t)T * Hq);
+    const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
+    const int hk = hq / P.grp;
+    const int64_t tok = b * T + t;
+    const int64_t L = P.kv_len[tok];
+    const uint64_t mask = P.tree_mask ? P.tree_mask[tok] : 0ull;
+    const int64_t tb = P.tree_mask ? P.tree_base[b] : 0;
+    const int64_t total = d + nkeys * (int64_t)(d + dv);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        if (i < d) {
+            dst[i] = P.q[b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride + i];
+            continue;
+        }
+        int64_t r = i - d;
+        const int isv = r >= nkeys * d ? 1 : 0;
+        if (isv) r -= nkeys * d;
+        const int wdt = isv ? dv : d;
+        const int64_t j = r / wdt;
+        const int e = (int)(r % wdt);
+        int64_t n = j;
+        if (j >= L) {
+            uint64_t m = mask;
+            for (int64_t c = j - L; c > 0; --c) m &= m - 1;
+            n = tb + (__ffsll((long long)m) - 1);
+        }
+        dst[i] = (isv ? P.v : P.k)[kv_off(P, b, n, hk, isv) + e];
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Known-answer kernels over the device helpers
 // ------------------------------------------------------------------------------------------------
@@ -998,9 +1041,9 @@ struct Plan {
     int nsplit, split_len, rb, nrb, r_seg, grp, nseg, pshift, dlog;
     int64_t rows;
     size_t off_q64, off_qinfo, off_qn, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
-    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr;
+    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr, off_pfpart;
     int t2_keys;
-    int prefill, pf_ntiles, pf_nrb;
+    int prefill, pf_ntiles, pf_nrb, pf_nsplit, pf_tps;
 };
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1014,6 +1057,8 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     if (g->page_size <= 0 || (g->page_size & (g->page_size - 1))) return -1;
     if (g->max_seq_len < 0) return -1;
     if (o->splits < 0) return -2;
+    if (o->kernel < EA_KERNEL_AUTO || o->kernel > EA_KERNEL_GENERAL) return -2;
+    if (o->prefill_waves != 0 && o->prefill_waves != 4 && o->prefill_waves != 8) return -2;
     pl->grp = g->num_q_heads / g->num_kv_heads;
     pl->r_seg = g->num_tokens * pl->grp;
     pl->rb = pl->r_seg >= 3 ? 4 : pl->r_seg;  // kernels exist for 1, 2 and 4 rows per block
@@ -1060,8 +1105,9 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->t2_keys = maxlen + 64;
     pl->off_t2M = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 4);
     pl->off_t2E = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 8);
-    pl->prefill = ea_prefill_eligible(*g, pl->grp, &pl->pf_ntiles, &pl->pf_nrb) ? 1 : 0;
-    pl->off_pfq = pl->off_pfqm = pl->off_pfkv = pl->off_pfscr = 0;
+    pl->prefill = ea_prefill_eligible(*g, pl->grp, o->kernel, &pl->pf_ntiles, &pl->pf_nrb) ? 1 : 0;
+    pl->off_pfq = pl->off_pfqm = pl->off_pfkv = pl->off_pfscr = pl->off_pfpart = 0;
+    pl->pf_nsplit = pl->pf_tps = 1;
     if (pl->prefill) {
         pl->off_pfq = off; off = align_up(off + (size_t)R * 512);
         pl->off_pfqm = off; off = align_up(off + (size_t)R * sizeof(PfQMeta));
@@ -1071,13 +1117,39 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
         } else {
             pl->off_pfkv = off; off = align_up(off + (size_t)pl->nseg * pl->pf_ntiles * EA_PF_TILE_BYTES);
         }
-        pl->off_pfscr = off; off = align_up(off + (size_t)pl->nseg * pl->pf_nrb * 512 * 32 * 8);
+        // key splits when the (segment, row block) grid alone leaves CUs idle (one prefill block
+        // fills a CU's LDS): double the splits while the grid is under 256 blocks and every split
+        // keeps at least 16 tiles; a caller's split count is taken as given
+        int ns = 1;
+        if (o->splits > 0) {
+            ns = o->splits;
+        } else {
+            while ((int64_t)pl->nseg * pl->pf_nrb * ns < 256 && pl->pf_ntiles / (2 * ns) >= 16) ns *= 2;
+        }
+        pl->pf_tps = (pl->pf_ntiles + ns - 1) / ns;
+        if (pl->pf_tps < 1) pl->pf_tps = 1;
+        pl->pf_nsplit = (pl->pf_ntiles + pl->pf_tps - 1) / pl->pf_tps;
+        if (pl->pf_nsplit < 1) pl->pf_nsplit = 1;
+        pl->off_pfscr = off;
+        off = align_up(off + (size_t)pl->nseg * pl->pf_nrb * pl->pf_nsplit * 512 * 32 * 8);
+        pl->off_pfpart = off;
+        if (pl->pf_nsplit > 1)
+            off = align_up(off + (size_t)pl->pf_nsplit * R * (sizeof(PfPart) + 128 * 16));
+        pl->nsplit = pl->pf_nsplit;  // the split count this step uses
     }
     pl->total = off;
     return 0;
 }
 
 int herr(hipError_t e) { return e == hipSuccess ? 0 : -100 - (int)e; }
+
+
+// ea_options.force_tier2: every row onto the tier-2 work list (after tier 1)
+int list_all(const Params& P, const ea_options* o, unsigned blocks, hipStream_t st) {
+    if (!o->force_tier2) return 0;
+    hipLaunchKernelGGL(ea_list_all, dim3(blocks), dim3(256), 0, st, P);
+    return herr(hipGetLastError());
+}
 
 }  // namespace
 
@@ -1152,6 +1224,10 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.pfscr = (double*)(ws + pl.off_pfscr);
     P.pf_ntiles = (pl.prefill && o->kv_digits) ? o->kv_digits_tiles : pl.pf_ntiles;
     P.pf_nrb = pl.pf_nrb;
+    P.pf_waves = o->prefill_waves == 4 ? 4 : 8;
+    P.pf_nsplit = pl.pf_nsplit;
+    P.pf_tps = pl.pf_tps;
+    P.pf_part = (void*)(ws + pl.off_pfpart);
     hipStream_t st = (hipStream_t)stream;
     unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
     auto mark = [&](int i) -> int {
@@ -1165,8 +1241,10 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         if ((rc = mark(1))) return rc;
         if ((rc = ea_launch_prefill_main(P, st))) return rc;
         if ((rc = mark(2))) return rc;
+        if ((rc = ea_launch_prefill_combine(P, st))) return rc;
         if ((rc = mark(3))) return rc;
         if (o->tier2) {
+            if ((rc = list_all(P, o, rb4 * 4 / 256 + 1, st))) return rc;
             hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_T2_THREADS), 0, st, P);
             rc = herr(hipGetLastError());
             if (rc) return rc;
@@ -1196,7 +1274,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         const dim3 blk(EA_THREADS);
         const size_t lds = sizeof(SplitSmem);
         int dec = 0;
-        if (!o->timers && !getenv("EA_FORCE_GENERAL")) {
+        if (!o->timers && o->kernel != EA_KERNEL_GENERAL) {
             dec = ea_launch_decode(P, pl.rb, grid, st);
             if (dec < 0) return dec;
         }
@@ -1221,6 +1299,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     if (rc) return rc;
     if ((rc = mark(3))) return rc;
     if (o->tier2) {
+        if ((rc = list_all(P, o, rb4 * 4 / 256 + 1, st))) return rc;
         hipLaunchKernelGGL(ea_tier2, dim3(EA_T2_BLOCKS), dim3(EA_T2_THREADS), 0, st, P);
         rc = herr(hipGetLastError());
         if (rc) return rc;
@@ -1228,19 +1307,132 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     return mark(4);
 }
 
+int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, ea_stream_t stream) {
+    Plan pl;
+    int rc = make_plan(g, o, &pl);
+    if (rc) return rc;
+    if (!bf || !bf->q || !bf->k || !bf->v || !bf->kv_len || !bf->out || !bf->flags) return -1;
+    if (bf->tree_mask && !bf->tree_base) return -1;
+    if (((o->alpha_bits >> 23) & 0xFF) == 0xFF) return -3;
+    if (pl.rows == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return herr(e);
+    std::vector<uint8_t> fl((size_t)pl.rows);
+    if ((e = hipMemcpy(fl.data(), bf->flags, (size_t)pl.rows, hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
+    std::vector<int64_t> todo;
+    for (int64_t r = 0; r < pl.rows; ++r)
+        if (fl[(size_t)r] == 1) todo.push_back(r);
+    if (todo.empty()) return 0;
+    Params P;
+    memset(&P, 0, sizeof(P));
+    P.g = *g;
+    P.q = bf->q; P.k = bf->k; P.v = bf->v;
+    P.seq_len = bf->seq_len; P.kv_len = bf->kv_len; P.bt = bf->block_table; P.bt_off = bf->block_table_offset;
+    P.tree_mask = bf->tree_mask; P.tree_base = bf->tree_base;
+    P.grp = pl.grp; P.pshift = pl.pshift; P.rows = pl.rows;
+    const int d = g->head_dim, dv = g->head_dim_v, T = g->num_tokens, Hq = g->num_q_heads;
+    // visible keys per listed row: the kv_len prefix plus the tree keys
+    std::vector<int64_t> nk(todo.size());
+    int64_t maxk = 0;
+    for (size_t i = 0; i < todo.size(); ++i) {
+        const int64_t row = todo[i], b = row / ((int64_t)T * Hq), t = (row / Hq) % T, tok = b * T + t;
+        int32_t L = 0;
+        uint64_t m = 0;
+        if ((e = hipMemcpy(&L, bf->kv_len + tok, 4, hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
+        if (bf->tree_mask && (e = hipMemcpy(&m, bf->tree_mask + tok, 8, hipMemcpyDeviceToHost)) != hipSuccess)
+            return herr(e);
+        if (L < 0) return -1;
+        nk[i] = (int64_t)L + __builtin_popcountll(m);
+        maxk = nk[i] > maxk ? nk[i] : maxk;
+    }
+    const size_t cap = (size_t)(d + maxk * (int64_t)(d + dv));
+    uint16_t* stage = nullptr;
+    if ((e = hipMalloc(&stage, cap * 2)) != hipSuccess) return herr(e);
+    std::vector<uint16_t> host(cap);
+    const size_t osz = o->out_fp32 ? 4 : 2;
+    int64_t fixed = 0, refused = 0, dom = 0;
+    for (size_t i = 0; i < todo.size() && e == hipSuccess; ++i) {
+        const int64_t row = todo[i], n = nk[i];
+        const int64_t b = row / ((int64_t)T * Hq), t = (row / Hq) % T, hq = row % Hq;
+        const size_t cnt = (size_t)(d + n * (int64_t)(d + dv));
+        const unsigned blocks = (unsigned)std::min<size_t>((cnt + 255) / 256, 4096);
+        hipLaunchKernelGGL(ea_gather_row, dim3(blocks), dim3(256), 0, st, P, row, n, stage);
+        if ((e = hipGetLastError()) != hipSuccess) break;
+        if ((e = hipMemcpyAsync(host.data(), stage, cnt * 2, hipMemcpyDeviceToHost, st)) != hipSuccess) break;
+        if ((e = hipStreamSynchronize(st)) != hipSuccess) break;
+        uint8_t res[EA_MAXDV * 4];  // dv bf16 (uint16) or fp32 (uint32) patterns, as exact_row writes them
+        const int x = eax::exact_row(host.data(), d, host.data() + d, host.data() + d + n * d, n, dv, o->alpha_bits,
+                                     o->out_fp32, res, nullptr);
+        uint8_t flag = x == eax::EAX_OK ? 0 : 2;
+        if (x != eax::EAX_OK) memset(res, 0, sizeof(res));
+        fixed += x == eax::EAX_OK;
+        refused += x == eax::EAX_REFUSED;
+        dom += x == eax::EAX_DOMAIN;
+        const int64_t obase = b * g->o_seq_stride + t * g->o_tok_stride + hq * g->o_head_stride;
+        char* dst = (char*)bf->out + obase * (int64_t)osz;
+        e = hipMemcpy(dst, res, (size_t)dv * osz, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(bf->flags + row, &flag, 1, hipMemcpyHostToDevice);
+    }
+    (void)hipFree(stage);
+    if (e != hipSuccess) return herr(e);
+    if (o->stats) {
+        int64_t hs[16];
+        if ((e = hipMemcpy(hs, o->stats, sizeof(hs), hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
+        hs[13] += fixed;
+        hs[14] += refused;
+        hs[4] += refused + dom;
+        if ((e = hipMemcpy(o->stats, hs, sizeof(hs), hipMemcpyHostToDevice)) != hipSuccess) return herr(e);
+    }
+    return 0;
+}
+
+int ea_exact_row(const uint16_t* q, int d, const uint16_t* k, const uint16_t* v, int64_t n, int dv,
+                 uint32_t alpha_bits, int fp32_out, void* out, uint32_t* t_bits, int32_t* w_m, int64_t* w_e) {
+    if (!q || !out || d <= 0 || dv <= 0 || n < 0 || (n > 0 && (!k || !v))) return -1;
+    eax::KeyTrace tr{t_bits, w_m, w_e};
+    return eax::exact_row(q, d, k, v, n, dv, alpha_bits, fp32_out ? 1 : 0, out,
+                          (t_bits || w_m || w_e) ? &tr : nullptr);
+}
+
+float ea_round_ratio(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo, int E, int neg, int fp32,
+                     int* overflow) {
+    int ov = 0;
+    const uint32_t bits = eax::round_ratio_bits(a_hi, a_lo, b_hi, b_lo, E, neg, fp32, &ov);
+    if (overflow) *overflow = ov;
+    const uint32_t f = fp32 ? bits : (bits << 16);
+    float r;
+    memcpy(&r, &f, 4);
+    return r;
+}
+
 int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
-                     int dv, uint32_t alpha_bits, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
+                     int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
                      int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
                      uint8_t* flags, int64_t* stats) {
-    (void)acc_bits; (void)tile; (void)order_seed; (void)nthreads;
-    if (d <= 0 || d > EA_MAXD || dv <= 0 || dv > EA_MAXDV || splits <= 0 || rows < 0 || nkeys < 0) return -1;
-    if ((d & 7) || (dv & 1)) return -1;
+    (void)order_seed; (void)nthreads;
+    // the reference's argument checks, in its order (csrc/exact_attention_cpu.cpp:589-592)
+    if (d <= 0 || d > EA_MAXD || dv <= 0 || dv > EA_MAXDV || tile <= 0 || splits <= 0) return -1;
+    if (acc_bits != 64 && acc_bits != 128) return -2;
+    uint32_t alpha_bits;
+    memcpy(&alpha_bits, &alpha, 4);
     if (((alpha_bits >> 23) & 0xFF) == 0xFF) return -3;
+    if ((d & 7) || (dv & 1) || rows < 0 || nkeys < 0) return -1;
     if (rows == 0) return 0;
+    if (!q || !row_ptr || !out || !flags || (nkeys > 0 && (!k || !v))) return -1;
     // Each CSR row is one sequence whose page table is its key list (page size 1).
-    int64_t maxn = 0, nnz = row_ptr[rows];
-    for (int64_t r = 0; r < rows; ++r) maxn = row_ptr[r + 1] - row_ptr[r] > maxn ? row_ptr[r + 1] - row_ptr[r] : maxn;
+    int64_t maxn = 0;
+    if (row_ptr[0] < 0) return -1;
+    for (int64_t r = 0; r < rows; ++r) {
+        const int64_t len = row_ptr[r + 1] - row_ptr[r];
+        if (len < 0) return -1;
+        maxn = len > maxn ? len : maxn;
+    }
+    const int64_t nnz = row_ptr[rows] - row_ptr[0];
     if (maxn > INT32_MAX / 2 || nkeys > INT32_MAX) return -1;
+    if (nnz > 0 && !key_idx) return -1;
+    for (int64_t j = row_ptr[0]; j < row_ptr[rows]; ++j)
+        if (key_idx[j] < 0 || key_idx[j] >= nkeys) return -1;  // the kernels gather through it
     ea_geometry g;
     memset(&g, 0, sizeof(g));
     g.num_seqs = (int32_t)rows; g.num_tokens = 1; g.num_q_heads = 1; g.num_kv_heads = 1;
@@ -1252,7 +1444,7 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
     g.page_size = 1; g.block_table_stride = 0; g.max_seq_len = (int32_t)maxn;
     ea_options o;
     memset(&o, 0, sizeof(o));
-    o.alpha_bits = alpha_bits; o.out_fp32 = fp32_out; o.splits = splits; o.tier2 = 1;
+    o.alpha_bits = alpha_bits; o.out_fp32 = fp32_out ? 1 : 0; o.splits = splits; o.tier2 = 1;
     size_t ws_bytes = 0;
     int32_t ns = 0;
     int rc = ea_hip_workspace_size(&g, &o, &ws_bytes, &ns);
@@ -1260,11 +1452,11 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
     std::vector<int32_t> bt((size_t)(nnz > 0 ? nnz : 1)), sl((size_t)rows);
     std::vector<int64_t> bo((size_t)rows);
     for (int64_t r = 0; r < rows; ++r) {
-        sl[r] = (int32_t)(row_ptr[r + 1] - row_ptr[r]);
-        bo[r] = row_ptr[r];
+        sl[(size_t)r] = (int32_t)(row_ptr[r + 1] - row_ptr[r]);
+        bo[(size_t)r] = row_ptr[r] - row_ptr[0];
     }
-    for (int64_t j = 0; j < nnz; ++j) bt[j] = (int32_t)key_idx[j];
-    size_t osz = fp32_out ? 4 : 2;
+    for (int64_t j = 0; j < nnz; ++j) bt[(size_t)j] = (int32_t)key_idx[row_ptr[0] + j];
+    const size_t osz = fp32_out ? 4 : 2;
     void *dq = 0, *dk = 0, *dv_ = 0, *dbt = 0, *dbo = 0, *dsl = 0, *dout = 0, *dfl = 0, *dws = 0, *dst = 0;
     hipError_t e = hipSuccess;
 #define EA_TRY(x) do { e = (x); if (e != hipSuccess) goto done; } while (0)
@@ -1301,10 +1493,31 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
     EA_TRY(hipDeviceSynchronize());
     EA_TRY(hipMemcpy(out, dout, (size_t)rows * dv * osz, hipMemcpyDeviceToHost));
     EA_TRY(hipMemcpy(flags, dfl, (size_t)rows, hipMemcpyDeviceToHost));
-    {
+    if (stats) {
         int64_t hs[16];
         EA_TRY(hipMemcpy(hs, dst, sizeof(hs), hipMemcpyDeviceToHost));
-        if (stats) stats[2] += hs[1];
+        stats[0] += hs[5];
+        stats[1] += hs[6];
+        stats[2] += hs[7];
+    }
+    {
+        // rows the device tiers left uncertified: the host exact tier on the caller's arrays
+        std::vector<uint16_t> kr, vr;
+        for (int64_t r = 0; r < rows; ++r) {
+            if (flags[r] != 1) continue;
+            const int64_t j0 = row_ptr[r], n = row_ptr[r + 1] - row_ptr[r];
+            kr.resize((size_t)(n * d));
+            vr.resize((size_t)(n * dv));
+            for (int64_t j = 0; j < n; ++j) {
+                memcpy(&kr[(size_t)(j * d)], k + key_idx[j0 + j] * d, (size_t)d * 2);
+                memcpy(&vr[(size_t)(j * dv)], v + key_idx[j0 + j] * dv, (size_t)dv * 2);
+            }
+            char* dst_row = (char*)out + (size_t)r * dv * osz;
+            const int x = eax::exact_row(q + r * d, d, kr.data(), vr.data(), n, dv, alpha_bits, fp32_out ? 1 : 0,
+                                         dst_row, nullptr);
+            if (x != eax::EAX_OK) memset(dst_row, 0, (size_t)dv * osz);
+            flags[r] = x == eax::EAX_OK ? 0 : 2;
+        }
     }
 done:
     (void)hipFree(dq); (void)hipFree(dk); (void)hipFree(dv_); (void)hipFree(dbt); (void)hipFree(dbo);

@@ -70,6 +70,10 @@ struct Params {
     int32_t kvd_span;
     int32_t pf_kv_cached;  // 1: pfkv is the caller's digit cache, already sliced
     const int32_t* pf_kv_slot;  // with pf_kv_cached: cache slot of each sequence (NULL: b)
+    int32_t pf_waves;           // prefill block shape: 8 waves (default) or 4
+    int32_t pf_nsplit;          // key splits per (segment, row block); 1: rounding in ea_pf_main
+    int32_t pf_tps;             // 64-key tiles per key split
+    void* pf_part;              // pf_nsplit > 1: the splits' partials (PfPart, then PfEntry arrays)
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
@@ -185,12 +189,25 @@ struct PfTileMeta {
     int32_t pad;
     double EVt;       // (2^38 + 1) / 2 * (inexact V elements of the tile, all channels)
 };
+// A key split's partial of one row (pf_nsplit > 1): the row's base exponent, its visible keys with
+// a weight, bit 0 a domain error and bit 1 an undecided pair, Z in units 2^base. Followed in the
+// workspace by the (N, bound) pairs of every (split, row, channel), also in units 2^base.
+struct PfPart {
+    int32_t base;
+    int32_t nv;
+    int32_t fl;
+    int32_t pad;
+    double z;
+    double pad2;
+};
 // Returns 1 when the prefill path handles this geometry (and sets the tile and block counts),
-// 0 otherwise.
-int ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb);
+// 0 otherwise. kernel: the ea_options.kernel choice (EA_KERNEL_*).
+int ea_prefill_eligible(const ea_geometry& g, int grp, int kernel, int* ntiles, int* nrb);
 // Enqueue the slicing kernels (q rows, K/V tiles), then the prefill kernel; 0 or -100 - e.
 int ea_launch_prefill(const Params& P, hipStream_t st);
 int ea_launch_prefill_main(const Params& P, hipStream_t st);
+// With key splits (P.pf_nsplit > 1): the merge of the splits' partials and the rounding.
+int ea_launch_prefill_combine(const Params& P, hipStream_t st);
 // Enqueue the re-slicing of the cached digit tiles P.kvd_begin / kvd_end name; 0 or -100 - e.
 int ea_launch_kv_digits(const Params& P, hipStream_t st);
 

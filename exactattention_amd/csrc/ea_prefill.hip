@@ -678,7 +678,8 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     const int g = lane >> 4, j = lane & 15;
     const int nseg = P.nseg;
     const int seg = blockIdx.x % nseg;
-    const int rbk = P.pf_nrb - 1 - (int)(blockIdx.x / nseg);
+    const int split = (int)(blockIdx.x / nseg) % P.pf_nsplit;  // key split (tile range) of the block
+    const int rbk = P.pf_nrb - 1 - (int)(blockIdx.x / nseg) / P.pf_nsplit;
     const int Hkv = P.g.num_kv_heads;
     const int64_t b = seg / Hkv;
     const int hk = seg % Hkv;
@@ -754,6 +755,9 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     __syncthreads();  // s_kend final, tables and q digits visible
     const int kend = s_kend;
     const int ntiles = (kend + 63) >> 6;
+    // this block's key split: tiles [t0, t1) of the rows' visible range
+    const int t0 = min(split * P.pf_tps, ntiles), t1 = min(t0 + P.pf_tps, ntiles);
+    const int nt = t1 - t0;
     const double* const T1s = sT1;
     const double* const T2 = sT2;
 
@@ -956,7 +960,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const PfTileMeta* const TMc = (const PfTileMeta*)(PA ? sM1 : sM0);
         const PfTileMeta* const TMp = (const PfTileMeta*)(PA ? sM0 : sM1);
         const uint32_t aMn = PA ? aM0 : aM1;        // metadata of tile it + 1
-        const bool k_next = it + 1 < ntiles;
+        const bool k_next = it + 1 < t1;
         tick(7);
         // every DMA landed: K(it) and its metadata, and V(it - 1) (the P.V of this step reads it)
         wait_vm<0>();
@@ -987,7 +991,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         };
         scores();
         tick(1);
-        if (it > 0) rebase_digits(evp);
+        if (it > t0) rebase_digits(evp);
         tick(2);
         // every wave has read the K planes of tile it and written the weight digits of tile it - 1:
         // K(it + 1) with its metadata and V(it) start loading
@@ -1002,8 +1006,8 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             score_fold(sacc[kk], lk4[kk], xs[kk]);
         }
         v4i Wd[5];
-        read_wd(Wd);  // zero at it = 0
-        if (it > 0) ++ep_tiles;
+        read_wd(Wd);  // zero at it = t0
+        if (it > t0) ++ep_tiles;
         tick(3);
         // ---- per-pair metadata, score bounds and visibility of tile it
         v4i vl4[NKT];
@@ -1056,7 +1060,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                     }
                 }
         }
-        // ---- P.V of tile it - 1 (zero digits at it = 0) beside the certification of tile it
+        // ---- P.V of tile it - 1 (zero digits at it = t0) beside the certification of tile it
         v4i Mk[NKT], Ek[NKT];
         uint32_t slowmask = 0;  // pairs the fast path left undecided (cold path below)
         int gm = INT_MIN;
@@ -1143,18 +1147,18 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     };
 
     wait_vm<0>();  // the prologue's global loads: from here on vmcnt counts DMAs (and folds)
-    if (ntiles > 0) issue_k(0, aM0);
+    if (nt > 0) issue_k(t0, aM0);
     tick(15);
-    for (int it = 0; it < ntiles; it += 2) {
+    for (int it = t0; it < t1; it += 2) {
         step(PfPar<0>{}, it);
-        if (it + 1 < ntiles) step(PfPar<1>{}, it + 1);
+        if (it + 1 < t1) step(PfPar<1>{}, it + 1);
     }
     tick(7);
     // ---- drain: digits and P.V of the last tile
-    if (ntiles > 0) {
+    if (nt > 0) {
         wait_vm<0>();
         pf_bar();
-        const bool odd = (ntiles - 1) & 1;
+        const bool odd = (nt - 1) & 1;
         const PfTileMeta* TMl = (const PfTileMeta*)(odd ? sM1 : sM0);
         double evp[NCT];
 #pragma unroll
@@ -1191,10 +1195,69 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         }
     }
     tick(10);
+    if (P.pf_nsplit > 1) {
+        // ---- key splits: this split's (N, bound) per (row, channel) and (base, nv, flags, Z) per
+        // row, in units 2^base; ea_pf_combine merges the splits and rounds. Every record a
+        // combine reads is written here (a split with no tile writes nv = 0 and its flags).
+        PfPart* const parts = (PfPart*)P.pf_part;
+        double2* const ent = (double2*)(parts + (int64_t)P.pf_nsplit * P.rows);
+        if (nt > 0) {
+            int nf = nf_pair + __shfl_xor(nf_pair, 16, 64);
+            nf += __shfl_xor(nf, 32, 64);
+            const double omit = (double)ep_tiles * 0x1p20;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int lri = rbk * RPB + rg * 16 + 4 * g + i;
+                if (lri >= P.r_seg) continue;
+                int ti;
+                const int64_t gr = seg_row(P, b, hk, lri, &ti);
+                const double fri = 0x1p29 * (double)__shfl(nf, 4 * g + i, 64);
+#pragma unroll
+                for (int cc = 0; cc < NCT; ++cc) {
+                    double en;
+                    double nn = epoch_sum(cc, i, fri, omit, &en);
+                    if (had_fold) {
+                        const double2 o = *(const double2*)(scr + 2 * (4 * cc + i));
+                        nn += o.x;
+                        en += o.y;
+                    }
+                    en += fabs(nn) * 0x1p-52;
+                    ent[((int64_t)split * P.rows + gr) * 128 + 16 * (NCT * hh + cc) + j] = make_double2(nn, en);
+                }
+            }
+        }
+        if (g == 0 && hh == 0 && rvalid) {
+            PfPart pr;
+            pr.base = nv > 0 ? base : INT_MIN;
+            pr.nv = nv;
+            pr.fl = (dom ? 1 : 0) | (unc ? 2 : 0);
+            pr.pad = 0;
+            pr.z = z;
+            pr.pad2 = 0.0;
+            parts[(int64_t)split * P.rows + grow] = pr;
+        }
+        if (P.stats) {
+            const int st5 = wave_sum_i(nunc_s), st6 = wave_sum_i(nunc_w), st8 = wave_sum_i(nslow);
+            // rows are counted once, by the blocks of split 0
+            const int cr = wave_sum_i((split == 0 && g == 0 && hh == 0 && rvalid) ? 1 : 0);
+            if (lane == 0) {
+                if (st5) atomicAdd((unsigned long long*)&P.stats[5], (unsigned long long)st5);
+                if (st6) atomicAdd((unsigned long long*)&P.stats[6], (unsigned long long)st6);
+                if (st8) atomicAdd((unsigned long long*)&P.stats[8], (unsigned long long)st8);
+                if (nfold) atomicAdd((unsigned long long*)&P.stats[11], (unsigned long long)nfold);
+                if (ncold) atomicAdd((unsigned long long*)&P.stats[12], (unsigned long long)ncold);
+                if (cr) {
+                    atomicAdd((unsigned long long*)&P.stats[0], (unsigned long long)cr);
+                    atomicAdd((unsigned long long*)&P.stats[10], (unsigned long long)cr);
+                }
+            }
+        }
+        return;
+    }
     // ---- the last epoch plus the earlier ones, then RN(N/Z) per (row, channel), certified:
     // q = N * RN(1/Z) (two roundings: below 2^-51.9 |q|, inside the 2^-51 |q| term) and
     // delta >= |N/Z - q| from the N bound en and the Z bound eZ
-    if (ntiles > 0) {
+    if (nt > 0) {
         double2 prev[4 * NCT];
 #pragma unroll
         for (int e = 0; e < 4 * NCT; ++e) prev[e] = had_fold ? *(const double2*)(scr + 2 * e) : make_double2(0.0, 0.0);
@@ -1280,7 +1343,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
 #pragma unroll
         for (int i = 9; i < 16; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
-        atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)ntiles);
+        atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)nt);
     }
     if (P.stats) {
         const int st5 = wave_sum_i(nunc_s), st6 = wave_sum_i(nunc_w), st8 = wave_sum_i(nslow);
@@ -1292,7 +1355,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             if (ncold) atomicAdd((unsigned long long*)&P.stats[12], (unsigned long long)ncold);
         }
     }
-    if (ntiles == 0) {
+    if (nt == 0) {
         // no key visible to any row of the block: every row is empty (+0) or a q domain error
         nv = 0;
         unc = 0;
@@ -1362,16 +1425,93 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Merge of the key splits' partials (pf_nsplit > 1) and the certified final rounding, one block of
+// 128 threads per row (thread = channel). Per split s with keys: Z_s and N_s in units 2^base_s with
+// bounds (nv_s + 8) u' Z_s + (nv_s + 64) 2^-1074 (the sums of the split's weights, as the kernel's
+// own epilogue bounds them) and en_s. Rescaled to the largest base B by exact powers of two (an
+// underflowing rescale loses at most 2^-1074 per term, added), then summed: ns - 1 more roundings
+// of at most u of the sum of magnitudes. q = N RN(1/Z) and its radius as in ea_pf_main's epilogue,
+// then certify_round; rows that fail go to the tier-2 work list.
+// ------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(128) ea_pf_combine(Params P) {
+    const int64_t row = blockIdx.x;
+    const int c = threadIdx.x;
+    const int ns = P.pf_nsplit;
+    const PfPart* const parts = (const PfPart*)P.pf_part;
+    const double2* const ent = (const double2*)(parts + (int64_t)ns * P.rows);
+    int B = INT_MIN, nv = 0, fl = 0;
+    for (int s = 0; s < ns; ++s) {
+        const PfPart pr = parts[(int64_t)s * P.rows + row];
+        fl |= pr.fl;
+        if (pr.nv > 0) {
+            B = max(B, pr.base);
+            nv += pr.nv;
+        }
+    }
+    uint32_t bits = 0;
+    bool fin = false;
+    if (nv > 0 && !fl) {
+        double z = 0.0, ezs = 0.0, nn = 0.0, an = 0.0, en = 0.0;
+        for (int s = 0; s < ns; ++s) {
+            const PfPart pr = parts[(int64_t)s * P.rows + row];
+            if (pr.nv <= 0) continue;
+            const int dsh = max(pr.base - B, -1100);
+            const double zs = ldexp(pr.z, dsh);
+            z += zs;
+            ezs += (double)(pr.nv + 8) * PF_U * zs + (double)(pr.nv + 65) * 0x1p-1074;
+            const double2 e = ent[((int64_t)s * P.rows + row) * 128 + c];
+            const double v = ldexp(e.x, dsh);
+            nn += v;
+            an += fabs(v);
+            en += ldexp(e.y, dsh) + 0x1p-1074;
+        }
+        // the merge's own roundings (ns - 1 additions each for Z and N, sums of positive bounds
+        // rounded up by the (1 + 2^-40) factors)
+        const double eZ = (ezs + (double)ns * PF_U * z) * (1.0 + 0x1p-40);
+        en = (en + (double)ns * 0x1p-52 * an) * (1.0 + 0x1p-40);
+        const bool zok = z > 2.0 * eZ && isfinite(z);
+        const double rz = zok ? 1.0 / z : 0.0, rze = zok ? 1.0 / (z - eZ) : 0.0;
+        const double q = nn * rz;
+        double delta = (en * (1.0 + 0x1p-40) + fabs(q) * eZ) * rze * (1.0 + 0x1p-40) + fabs(q) * 0x1p-51 + 0x1p-1070;
+        if (!isfinite(q) || !isfinite(delta) || !zok) delta = __builtin_inf();
+        fin = !certify_round(q, delta, P.out_fp32, &bits);
+        if (fin) bits = 0;
+    }
+    const bool anyfin = __syncthreads_or(fin) != 0;  // every thread reaches this barrier
+    const int flag = (fl & 1) ? 2 : (((fl & 2) || anyfin) ? 1 : 0);
+    const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
+    const int64_t b = row / ((int64_t)T * Hq);
+    const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
+    const int64_t o = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride + c;
+    if (flag) bits = 0;
+    if (c < P.g.head_dim_v) {
+        if (P.out_fp32) ((uint32_t*)P.out)[o] = bits;
+        else ((uint16_t*)P.out)[o] = (uint16_t)bits;
+    }
+    if (c == 0) {
+        P.flags[row] = (uint8_t)flag;
+        if (flag == 1) {
+            const int slot = atomicAdd(P.wl_cnt, 1);
+            P.wl[slot] = (int32_t)row;
+        }
+        if (P.stats && flag) {
+            atomicAdd((unsigned long long*)&P.stats[1], 1ull);
+            if (flag == 2) atomicAdd((unsigned long long*)&P.stats[4], 1ull);
+            if (flag == 1 && !(fl & 2)) atomicAdd((unsigned long long*)&P.stats[7], 1ull);
+        }
+    }
+}
+
 namespace {
 // kernel shape: 32 rows per block; 8 waves (2 row groups x 4 waves, 2 waves per SIMD, 256
-// registers each) by default, EA_PF_SHAPE=4 selects 4 waves (2 x 2, 1 wave per SIMD)
+// registers each) by default, ea_options.prefill_waves = 4 selects 4 waves (2 x 2, 1 wave per SIMD)
 constexpr int PF_RPB = 32;
-int pf_waves() { return (getenv("EA_PF_SHAPE") && getenv("EA_PF_SHAPE")[0] == '4') ? 4 : 8; }
 }  // namespace
 
-int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int* ntiles, int* nrb) {
-    if (getenv("EA_PREFILL") && getenv("EA_PREFILL")[0] == '0') return 0;
-    const bool force = getenv("EA_PREFILL") && getenv("EA_PREFILL")[0] == '1';
+int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int kernel, int* ntiles, int* nrb) {
+    if (kernel == EA_KERNEL_DECODE || kernel == EA_KERNEL_GENERAL) return 0;
+    const bool force = kernel == EA_KERNEL_PREFILL;
     if (g.head_dim != 128 || g.head_dim_v != 128) return 0;
     const int64_t r_seg = (int64_t)g.num_tokens * grp;
     // Rows of one (sequence, KV head) that fill a 32-row block (64 tokens, or fewer tokens with a
@@ -1419,8 +1559,8 @@ int ea::ea_launch_kv_digits(const Params& P, hipStream_t st) {
 int ea::ea_launch_prefill_main(const Params& P, hipStream_t st) {
     Params Pc = P;
     if (P.nseg > 0 && P.pf_nrb > 0) {
-        const dim3 grid((unsigned)(P.nseg * P.pf_nrb));
-        if (pf_waves() == 8) {
+        const dim3 grid((unsigned)(P.nseg * P.pf_nrb * P.pf_nsplit));
+        if (P.pf_waves != 4) {
             if (P.timers) hipLaunchKernelGGL((ea_pf_main<8, true>), grid, dim3(512), PF_LDS, st, Pc);
             else hipLaunchKernelGGL((ea_pf_main<8, false>), grid, dim3(512), PF_LDS, st, Pc);
         } else {
@@ -1431,4 +1571,12 @@ int ea::ea_launch_prefill_main(const Params& P, hipStream_t st) {
         if (e != hipSuccess) return -100 - (int)e;
     }
     return 0;
+}
+
+int ea::ea_launch_prefill_combine(const Params& P, hipStream_t st) {
+    if (P.pf_nsplit <= 1 || P.rows == 0) return 0;
+    Params Pc = P;
+    hipLaunchKernelGGL(ea_pf_combine, dim3((unsigned)P.rows), dim3(128), 0, st, Pc);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : -100 - (int)e;
 }

@@ -42,14 +42,20 @@ class Options(ctypes.Structure):
     _fields_ = [("alpha_bits", ctypes.c_uint32), ("out_fp32", ctypes.c_int32), ("splits", ctypes.c_int32),
                 ("tier2", ctypes.c_int32), ("merge_order", P), ("stats", P), ("events", P), ("timers", P),
                 ("kv_digits", P), ("kv_digits_tiles", ctypes.c_int32), ("pad1", ctypes.c_int32),
-                ("kv_digits_slot", P)]
+                ("kv_digits_slot", P), ("force_tier2", ctypes.c_int32), ("kernel", ctypes.c_int32),
+                ("prefill_waves", ctypes.c_int32), ("pad2", ctypes.c_int32)]
+
+
+# ea_options.kernel (include/exactattn_hip.h EA_KERNEL_*)
+KERNELS = {"auto": 0, "prefill": 1, "decode": 2, "general": 3}
 
 
 EA_PF_TILE_BYTES = 69632  # one 64-key digit tile (ea_params.h)
 
 STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
          "undecided_weights", "uncertified_final", "slow_path_scores",
-         "decode_kernel_rows", "prefill_kernel_rows", "prefill_epoch_folds", "prefill_cold_waves"]
+         "decode_kernel_rows", "prefill_kernel_rows", "prefill_epoch_folds", "prefill_cold_waves",
+         "host_exact_rows", "host_exact_refused"]
 
 
 def available() -> bool:
@@ -70,10 +76,19 @@ def load():
         lib.ea_hip_attention.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), ctypes.POINTER(Options),
                                          P, ctypes.c_size_t, P]
         lib.ea_hip_attention.restype = ctypes.c_int
+        # the reference's ea_attention_cpu argtypes (src/exactattn/cpu.py:35-38)
         lib.ea_attention_hip.argtypes = [P, ctypes.c_int64, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int,
-                                         ctypes.c_uint32, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_float, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_uint64, ctypes.c_int, P, P, P]
         lib.ea_attention_hip.restype = ctypes.c_int
+        lib.ea_round_ratio.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)]
+        lib.ea_round_ratio.restype = ctypes.c_float
+        lib.ea_hip_exact_rows.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), ctypes.POINTER(Options),
+                                          P]
+        lib.ea_hip_exact_rows.restype = ctypes.c_int
+        lib.ea_exact_row.argtypes = [P, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32,
+                                     ctypes.c_int, P, P, P, P]
+        lib.ea_exact_row.restype = ctypes.c_int
         lib.ea_hip_kat_weight.argtypes = [ctypes.c_int64] + [P] * 7 + [P]
         lib.ea_hip_kat_weight.restype = ctypes.c_int
         lib.ea_hip_kat_round.argtypes = [ctypes.c_int64, P, P, ctypes.c_int32, P, P, P]
@@ -107,9 +122,9 @@ def _stream_ptr(torch):
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def workspace_size(g: dict, splits: int = 0, out_fp32: bool = False) -> tuple[int, int]:
+def workspace_size(g: dict, splits: int = 0, out_fp32: bool = False, kernel: int = 0) -> tuple[int, int]:
     lib = load()
-    o = Options(splits=splits, out_fp32=int(out_fp32), tier2=1)
+    o = Options(splits=splits, out_fp32=int(out_fp32), tier2=1, kernel=kernel)
     nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
     _check(lib.ea_hip_workspace_size(ctypes.byref(geometry(g)), ctypes.byref(o), ctypes.byref(nb), ctypes.byref(ns)),
            "ea_hip_workspace_size")
@@ -120,13 +135,16 @@ class DeviceProblem:
     """A problem's arrays resident on the GPU, plus output, flags, workspace and stats buffers.
     Built once; `launch_hip` then runs steps on it with no allocation."""
 
-    def __init__(self, prob: dict, out: str = "bf16", splits: int = 0, device: str = "cuda"):
+    def __init__(self, prob: dict, out: str = "bf16", splits: int = 0, device: str = "cuda", kernel: str = "auto",
+                 prefill_waves: int = 0):
         import torch
         self.torch = torch
         self.prob = prob
         self.geom = dict(prob["geom"])
         self.out_fp32 = out == "fp32"
         self.splits = splits
+        self.kernel = KERNELS[kernel]
+        self.prefill_waves = int(prefill_waves)
         dev = torch.device(device)
 
         def t(a, dt=None):
@@ -145,7 +163,7 @@ class DeviceProblem:
         self.rows = rows
         self.out = torch.empty(prob["out_shape"], dtype=torch.int32 if self.out_fp32 else torch.int16, device=dev)
         self.flags = torch.empty(rows, dtype=torch.uint8, device=dev)
-        nb, self.nsplit = workspace_size(self.geom, splits, self.out_fp32)
+        nb, self.nsplit = workspace_size(self.geom, splits, self.out_fp32, self.kernel)
         self.workspace = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
         self.ws_bytes = nb
         self.stats = torch.zeros(16, dtype=torch.int64, device=dev)
@@ -159,24 +177,40 @@ class DeviceProblem:
 TIMER_PHASES = ["prologue", "tile_barrier", "scores", "score_barrier", "weights", "pv", "epilogue", "tiles"]
 
 
+def options(dp: "DeviceProblem", alpha_bits: int, merge_order=None, tier2: bool = True, events=None, timers=None,
+            kv_digits=None, force_tier2: bool = False) -> Options:
+    """The ea_options of a step on dp (its kernel choice and prefill block shape come from dp)."""
+    mo = merge_order if (merge_order is not None and hasattr(merge_order, "data_ptr")) else None
+    return Options(alpha_bits=alpha_bits, out_fp32=int(dp.out_fp32), splits=dp.splits, tier2=int(tier2),
+                   merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr(),
+                   events=None if events is None else ctypes.cast(events, P),
+                   timers=None if timers is None else timers.data_ptr(),
+                   kv_digits=None if kv_digits is None else kv_digits.buf.data_ptr(),
+                   kv_digits_tiles=0 if kv_digits is None else kv_digits.tiles,
+                   force_tier2=int(force_tier2), kernel=dp.kernel, prefill_waves=dp.prefill_waves)
+
+
 def launch_hip(dp: DeviceProblem, alpha_bits: int, merge_order=None, tier2: bool = True, events=None,
-               timers=None, kv_digits=None) -> None:
+               timers=None, kv_digits=None, force_tier2: bool = False) -> None:
     """Enqueue one step on torch's current stream (no sync, no host copies, no allocation).
     `events`: optional ctypes array of 5 hipEvent_t handles recorded between the kernels.
-    `kv_digits`: optional KVDigits cache; the int8 prefill path then reads its K/V tiles there."""
+    `kv_digits`: optional KVDigits cache; the int8 prefill path then reads its K/V tiles there.
+    `force_tier2`: every row through the device tier 2 (tests of the exact tier)."""
     lib = load()
-    mo = None
-    if merge_order is not None:
-        mo = merge_order if hasattr(merge_order, "data_ptr") else None
-    o = Options(alpha_bits=alpha_bits, out_fp32=int(dp.out_fp32), splits=dp.splits, tier2=int(tier2),
-                merge_order=None if mo is None else mo.data_ptr(), stats=dp.stats.data_ptr(),
-                events=None if events is None else ctypes.cast(events, P),
-                timers=None if timers is None else timers.data_ptr(),
-                kv_digits=None if kv_digits is None else kv_digits.buf.data_ptr(),
-                kv_digits_tiles=0 if kv_digits is None else kv_digits.tiles)
+    o = options(dp, alpha_bits, merge_order, tier2, events, timers, kv_digits, force_tier2)
     b = dp.buffers()
     _check(lib.ea_hip_attention(ctypes.byref(dp._geom_c), ctypes.byref(b), ctypes.byref(o), dp.workspace.data_ptr(),
                                 dp.ws_bytes, _stream_ptr(dp.torch)), "ea_hip_attention")
+
+
+def exact_rows(dp: DeviceProblem, alpha_bits: int) -> None:
+    """The host exact tier on dp's last step: waits for torch's current stream, recomputes every
+    row left at flag 1 exactly on the host and writes its bits and flag (ea_hip_exact_rows)."""
+    lib = load()
+    o = options(dp, alpha_bits)
+    b = dp.buffers()
+    _check(lib.ea_hip_exact_rows(ctypes.byref(dp._geom_c), ctypes.byref(b), ctypes.byref(o), _stream_ptr(dp.torch)),
+           "ea_hip_exact_rows")
 
 
 class KVDigits:
@@ -216,34 +250,40 @@ def merge_order_tensor(order, nsplit: int, device="cuda"):
 
 
 def attention_problem(prob: dict, alpha, out: str = "bf16", splits: int = 0, merge_order=None, tier2: bool = True,
-                      fallback: bool = True, device: str = "cuda"):
+                      fallback: bool = True, device: str = "cuda", kernel: str = "auto", force_tier2: bool = False,
+                      prefill_waves: int = 0):
     """Run a problem on the GPU. Returns (out bits shaped (B, T, Hq, dv): uint16 for bf16, uint32
-    for fp32; flags (rows,) uint8; stats dict). With fallback=True, flag 2 raises
-    ExactAttentionDomainError and flag 1 raises ExactAttentionUncertifiedError."""
+    for fp32; flags (rows,) uint8; stats dict). fallback=False returns the device tiers' flags as
+    they are. With fallback=True rows the device tiers leave at flag 1 are recomputed by the host
+    exact tier (ea_hip_exact_rows, counted in stats["host_exact_rows"]), and flag 2 raises
+    ExactAttentionDomainError, as the reference's backends do (src/exactattn/cpu.py:103-108)."""
     import torch
     alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
-    dp = DeviceProblem(prob, out, splits, device)
+    dp = DeviceProblem(prob, out, splits, device, kernel, prefill_waves)
     mo = merge_order_tensor(merge_order, dp.nsplit, device) if merge_order is not None else None
-    launch_hip(dp, int(alpha_bits), mo, tier2)
+    launch_hip(dp, int(alpha_bits), mo, tier2, force_tier2=force_tier2)
     torch.cuda.synchronize()
+    flags = dp.flags.cpu().numpy()
+    if fallback and np.any(flags == 1):
+        exact_rows(dp, int(alpha_bits))
+        torch.cuda.synchronize()
+        flags = dp.flags.cpu().numpy()
     res = dp.out.cpu().numpy()
     res = res.view(np.uint32) if dp.out_fp32 else res.view(np.uint16)
-    flags = dp.flags.cpu().numpy()
     st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
     st["nsplit"] = dp.nsplit
     if fallback:
         if np.any(flags == 2):
-            raise ExactAttentionDomainError(f"non-finite input or fp32 logit overflow in rows "
-                                            f"{np.flatnonzero(flags == 2)[:8].tolist()}")
+            raise ExactAttentionDomainError(f"non-finite input, fp32 logit overflow or an exponent spread past "
+                                            f"2^20 in rows {np.flatnonzero(flags == 2)[:8].tolist()}")
         if np.any(flags == 1):
-            raise ExactAttentionUncertifiedError(f"rows {np.flatnonzero(flags == 1)[:8].tolist()} not certified "
-                                                 "by any device tier")
+            raise ExactAttentionUncertifiedError(f"rows {np.flatnonzero(flags == 1)[:8].tolist()} not certified")
     return res, flags, st
 
 
-def ea_attention_hip(q, k, v, alpha_bits, row_ptr, key_idx, out="bf16", splits=8):
-    """The drop-in C entry point (host pointers, same arguments as the reference's
-    ea_attention_cpu). Returns (out bits, flags, stats[3])."""
+def ea_attention_hip(q, k, v, alpha, row_ptr, key_idx, out="bf16", splits=8, acc_bits=64, tile=64):
+    """The drop-in C entry point (host pointers; the reference's ea_attention_cpu argument list and
+    argtypes, src/exactattn/cpu.py:35-38,86-94). Returns (out bits, flags, stats[3])."""
     lib = load()
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
@@ -256,8 +296,34 @@ def ea_attention_hip(q, k, v, alpha_bits, row_ptr, key_idx, out="bf16", splits=8
     res = np.zeros((rows, dv), dtype=np.uint32 if fp32 else np.uint16)
     flags = np.zeros(rows, dtype=np.uint8)
     st = np.zeros(3, dtype=np.int64)
-    rc = lib.ea_attention_hip(q.ctypes.data, rows, d, k.ctypes.data, v.ctypes.data, n, dv, int(alpha_bits),
-                              rp.ctypes.data, ki.ctypes.data, int(fp32), 64, 64, splits, 0, 1, res.ctypes.data,
-                              flags.ctypes.data, st.ctypes.data)
+    rc = lib.ea_attention_hip(q.ctypes.data, rows, d, k.ctypes.data, v.ctypes.data, n, dv,
+                              ctypes.c_float(float(np.float32(alpha))), rp.ctypes.data, ki.ctypes.data, int(fp32),
+                              acc_bits, tile, splits, 0, 1, res.ctypes.data, flags.ctypes.data, st.ctypes.data)
     _check(rc, "ea_attention_hip")
     return res, flags, st
+
+
+def exact_row(q, k, v, alpha_bits: int, out: str = "bf16", trace: bool = False):
+    """The host exact tier on one row of host arrays (ea_exact_row): q (d,), k (n, d), v (n, dv)
+    bf16 bits. Returns the output bits, plus (t bits, w_m, w_e) per key when trace=True. Raises
+    ExactAttentionDomainError for NaN/inf, an fp32 logit overflow or a spread past 2^20 bits."""
+    lib = load()
+    q = np.ascontiguousarray(q, dtype=np.uint16).reshape(-1)
+    d = q.shape[0]
+    k = np.ascontiguousarray(k, dtype=np.uint16).reshape(-1, d)
+    n = k.shape[0]
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    dv = v.shape[-1]
+    v = v.reshape(n, dv)
+    fp32 = out == "fp32"
+    res = np.zeros(dv, dtype=np.uint32 if fp32 else np.uint16)
+    tb = np.zeros(max(n, 1), np.uint32)
+    wm = np.zeros(max(n, 1), np.int32)
+    we = np.zeros(max(n, 1), np.int64)
+    rc = lib.ea_exact_row(q.ctypes.data, d, k.ctypes.data, v.ctypes.data, n, dv, int(alpha_bits), int(fp32),
+                          res.ctypes.data, tb.ctypes.data if trace else None, wm.ctypes.data if trace else None,
+                          we.ctypes.data if trace else None)
+    if rc == 2 or rc == 3:
+        raise ExactAttentionDomainError("non-finite input, fp32 logit overflow or an exponent spread past 2^20")
+    _check(rc, "ea_exact_row")
+    return (res, tb[:n], wm[:n], we[:n]) if trace else res

@@ -24,7 +24,7 @@ import ctypes
 import numpy as np
 
 from . import hip
-from .formats import ExactAttentionDomainError, alpha_bits_for, fp32_bits
+from .formats import ExactAttentionDomainError, ExactAttentionUncertifiedError, alpha_bits_for, fp32_bits
 
 TILE = 64  # keys per digit tile
 
@@ -118,6 +118,16 @@ class PagedKVCache:
                 return s
         raise RuntimeError("no free sequence slot")
 
+    def _check_slots(self, seqs) -> None:
+        """Every slot an in-range, live sequence, and each at most once (nothing has changed yet)."""
+        for s in seqs:
+            if not isinstance(s, (int, np.integer)) or not 0 <= int(s) < self.max_seqs:
+                raise ValueError(f"sequence slot {s!r} is outside [0, {self.max_seqs})")
+            if not self.live[int(s)]:
+                raise ValueError(f"sequence slot {int(s)} holds no live sequence")
+        if len(set(int(s) for s in seqs)) != len(seqs):
+            raise ValueError("a slot may appear once per batch")
+
     def drop_sequence(self, s: int) -> None:
         self.free.extend(self.pages[s][::-1])
         self.pages[s], self.length[s], self.live[s] = [], 0, False
@@ -158,10 +168,11 @@ class PagedKVCache:
         k_new = _dev16(torch, k_bits, self.dev)
         v_new = _dev16(torch, v_bits, self.dev)
         counts = [int(n) for n in counts]
+        if len(counts) != len(seqs):
+            raise ValueError("one count per sequence slot")
         if k_new.shape[0] != sum(counts) or v_new.shape[0] != sum(counts):
             raise ValueError("k/v must hold sum(counts) keys")
-        if len(set(seqs)) != len(seqs):
-            raise ValueError("a slot may appear once per batch")
+        self._check_slots(seqs)
         if sum(counts) == 0:
             return None
         sa = np.asarray(seqs, dtype=np.int64)
@@ -209,7 +220,8 @@ class PagedKVCache:
     def truncate(self, s: int, length: int) -> None:
         """Drop the keys at or past `length` (rejected draft nodes); the tile holding the new end is
         sliced again so its digits match the shorter sequence."""
-        if length > self.length[s]:
+        self._check_slots([s])
+        if length < 0 or length > self.length[s]:
             raise ValueError("truncate cannot grow a sequence")
         self.length[s] = length
         keep = (length + self.P - 1) // self.P
@@ -256,6 +268,7 @@ class ExactAttentionBackend:
         self.cache, self.Hq, self.out = cache, num_q_heads, out
         self.alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
         self.ws = None
+        self._last = None  # the latest launch: its ea_* arguments and the tensors they point at
 
     def _launch(self, seqs, qd, kvl, tree_mask=None, tree_base=None, digits_slot=None, staged=None, stream=None):
         """Enqueue one ea_hip_attention call over sequences `seqs` on torch's current stream.
@@ -305,7 +318,17 @@ class ExactAttentionBackend:
                         out=out.data_ptr(), flags=flags.data_ptr())
         hip._check(lib.ea_hip_attention(ctypes.byref(gc), ctypes.byref(b), ctypes.byref(o), ws.data_ptr(), int(nb.value),
                                         stream or hip._stream_ptr(torch)), "ea_hip_attention")
+        self._last = {"args": (gc, b, o), "keep": (qd, kvl, seq, off, tm, tb, staged), "out": out, "flags": flags,
+                      "ret": None}
         return out, flags
+
+    def _exact_tier(self) -> None:
+        """The host exact tier on the latest launch (ea_hip_exact_rows): waits for torch's current
+        stream and recomputes every row left at flag 1 in place (flag 0, or 2 on a domain error)."""
+        c = self.cache
+        gc, b, o = self._last["args"]
+        hip._check(hip.load().ea_hip_exact_rows(ctypes.byref(gc), ctypes.byref(b), ctypes.byref(o),
+                                                hip._stream_ptr(c.torch)), "ea_hip_exact_rows")
 
     def _run(self, seqs, q, kv_len, tree_mask=None, tree_base=None, digits_slot=None):
         """_launch, then the result on the host: (out bits (B, T, Hq, d), flags); flag 2 raises."""
@@ -315,9 +338,12 @@ class ExactAttentionBackend:
         (kvl,) = c.stage.put(np.asarray(kv_len, dtype=np.int32).reshape(-1))
         out, flags = self._launch(seqs, qd, kvl, tree_mask, tree_base, digits_slot)
         torch.cuda.current_stream().synchronize()  # the launch stream only, not the whole device
+        fl = flags.cpu().numpy()
+        if np.any(fl == 1):
+            self._exact_tier()
+            fl = flags.cpu().numpy()
         res = out.cpu().numpy()
         res = res.view(np.uint32) if self.out == "fp32" else res.view(np.uint16)
-        fl = flags.cpu().numpy()
         if np.any(fl == 2):
             raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
         return res, fl
@@ -329,13 +355,15 @@ class ExactAttentionBackend:
         Their K/V are appended to the cache; token j of sequence i attends the cached prefix and
         tokens 0..j of its chunk (a decode step is a chunk of one token). Enqueued on torch's
         current stream, no host synchronisation: returns device (out (num_tokens, Hq, d) bf16/fp32
-        bits, flags (num_tokens, Hq) uint8; 0 certified, 1 certified by the exact tier, 2 domain
-        error — check with check_flags)."""
+        bits, flags (num_tokens, Hq) uint8; 0 certified, 1 not certified by the device tiers (the
+        row holds +0), 2 domain error). Call check_flags(flags) before the next forward: it
+        finishes flag-1 rows with the host exact tier, in place, and raises on flag 2."""
         c = self.cache
         torch = c.torch
         ql = [int(n) for n in query_lens]
         if len(ql) != len(seqs) or any(n <= 0 for n in ql):
             raise ValueError("query_lens must give a positive token count per sequence")
+        c._check_slots(seqs)
         ntok = sum(ql)
         if query.shape[0] != ntok or key.shape[0] != ntok or value.shape[0] != ntok:
             raise ValueError("query/key/value must hold sum(query_lens) tokens")
@@ -366,13 +394,29 @@ class ExactAttentionBackend:
             qd = qd.view(B, T, Hq, d)
         slots = list(seqs)
         out, flags = self._launch(slots, qd, kvl, digits_slot=slots[0], staged=staged, stream=st)
+        self._last["keep"] += (q16, row)
         if T == 1:
-            return out.view(B, Hq, -1), flags.view(B, Hq)
-        return out.view(B * T, Hq, -1).index_select(0, row), flags.view(B * T, Hq).index_select(0, row)
+            ret = (out.view(B, Hq, -1), flags.view(B, Hq))
+        else:
+            ret = (out.view(B * T, Hq, -1).index_select(0, row), flags.view(B * T, Hq).index_select(0, row))
+        self._last["ret"] = (ret, row, T)
+        return ret
 
-    @staticmethod
-    def check_flags(flags) -> None:
-        """Synchronise on `flags` (from forward) and raise on a domain error (flag 2)."""
+    def check_flags(self, flags) -> None:
+        """Synchronise on `flags` (from forward) and make every row usable: rows the device tiers
+        left at flag 1 are recomputed by the host exact tier (in the returned out and flags, when
+        `flags` is the latest forward's; otherwise ExactAttentionUncertifiedError); flag 2 raises
+        ExactAttentionDomainError."""
+        if bool((flags == 1).any().item()):
+            last = self._last
+            if last is None or last["ret"] is None or last["ret"][0][1] is not flags:
+                raise ExactAttentionUncertifiedError("flag-1 rows of an earlier forward: call check_flags before "
+                                                     "the next forward")
+            self._exact_tier()
+            (ret_out, ret_flags), row, T = last["ret"]
+            if T > 1:
+                ret_out.copy_(last["out"].view(-1, *ret_out.shape[1:]).index_select(0, row))
+                ret_flags.copy_(last["flags"].view(-1, ret_flags.shape[1]).index_select(0, row))
         if bool((flags == 2).any().item()):
             raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
 
@@ -437,9 +481,10 @@ def hf_attention(module, query, key, value, attention_mask=None, scaling=None, d
     causal with the queries at the end of the key range (query t attends keys 0 .. kl-ql+t);
     `attention_mask` is not read, as in the reference (batches without padding). alpha =
     RN_fp32(scaling / ln 2), scaling defaulting to `module.scaling`. One ea_hip_attention launch
-    straight on the tensors' strides (no copies); returns (out (B, ql, H, D) bf16, None). Raises
-    on non-finite input or fp32 logit overflow, like the reference's kernels (this waits for
-    the launch)."""
+    straight on the tensors' strides (no copies); returns (out (B, ql, H, D) bf16, None). Rows the
+    device tiers leave uncertified are finished by the host exact tier (ea_hip_exact_rows); raises
+    on non-finite input or fp32 logit overflow, like the reference's kernels (this waits for the
+    launch)."""
     import torch
     if dropout:
         raise ValueError("dropout is not part of ExactAttention")
@@ -479,6 +524,10 @@ def hf_attention(module, query, key, value, attention_mask=None, scaling=None, d
                     out=out.data_ptr(), flags=flags.data_ptr())
     hip._check(lib.ea_hip_attention(ctypes.byref(g), ctypes.byref(b), ctypes.byref(o), ws.data_ptr(), int(nb.value),
                                     hip._stream_ptr(torch)), "ea_hip_attention")
+    if bool((flags == 1).any().item()):
+        # rows the device tiers left uncertified: the host exact tier, in place
+        hip._check(lib.ea_hip_exact_rows(ctypes.byref(g), ctypes.byref(b), ctypes.byref(o), hip._stream_ptr(torch)),
+                   "ea_hip_exact_rows")
     if bool((flags == 2).any().item()):
         raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
     return out, None

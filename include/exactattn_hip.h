@@ -11,8 +11,12 @@
  *
  * Per-row flags (uint8), the reference's meaning (csrc/exact_attention_cpu.cpp:580-584):
  *   0 = certified (bits equal the definition)
- *   1 = not certified by any device tier (the row's output is +0 and must not be used)
- *   2 = domain error: a NaN/inf input in the row's visible set, or an fp32 logit overflow
+ *   1 = not certified by the device tiers (the row's output is +0 and must not be used):
+ *       ea_hip_exact_rows recomputes such rows exactly on the host and clears the flag
+ *   2 = domain error: a NaN/inf input in the row's visible set, or an fp32 logit overflow (and,
+ *       from the host exact tier only, a row whose rounding would need exact sums over an
+ *       exponent spread above 2^20 bits, where the reference raises its domain error too,
+ *       src/exactattn/reference.py:27-30,124-125)
  */
 #ifndef EXACTATTN_HIP_H
 #define EXACTATTN_HIP_H
@@ -85,10 +89,14 @@ typedef struct ea_options {
                                kernel, [10] rows whose tier 1 ran in the int8-MFMA
                                prefill kernel, [11] prefill epoch folds before the last
                                tile (waves), [12] prefill waves that ran the exact
-                               per-pair path, [13..15] reserved */
-    void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep, split,
-                               combine and tier 2, and after tier 2 (per-kernel timing); a null
-                               entry is skipped (each record is one more packet in the stream) */
+                               per-pair path, [13] rows certified by the host exact
+                               tier (ea_hip_exact_rows), [14] rows it refused (spread
+                               limit, flag 2), [15] reserved */
+    void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep (the
+                               int8 path: q and K/V slicing), the tier-1 kernel, the combine (the
+                               int8 path: the merge of its key splits, when it has any) and tier 2,
+                               and after tier 2 (per-kernel timing); a null entry is skipped (each
+                               record is one more packet in the stream) */
     int64_t* timers;        /* optional device int64[16]: when set, the split kernel runs its
                                phase-clock build and adds shader-clock cycles (s_memtime) summed
                                over waves: [0] prologue, [1] wait for the tile barrier, [2] scores,
@@ -105,7 +113,21 @@ typedef struct ea_options {
     const int32_t* kv_digits_slot; /* optional, with kv_digits: device array, per sequence b of
                                the geometry the cache slot holding its tiles (a serving loop's
                                sequence slot); NULL: slot b */
+    int32_t force_tier2;    /* 1: list every row for the device tier 2, whatever tier 1 decided
+                               (tier 2 then recomputes and rewrites every row: a test of the
+                               exact tier on whole problems; needs tier2 = 1) */
+    int32_t kernel;         /* tier-1 kernel: EA_KERNEL_AUTO (by geometry), EA_KERNEL_PREFILL (the
+                               int8 prefill kernel for every d = dv = 128 problem),
+                               EA_KERNEL_DECODE (never the prefill kernel), EA_KERNEL_GENERAL (the
+                               general fp64 split kernel for every problem); never changes bits */
+    int32_t prefill_waves;  /* prefill block shape: 0 or 8 = 8 waves, 4 = 4 waves (same bits) */
+    int32_t pad2;
 } ea_options;
+
+#define EA_KERNEL_AUTO 0
+#define EA_KERNEL_PREFILL 1
+#define EA_KERNEL_DECODE 2
+#define EA_KERNEL_GENERAL 3
 
 /* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
  * the split count it will use. Reference counterpart: none (the Triton launcher allocates its
@@ -121,15 +143,45 @@ int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* byt
 int ea_hip_attention(const ea_geometry* g, const ea_buffers* b, const ea_options* o, void* workspace,
                      size_t workspace_bytes, ea_stream_t stream);
 
-/* Drop-in for the reference CPU ABI ea_attention_cpu (csrc/exact_attention_cpu.cpp:585-588),
- * same arguments and meaning, host pointers; computes on the current HIP device and returns when
- * done. `acc_bits`, `tile`, `nthreads` and `order_seed` are accepted and ignored (they cannot
- * change certified bits). `alpha` is passed as its fp32 bits. Flags 1 mean "not certified on the
- * device"; stats[0..2] += score, weight and final-rounding fallbacks of tier 1. */
+/* Host exact tier (tier 3) for a step ea_hip_attention enqueued with the same geometry, buffers
+ * and options: synchronises `stream`, reads the flags, and recomputes every row left at flag 1
+ * exactly on the host (its q, K and V rows gathered on the device into a staging buffer this call
+ * allocates and frees), writing the row's bits and flag 0 (flag 2 on a domain error or a refusal,
+ * see the flags above). Adds the rows to stats[13] / stats[14] when o->stats is set. Returns 0,
+ * -1 on bad arguments, -100 - e on a HIP error. Not capturable (it waits for the device).
+ * Reference counterpart: the host recompute of flagged rows, src/exactattn/triton_kernels.py:
+ * 1553-1559 and src/exactattn/cpu.py:105-108 (reference.attention_row). */
+int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* b, const ea_options* o, ea_stream_t stream);
+
+/* The host exact tier on one row of host arrays: q (d), k (n x d), v (n x dv) bf16 bits, alpha as
+ * fp32 bits -> out (dv bf16 or fp32 bits). t_bits, w_m, w_e (optional, n entries each) receive
+ * the per-key logits t = RN32(alpha s) and weights w = RN24(2^t) = w_m 2^w_e. Returns 0, 2 for a
+ * domain error (NaN/inf input, fp32 logit overflow), 3 when the row needs exact sums over an
+ * exponent spread above 2^20 bits, -1 on bad arguments. Runs on the CPU only (no device call).
+ * Reference counterpart: reference.trace_row / attention_row (src/exactattn/reference.py:82-147). */
+int ea_exact_row(const uint16_t* q, int d, const uint16_t* k, const uint16_t* v, int64_t n, int dv,
+                 uint32_t alpha_bits, int fp32_out, void* out, uint32_t* t_bits, int32_t* w_m, int64_t* w_e);
+
+/* Drop-in for the reference CPU ABI (csrc/exact_attention_cpu.cpp:585-588): the same argument
+ * list, types and return codes as ea_attention_cpu, host pointers; computes on the current HIP
+ * device and returns when done. rc -1 for d or dv outside [1, 128] (this build's head sizes;
+ * d a multiple of 8, dv even), tile <= 0 or splits <= 0; -2 for acc_bits other than 64 and 128;
+ * -3 for a non-finite alpha; -100 - e for a HIP error. `tile`, `acc_bits`, `order_seed` and
+ * `nthreads` are validated and otherwise ignored (they cannot change certified bits); `splits` is
+ * the KV split count. stats[0..2] += tier-1 score, weight and final-rounding fallbacks, as in the
+ * reference. Rows the device tiers leave uncertified are recomputed exactly by the host exact
+ * tier, so flags are 0, or 2 for rows that see a NaN/inf (their output is +0). */
 int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
-                     int dv, uint32_t alpha_bits, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
+                     int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
                      int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
                      uint8_t* flags, int64_t* stats);
+
+/* The reference's test hook (csrc/exact_attention_cpu.cpp:630-638), same signature and result:
+ * RN-even of (a / b) * 2^E, a and b as 128-bit (hi, lo) halves, into fp32 (fp32 = 1) or bf16,
+ * returned as a float (negated when neg); *overflow = 1 (result 0) when it exceeds the format's
+ * largest finite value. Host code only. */
+float ea_round_ratio(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo, int E, int neg, int fp32,
+                     int* overflow);
 
 /* Known-answer entry points over the device helper routines (device arrays, n elements).
  * ea_hip_kat_weight: w = RN24(2^t) for fp32 t bits -> M, E, status (0 certified by the fp64

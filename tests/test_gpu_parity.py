@@ -19,9 +19,10 @@ pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
 
 
-def _run(prob, alpha_bits, out="bf16", splits=0, merge_order=None):
+def _run(prob, alpha_bits, out="bf16", splits=0, merge_order=None, **kw):
+    """The device tiers only (fallback=False): flags as tier 1 and tier 2 leave them."""
     from exactattention_amd.hip import attention_problem
-    return attention_problem(prob, alpha_bits, out, splits, merge_order, True, False)
+    return attention_problem(prob, alpha_bits, out, splits, merge_order, True, False, **kw)
 
 
 def _oracle(prob, alpha_bits, out="bf16"):
@@ -433,23 +434,18 @@ def test_decode_kernel_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
 # the int8-MFMA prefill kernel (64 rows per block, balanced radix-256 digits)
 # ---------------------------------------------------------------------------------------------
 
-@pytest.fixture
-def force_prefill(monkeypatch):
-    monkeypatch.setenv("EA_PREFILL", "1")
-
-
 def _rows(prob):
     return prob["q"].shape[0] * prob["q"].shape[1] * prob["q"].shape[2]
 
 
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("vkind", ["normal", "wide", "dupes"])
-def test_prefill_kernel_kinds_match_oracle(gpu, force_prefill, kind, vkind):
+def test_prefill_kernel_kinds_match_oracle(gpu, kind, vkind):
     rng = np.random.default_rng(hash(("pf", kind, vkind)) % (1 << 32))
     prob = _rand_problem(rng, kind, vkind, B=2, T=40, Hq=4, Hkv=2, S=150, d=128, dv=128)
     ab = default_alpha_bits(128)
     want, _ = _oracle(prob, ab)
-    got, flags, st = _run(prob, ab)
+    got, flags, st = _run(prob, ab, kernel="prefill")
     assert st["prefill_kernel_rows"] == _rows(prob), st
     assert not np.any(flags == 1), st
     assert np.array_equal(got, want), st
@@ -479,7 +475,7 @@ def test_prefill_causal_matches_oracle_and_decode(gpu, out):
     assert np.array_equal(got_d.reshape(got.shape[1:]), got[0])
 
 
-def test_prefill_paged_gqa_ragged(gpu, force_prefill):
+def test_prefill_paged_gqa_ragged(gpu):
     """Paged NHD cache (page 16), GQA 4, ragged sequence lengths (partial 64-row blocks and
     partial 64-key tiles), rows whose prefix is empty."""
     rng = np.random.default_rng(32)
@@ -494,13 +490,13 @@ def test_prefill_paged_gqa_ragged(gpu, force_prefill):
     prob = problem.to_paged(base, 16, np.random.default_rng(3), "NHD")
     ab = default_alpha_bits(d)
     want, _ = _oracle(base, ab)
-    got, flags, st = _run(prob, ab)
+    got, flags, st = _run(prob, ab, kernel="prefill")
     assert st["prefill_kernel_rows"] == _rows(prob), st
     assert not np.any(flags), st
     assert np.array_equal(got, want)
 
 
-def test_prefill_tree_masks_equal_decode(gpu, monkeypatch):
+def test_prefill_tree_masks_equal_decode(gpu):
     """Speculative-tree rows (prefix + 64-bit draft mask) through the prefill kernel give the same
     bits as the decode path on the same problem."""
     rng = np.random.default_rng(22)
@@ -515,27 +511,43 @@ def test_prefill_tree_masks_equal_decode(gpu, monkeypatch):
     ab = default_alpha_bits(d)
     want, fl_d, st_d = _run(tree, ab, splits=2)
     assert st_d["prefill_kernel_rows"] == 0 and not np.any(fl_d), st_d
-    monkeypatch.setenv("EA_PREFILL", "1")
-    got, flags, st = _run(tree, ab)
+    got, flags, st = _run(tree, ab, kernel="prefill")
     assert st["prefill_kernel_rows"] == _rows(tree), st
     assert not np.any(flags), st
     assert np.array_equal(got, want)
 
 
-def test_prefill_four_wave_block_matches_oracle(gpu, force_prefill, monkeypatch):
-    """The 4-wave prefill block (EA_PF_SHAPE=4) gives the oracle's bits, like the default 8-wave
-    block."""
+def test_prefill_four_wave_block_matches_oracle(gpu):
+    """The 4-wave prefill block (ea_options.prefill_waves = 4) gives the oracle's bits, like the
+    default 8-wave block."""
     rng = np.random.default_rng(23)
     prob = _rand_problem(rng, "normal", "normal", B=2, T=70, Hq=4, Hkv=2, S=300, d=128, dv=128)
     ab = default_alpha_bits(128)
     want, _ = _oracle(prob, ab)
-    got8, fl8, st8 = _run(prob, ab)
-    monkeypatch.setenv("EA_PF_SHAPE", "4")
-    got4, fl4, st4 = _run(prob, ab)
+    got8, fl8, st8 = _run(prob, ab, kernel="prefill")
+    got4, fl4, st4 = _run(prob, ab, kernel="prefill", prefill_waves=4)
     for got, fl, st in ((got8, fl8, st8), (got4, fl4, st4)):
         assert st["prefill_kernel_rows"] == _rows(prob), st
         assert not np.any(fl == 1), st
         assert np.array_equal(got, want), st
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5])
+def test_prefill_key_splits_match_oracle(gpu, splits):
+    """The int8 prefill kernel with its key range cut into 2, 3 and 5 splits (partials merged and
+    rounded by ea_pf_combine): the oracle's bits, as with one split; ragged causal rows, so some
+    splits of a row block hold no visible key, and wide values whose bases differ per split."""
+    rng = np.random.default_rng(70 + splits)
+    prob = _rand_problem(rng, "outlier", "wide", B=2, T=40, Hq=4, Hkv=2, S=700, d=128, dv=128)
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    one, fl1, st1 = _run(prob, ab, splits=1, kernel="prefill")
+    got, flags, st = _run(prob, ab, splits=splits, kernel="prefill")
+    assert st["nsplit"] >= 2 and st1["nsplit"] == 1, (st, st1)  # 11 tiles: 2, 3 and 4 splits
+    assert st["prefill_kernel_rows"] == _rows(prob), st
+    assert not np.any(flags == 1) and not np.any(fl1 == 1), (st, st1)
+    assert np.array_equal(one, want)
+    assert np.array_equal(got, want)
 
 
 def test_prefill_rows_longer_than_256_tiles(gpu):
@@ -596,7 +608,7 @@ def test_kv_digits_appends_equal_one_update(gpu, paged_cache):
 
 
 @pytest.mark.parametrize("paged_cache", [False, True])
-def test_prefill_reads_kv_digits_cache(gpu, force_prefill, paged_cache):
+def test_prefill_reads_kv_digits_cache(gpu, paged_cache):
     """The prefill kernel reading the caller's digit cache gives the bits it gives when it slices
     K/V itself, and the oracle's."""
     import torch
@@ -604,10 +616,10 @@ def test_prefill_reads_kv_digits_cache(gpu, force_prefill, paged_cache):
     prob = _kv_digits_problem(np.random.default_rng(62), paged_cache)
     ab = default_alpha_bits(128)
     want, _ = _oracle(prob, ab)
-    plain, fl, st = _run(prob, ab)
+    plain, fl, st = _run(prob, ab, kernel="prefill")
     assert st["prefill_kernel_rows"] == _rows(prob) and not np.any(fl), st
     assert np.array_equal(plain, want)
-    dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+    dp = DeviceProblem(prob, "bf16", 0, "cuda:0", kernel="prefill")
     cache = KVDigits(dp, (int(prob["seq_len"].max()) + 63) // 64)
     cache.update(dp, torch.zeros(2, dtype=torch.int32, device="cuda"), dp.t["seq_len"].clone(),
                  int(prob["seq_len"].max()))
@@ -652,7 +664,7 @@ def test_chunked_prefill_from_the_cache_equals_full_prefill(gpu):
         assert np.array_equal(got[0], want[0, a:e]), c
 
 
-def test_prefill_nonfinite_flags_exactly_the_rows_that_see_them(gpu, force_prefill):
+def test_prefill_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
     rng = np.random.default_rng(45)
     T = 80
     prob = _rand_problem(rng, "normal", "normal", B=1, T=T, Hq=2, Hkv=1, S=T, d=128, dv=128)
@@ -662,7 +674,7 @@ def test_prefill_nonfinite_flags_exactly_the_rows_that_see_them(gpu, force_prefi
     prob["v"][0, 0, 70, 100] = 0xFF80  # -inf value at position 70
     prob["q"][0, 10, 1, 5] = 0x7F80    # inf in one query row
     ab = default_alpha_bits(128)
-    got, flags, st = _run(prob, ab)
+    got, flags, st = _run(prob, ab, kernel="prefill")
     clean = {**prob, "k": prob["k"].copy(), "v": prob["v"].copy(), "q": prob["q"].copy()}
     clean["k"][0, 0, 50, 3] = 0
     clean["v"][0, 0, 70, 100] = 0
@@ -692,23 +704,58 @@ def c4_problem():
     return configs.c4()
 
 
-@pytest.mark.parametrize("name,path", [("C1", None), ("C2", None), ("C4", None), ("C4", "0")],
-                         ids=["C1", "C2", "C4", "C4-decode-kernel"])
-def test_config_golden_hash(gpu, monkeypatch, request, name, path):
+@pytest.mark.parametrize("name,kernel,splits", [("C1", "auto", 0), ("C2", "auto", 0), ("C2", "auto", 1),
+                                                 ("C2", "auto", 8), ("C4", "auto", 0), ("C4", "decode", 0)],
+                         ids=["C1", "C2", "C2-splits1", "C2-splits8", "C4", "C4-decode-kernel"])
+def test_config_golden_hash(gpu, request, name, kernel, splits):
     """BASELINE configs C1, C2 and C4 at full size against the committed hashes (the oracle's and
-    the reference C++ kernel's bits). C4 (16-node draft trees, GQA 2: 32 rows per sequence and KV
-    head) runs on the int8 prefill kernel by default and on the decode kernel with EA_PREFILL=0;
-    both give the golden bits. C5 (4.97 GB of K/V, about six minutes of seeded input generation)
-    is checked by hand, not here."""
-    if path is not None:
-        monkeypatch.setenv("EA_PREFILL", path)
+    the reference C++ kernel's bits). C2 also at 1 and 8 KV splits (BASELINE: the bits must not
+    depend on the split count). C4 (16-node draft trees, GQA 2: 32 rows per sequence and KV head)
+    runs on the int8 prefill kernel by default and on the decode kernel when the prefill kernel is
+    switched off; both give the golden bits. No row may need more than the device tiers."""
     p = request.getfixturevalue("c4_problem") if name == "C4" else configs.CONFIGS[name]()
-    got, flags, st = _run(p, configs.alpha_bits())
+    got, flags, st = _run(p, configs.alpha_bits(), splits=splits, kernel=kernel)
     gold = json.load(open(os.path.join(GOLD, "baseline_sha256.json")))[name]["sha256"]
+    assert not flags.any() and st["uncertified"] == 0, st
+    if splits:
+        assert st["nsplit"] == splits, st
     assert hashlib.sha256(got.tobytes()).hexdigest() == gold, st
     if name == "C4":
-        assert st["prefill_kernel_rows"] == (_rows(p) if path is None else 0), st
-    assert np.all(flags[flags != 0] == 1), st   # flagged rows (if any) certified by tier 2
+        assert st["prefill_kernel_rows"] == (_rows(p) if kernel == "auto" else 0), st
+
+
+@pytest.fixture(scope="module")
+def c5_problem(request):
+    """BASELINE config C5 (16 sequences of 8K-131K keys, outlier channels): about 4.5 GB of K/V
+    generated from its seed on the host, once for the module. Generation prints its progress (the
+    seeded draws take a minute or two)."""
+    import time
+    capman = request.config.pluginmanager.getplugin("capturemanager")
+    t0 = time.time()
+    with capman.global_and_fixture_disabled():
+        print(f"\n[c5] generating BASELINE C5 inputs (seed 1005) ...", flush=True)
+    p = configs.c5()
+    with capman.global_and_fixture_disabled():
+        print(f"[c5] generated in {time.time() - t0:.0f} s", flush=True)
+    return p
+
+
+@pytest.mark.parametrize("page", [16, 64])
+def test_c5_golden_hash_page_sizes(gpu, request, page):
+    """BASELINE config C5 at full size, the cache in pages of 16 and of 64 keys: both give the
+    committed golden bits (the reference C++ kernel's), and no row needs more than tier 1."""
+    import time
+    p = request.getfixturevalue("c5_problem")
+    capman = request.config.pluginmanager.getplugin("capturemanager")
+    if page != 16:
+        t0 = time.time()
+        p = configs.c5_repage(p, page)
+        with capman.global_and_fixture_disabled():
+            print(f"\n[c5] repaged to {page} in {time.time() - t0:.0f} s", flush=True)
+    got, flags, st = _run(p, configs.alpha_bits())
+    gold = json.load(open(os.path.join(GOLD, "baseline_sha256.json")))["C5"]["sha256"]
+    assert not flags.any() and st["tier1_flagged"] == 0, st
+    assert hashlib.sha256(got.tobytes()).hexdigest() == gold, (page, st)
 
 
 def test_prefill_c3_back_to_back(gpu):

@@ -152,3 +152,32 @@ def test_forward_rejects_bad_batches_without_touching_the_cache():
         with pytest.raises(ValueError):
             be.forward(q, k, k, seqs, lens)
     assert c.length == [0, 0] and c.pages == [[], []] and len(c.free) == 4
+    # slots out of range (a negative slot would index from the end on the host and read before
+    # the block table on the device), dropped, or repeated
+    c.drop_sequence(b)
+    for seqs, lens in (([-1], [3]), ([2], [3]), ([b], [3]), ([a, a], [2, 1]), ([1.0], [3])):
+        with pytest.raises(ValueError):
+            be.forward(q, k, k, seqs, lens)
+        with pytest.raises(ValueError):
+            c.append_batch(seqs, lens, bf16(np.random.default_rng(0), (3, 1, 8)), bf16(np.random.default_rng(0),
+                                                                                        (3, 1, 8)))
+    with pytest.raises(ValueError):
+        c.truncate(b, 0)
+    assert c.length == [0, 0] and c.pages == [[], []] and len(c.free) == 4
+
+
+def test_check_flags_never_passes_flag_one():
+    """A flag-1 row (not certified by the device tiers, output +0) is never handed back as valid:
+    check_flags finishes the latest forward's rows with the host exact tier, and for any other
+    flags tensor raises ExactAttentionUncertifiedError; flag 2 raises ExactAttentionDomainError."""
+    import torch
+    from exactattention_amd.formats import ExactAttentionDomainError, ExactAttentionUncertifiedError
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    c = PagedKVCache(num_pages=4, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
+                     digits=False, device="cpu")
+    be = ExactAttentionBackend(c, 2, 0x3E0293EE)
+    be.check_flags(torch.zeros((3, 2), dtype=torch.uint8))
+    with pytest.raises(ExactAttentionUncertifiedError):
+        be.check_flags(torch.tensor([[0, 1], [0, 0]], dtype=torch.uint8))
+    with pytest.raises(ExactAttentionDomainError):
+        be.check_flags(torch.tensor([[0, 2]], dtype=torch.uint8))
