@@ -1143,6 +1143,38 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
 
 int herr(hipError_t e) { return e == hipSuccess ? 0 : -100 - (int)e; }
 
+}  // namespace
+
+// The allocation-free entry point's workspace (ea_hip_attention_noalloc): one array per device,
+// held by the device until the process ends. Host code never passes this name to a kernel or a
+// copy (on the host it only stands for the symbol): it uses the device address that
+// hipGetSymbolAddress returned for the current device, kept in scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[EA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int EA_MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[EA_MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (with that
+// device current) and cached; 0 or -100 - e.
+int scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return herr(e);
+    if (dev < 0 || dev >= EA_MAX_DEVICES) return -1;
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return herr(e);
+        if (!p) return -1;
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return 0;
+}
 
 // ea_options.force_tier2: every row onto the tier-2 work list (after tier 1)
 int list_all(const Params& P, const ea_options* o, unsigned blocks, hipStream_t st) {
@@ -1305,6 +1337,17 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         if (rc) return rc;
     }
     return mark(4);
+}
+
+int ea_hip_attention_noalloc(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, ea_stream_t stream) {
+    size_t need = 0;
+    int32_t ns = 0;
+    int rc = ea_hip_workspace_size(g, o, &need, &ns);
+    if (rc) return rc;
+    if (need > (size_t)EA_NOALLOC_SCRATCH_BYTES) return -4;
+    void* ws = nullptr;
+    if ((rc = scratch_address(&ws))) return rc;
+    return ea_hip_attention(g, bf, o, ws, (size_t)EA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, ea_stream_t stream) {

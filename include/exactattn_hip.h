@@ -143,6 +143,18 @@ int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* byt
 int ea_hip_attention(const ea_geometry* g, const ea_buffers* b, const ea_options* o, void* workspace,
                      size_t workspace_bytes, ea_stream_t stream);
 
+/* ea_hip_attention without a caller workspace, for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The workspace is a fixed array of EA_NOALLOC_SCRATCH_BYTES in device memory that each
+ * GPU the library runs on holds until the process ends; the call allocates nothing. Geometries
+ * whose ea_hip_workspace_size exceeds it return -4 (decode and verification steps fit: C2 needs
+ * about 5 MB; long-context decode of 131K keys about 60 MB; int8 prefill steps usually do not).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller. Same buffers, options, return codes and
+ * stream semantics as ea_hip_attention otherwise (enqueue only, no sync). */
+#define EA_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ea_hip_attention_noalloc(const ea_geometry* g, const ea_buffers* b, const ea_options* o, ea_stream_t stream);
+
 /* Host exact tier (tier 3) for a step ea_hip_attention enqueued with the same geometry, buffers
  * and options: synchronises `stream`, reads the flags, and recomputes every row left at flag 1
  * exactly on the host (its q, K and V rows gathered on the device into a staging buffer this call
