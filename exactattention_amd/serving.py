@@ -470,6 +470,184 @@ class ExactAttentionBackend:
             self.cache.append(s, np.asarray(k)[idx], np.asarray(v)[idx])
 
 
+class DecodeGraph:
+    """One decode step of a fixed batch of sequence slots (one new token each), captured once in a
+    HIP graph and replayed per step: the block-table update, the K/V scatter into the paged pools,
+    the digit re-slice of the touched tiles and the certified attention launch. Per step the host
+    plans the appends (page allocation, scatter slots, lengths) into a pinned buffer, enqueues one
+    copy of it and one graph launch on torch's current stream; there is no host synchronisation.
+
+    The caller writes the step's inputs into the static tensors `q` (B, 1, Hq, d), `k` and `v`
+    (B, Hkv, d) (int16 views of bf16) before calling step(); the outputs land in `out` and `flags`.
+    `max_len` bounds every sequence's length while the graph lives: it sizes the split grid (the
+    kernel skips the splits past a sequence's end), so a tight bound keeps the grid dense."""
+
+    RING = 4  # pinned metadata buffers: the host may run this many steps ahead of the GPU
+
+    def __init__(self, backend: "ExactAttentionBackend", seqs, max_len: int | None = None):
+        import torch
+        from .graph import EVENT_DISABLE_TIMING, HipGraph, hip_rt
+        c = backend.cache
+        self.be, self.c, self.torch = backend, c, torch
+        c._check_slots(seqs)
+        self.seqs = np.asarray(seqs, dtype=np.int64)
+        B, Hq, Hkv, d, ms = len(seqs), backend.Hq, c.Hkv, c.d, c.max_seqs
+        self.B = B
+        self.max_len = int(min(max_len or c.max_seq_len, c.max_seq_len))
+        if max(c.length[s] for s in seqs) + 1 > self.max_len:
+            raise ValueError("max_len is below a sequence's next length")
+        dev = c.dev
+        self.q = torch.zeros((B, 1, Hq, d), dtype=torch.int16, device=dev)
+        self.k = torch.zeros((B, Hkv, d), dtype=torch.int16, device=dev)
+        self.v = torch.zeros((B, Hkv, d), dtype=torch.int16, device=dev)
+        fp32 = backend.out == "fp32"
+        self.out = torch.empty((B, 1, Hq, d), dtype=torch.int32 if fp32 else torch.int16, device=dev)
+        self.flags = torch.empty(B * Hq, dtype=torch.uint8, device=dev)
+        # metadata layout (bytes): idx, bt_pos, bt_off (B int64); bt_val, kvl (B int32); kb, ke,
+        # lens (max_seqs int32)
+        lay = {}
+        at = 0
+        for name, n, dt in (("idx", B, np.int64), ("bt_pos", B, np.int64), ("bt_off", B, np.int64),
+                            ("bt_val", B, np.int32), ("kvl", B, np.int32), ("kb", ms, np.int32),
+                            ("ke", ms, np.int32), ("lens", ms, np.int32)):
+            lay[name] = (at, n, dt)
+            at += (n * np.dtype(dt).itemsize + 255) // 256 * 256
+        self._nbytes = at
+        self._host = [torch.zeros(at, dtype=torch.uint8, pin_memory=True) for _ in range(self.RING)]
+        # numpy views of each pinned buffer's fields, made once
+        self._hv = [{k: h.numpy()[o:o + n * np.dtype(dt).itemsize].view(dt) for k, (o, n, dt) in lay.items()}
+                    for h in self._host]
+        for hv in self._hv:
+            hv["bt_off"][:] = self.seqs * c.max_pages
+        self.meta = torch.zeros(at, dtype=torch.uint8, device=dev)
+        tdt = {np.int64: torch.int64, np.int32: torch.int32}
+        self.dv = {k: self.meta[o:o + n * np.dtype(dt).itemsize].view(tdt[dt]) for k, (o, n, dt) in lay.items()}
+        self.h = hip_rt()
+        self._ev = []
+        for _ in range(self.RING):
+            e = ctypes.c_void_p()
+            if self.h.hipEventCreateWithFlags(ctypes.byref(e), EVENT_DISABLE_TIMING) != 0:
+                raise RuntimeError("hipEventCreateWithFlags")
+            self._ev.append(e)
+        self._used = [False] * self.RING
+        self._ring = 0
+        # host mirrors of the batch's lengths and page counts
+        self.L = np.asarray([c.length[s] for s in seqs], dtype=np.int64)
+        self.npg = np.asarray([len(c.pages[s]) for s in seqs], dtype=np.int64)
+        # the attention call's arguments, fixed for the graph's life
+        lib = hip.load()
+        g = c._geom1(int(self.seqs[0]), 1, Hq, self.max_len)
+        g["num_seqs"] = B
+        self.gc = hip.geometry(g)
+        self.o = hip.Options(alpha_bits=backend.alpha_bits, out_fp32=int(fp32), splits=0, tier2=1)
+        nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
+        hip._check(lib.ea_hip_workspace_size(ctypes.byref(self.gc), ctypes.byref(self.o), ctypes.byref(nb),
+                                             ctypes.byref(ns)), "ea_hip_workspace_size")
+        self.ws_bytes = int(nb.value)
+        self.ws = torch.empty(max(self.ws_bytes, 256), dtype=torch.uint8, device=dev)
+        self.bufs = hip.Buffers(q=self.q.data_ptr(), k=c.k.data_ptr(), v=c.v.data_ptr(),
+                                seq_len=self.dv["kvl"].data_ptr(), kv_len=self.dv["kvl"].data_ptr(),
+                                block_table=c.block_table.data_ptr(), block_table_offset=self.dv["bt_off"].data_ptr(),
+                                tree_mask=None, tree_base=None, out=self.out.data_ptr(),
+                                flags=self.flags.data_ptr())
+        if c.digits is not None:
+            gd = c._geom1(0, 1, Hkv, c.max_seq_len)
+            gd["num_seqs"] = ms
+            self.gd = hip.geometry(gd)
+            self.bd = hip.Buffers(q=None, k=c.k.data_ptr(), v=c.v.data_ptr(), seq_len=self.dv["lens"].data_ptr(),
+                                  kv_len=None, block_table=c.block_table.data_ptr(), block_table_offset=None,
+                                  tree_mask=None, tree_base=None, out=None, flags=None)
+        # captured on a side stream (capture records the work without running it); replayed on
+        # torch's current stream, right after the step's metadata copy
+        self.graph = HipGraph()
+        cap = torch.cuda.Stream(device=dev)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(cap):
+            self.graph.capture(cap, lambda: self._enqueue(cap))
+        torch.cuda.synchronize()
+
+    def _enqueue(self, stream) -> None:
+        c, lib, d = self.c, hip.load(), self.dv
+        st = ctypes.c_void_p(stream.cuda_stream)
+        c.block_table.view(-1).index_copy_(0, d["bt_pos"], d["bt_val"])
+        H, dd = c.Hkv, c.d
+        c.k.view(-1, H, dd).index_copy_(0, d["idx"], self.k)
+        c.v.view(-1, H, dd).index_copy_(0, d["idx"], self.v)
+        if c.digits is not None:
+            hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(self.gd), ctypes.byref(self.bd), d["kb"].data_ptr(),
+                                                   d["ke"].data_ptr(), 1, ctypes.c_void_p(c.digits.data_ptr()),
+                                                   c.tiles, st), "ea_hip_kv_digits_update")
+        hip._check(lib.ea_hip_attention(ctypes.byref(self.gc), ctypes.byref(self.bufs), ctypes.byref(self.o),
+                                        self.ws.data_ptr(), self.ws_bytes, st), "ea_hip_attention")
+
+    def _plan(self) -> int:
+        """Host half of a step: one key per slot appended (pages allocated as needed) into the
+        next pinned buffer. Returns the buffer's index."""
+        c, seqs, L = self.c, self.seqs, self.L
+        if int(L.max()) + 1 > self.max_len:
+            raise ValueError("a sequence would pass the graph's max_len")
+        pg = L // c.P
+        grow = np.flatnonzero(pg >= self.npg)
+        if grow.size:
+            if grow.size > len(c.free):
+                raise RuntimeError("out of pages")
+            for i in grow.tolist():
+                s = int(seqs[i])
+                c.pages[s].append(c.free.pop())
+                c.bt_host[s, len(c.pages[s]) - 1] = c.pages[s][-1]
+                self.npg[i] += 1
+        i = self._ring
+        self._ring = (i + 1) % self.RING
+        if self._used[i] and self.h.hipEventSynchronize(self._ev[i]) != 0:
+            raise RuntimeError("hipEventSynchronize")
+        hv = self._hv[i]
+        bt_val = c.bt_host[seqs, pg]
+        hv["bt_val"][:] = bt_val
+        hv["idx"][:] = bt_val.astype(np.int64) * c.P + L % c.P
+        hv["bt_pos"][:] = seqs * c.max_pages + pg
+        L += 1
+        hv["kvl"][:] = L
+        hv["kb"][:] = 0
+        hv["ke"][:] = 0
+        hv["kb"][seqs] = L - 1
+        hv["ke"][seqs] = L
+        for s, n in zip(seqs.tolist(), L.tolist()):
+            c.length[s] = n
+        hv["lens"][:] = c.length
+        return i
+
+    def step(self):
+        """Append the keys in `k`, `v` to every slot and attend with `q`, enqueued on torch's
+        current stream. Returns device (out (B, Hq, d), flags (B, Hq))."""
+        i = self._plan()
+        st = ctypes.c_void_p(self.torch.cuda.current_stream(self.c.dev).cuda_stream)
+        if self.h.hipMemcpyAsync(ctypes.c_void_p(self.meta.data_ptr()), ctypes.c_void_p(self._host[i].data_ptr()),
+                                 self._nbytes, 1, st) != 0:
+            raise RuntimeError("hipMemcpyAsync")
+        if self.h.hipEventRecord(self._ev[i], st) != 0:
+            raise RuntimeError("hipEventRecord")
+        self._used[i] = True
+        if self.h.hipGraphLaunch(self.graph.exec, st) != 0:
+            raise RuntimeError("hipGraphLaunch")
+        return self.out.view(self.B, self.be.Hq, -1), self.flags.view(self.B, self.be.Hq)
+
+    def check_flags(self, flags=None) -> None:
+        """After the latest step: flag-1 rows finished by the host exact tier, flag 2 raises."""
+        st = ctypes.c_void_p(self.torch.cuda.current_stream(self.c.dev).cuda_stream)
+        if bool((self.flags == 1).any().item()):
+            hip._check(hip.load().ea_hip_exact_rows(ctypes.byref(self.gc), ctypes.byref(self.bufs),
+                                                    ctypes.byref(self.o), st), "ea_hip_exact_rows")
+        if bool((self.flags == 2).any().item()):
+            raise ExactAttentionDomainError("non-finite input or fp32 logit overflow")
+
+    def close(self) -> None:
+        self.graph.close()
+        for e in self._ev:
+            if e:
+                self.h.hipEventDestroy(e)
+        self._ev = []
+
+
 _HF_WS = {}
 
 

@@ -7,7 +7,6 @@ D16). The step is captured with hipStreamBeginCapture on a torch stream, its nod
 work and synchronisations between the replays; every replay must give the eager step's bits.
 """
 
-import ctypes
 import hashlib
 import json
 import os
@@ -17,59 +16,11 @@ import pytest
 
 from exactattention_amd import configs, problem
 from exactattention_amd.formats import default_alpha_bits
+from exactattention_amd.graph import NODE_KERNEL, HipGraph
 from gen import bf16
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
-NODE_KERNEL, NODE_MEMSET = 0, 2
-
-
-class HipGraph:
-    """hipStreamBeginCapture / EndCapture / Instantiate / Launch through libamdhip64."""
-
-    def __init__(self):
-        h = ctypes.CDLL("libamdhip64.so")
-        P = ctypes.c_void_p
-        h.hipStreamBeginCapture.argtypes = [P, ctypes.c_int]
-        h.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
-        h.hipGraphGetNodes.argtypes = [P, ctypes.POINTER(P), ctypes.POINTER(ctypes.c_size_t)]
-        h.hipGraphNodeGetType.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
-        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, ctypes.c_size_t]
-        h.hipGraphLaunch.argtypes = [P, P]
-        h.hipGraphExecDestroy.argtypes = [P]
-        h.hipGraphDestroy.argtypes = [P]
-        self.h = h
-        self.graph = P()
-        self.exec = P()
-
-    def capture(self, stream, fn):
-        s = ctypes.c_void_p(stream.cuda_stream)
-        assert self.h.hipStreamBeginCapture(s, 1) == 0  # thread-local capture mode
-        try:
-            fn()
-        finally:
-            rc = self.h.hipStreamEndCapture(s, ctypes.byref(self.graph))
-        assert rc == 0
-        assert self.h.hipGraphInstantiate(ctypes.byref(self.exec), self.graph, None, None, 0) == 0
-
-    def node_types(self):
-        n = ctypes.c_size_t(0)
-        assert self.h.hipGraphGetNodes(self.graph, None, ctypes.byref(n)) == 0
-        nodes = (ctypes.c_void_p * n.value)()
-        assert self.h.hipGraphGetNodes(self.graph, nodes, ctypes.byref(n)) == 0
-        types = []
-        for i in range(n.value):
-            t = ctypes.c_int(-1)
-            assert self.h.hipGraphNodeGetType(nodes[i], ctypes.byref(t)) == 0
-            types.append(t.value)
-        return types
-
-    def replay(self, stream):
-        assert self.h.hipGraphLaunch(self.exec, ctypes.c_void_p(stream.cuda_stream)) == 0
-
-    def close(self):
-        self.h.hipGraphExecDestroy(self.exec)
-        self.h.hipGraphDestroy(self.graph)
 
 
 def _captured_replays(prob, ab, replays=4, **kw):

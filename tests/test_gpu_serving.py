@@ -237,3 +237,61 @@ def test_forward_fp32_output_matches_oracle(gpu):
             want = _oracle_rows(q[at:at + T], *hist[s], L + 1 + np.arange(T), ab, out="fp32")
             assert np.array_equal(got[at:at + T], want), (lens, s)
             at += T
+
+
+def test_decode_graph_equals_forward_and_oracle(gpu):
+    """DecodeGraph (block-table update, K/V scatter, digit re-slice and attention captured in one
+    HIP graph, replayed per step) against ExactAttentionBackend.forward on a twin cache: the same
+    bits and flags every step, the same pools, block tables and digit tiles afterwards, every
+    replay's rows equal to the oracle's on the logical history, kernels only in the graph."""
+    import torch
+    from exactattention_amd.graph import NODE_KERNEL
+    from exactattention_amd.serving import DecodeGraph, ExactAttentionBackend, PagedKVCache
+    rng = np.random.default_rng(72)
+    Hq, Hkv, d, P = 4, 2, 128, 16
+    ab = default_alpha_bits(d)
+    lens0 = [30, 64, 100, 17]
+    caches, backs, slots = [], [], []
+    hist = {}
+    pre = [(bf16(rng, (n, Hkv, d)), bf16(rng, (n, Hkv, d))) for n in lens0]
+    for _ in range(2):
+        c = PagedKVCache(num_pages=64, page_size=P, num_kv_heads=Hkv, head_dim=d, max_seqs=6, max_seq_len=160)
+        be = ExactAttentionBackend(c, Hq, ab)
+        ss = [c.add_sequence() for _ in lens0]
+        for s, (k, v) in zip(ss, pre):
+            c.append(s, k, v)
+        caches.append(c)
+        backs.append(be)
+        slots.append(ss)
+    for i, (k, v) in enumerate(pre):
+        hist[i] = (k, v)
+    dg = DecodeGraph(backs[0], slots[0], max_len=140)
+    assert dg.graph.node_types() and all(t == NODE_KERNEL for t in dg.graph.node_types())
+    B = len(lens0)
+    for step in range(20):  # crosses page boundaries (lengths 30 + 20, 64 + 20, ...)
+        q, k, v = bf16(rng, (B, Hq, d)), bf16(rng, (B, Hkv, d)), bf16(rng, (B, Hkv, d))
+        dg.q.copy_(torch.from_numpy(q.view(np.int16)).view(B, 1, Hq, d))
+        dg.k.copy_(torch.from_numpy(k.view(np.int16)))
+        dg.v.copy_(torch.from_numpy(v.view(np.int16)))
+        out_g, fl_g = dg.step()
+        dg.check_flags()
+        out_f, fl_f = backs[1].forward(torch.from_numpy(q.view(np.int16)).cuda(), torch.from_numpy(k.view(np.int16)).cuda(),
+                                       torch.from_numpy(v.view(np.int16)).cuda(), slots[1], [1] * B)
+        backs[1].check_flags(fl_f)
+        torch.cuda.synchronize()
+        got = out_g.cpu().numpy().view(np.uint16)
+        assert np.array_equal(got, out_f.cpu().numpy().view(np.uint16)), step
+        assert not fl_g.cpu().numpy().any() and not fl_f.cpu().numpy().any(), step
+        for i in range(B):
+            hist[i] = (np.concatenate([hist[i][0], k[i:i + 1]]), np.concatenate([hist[i][1], v[i:i + 1]]))
+        if step in (0, 7, 19):
+            for i in range(B):
+                want = _oracle_rows(q[i:i + 1], *hist[i], [len(hist[i][0])], ab)
+                assert np.array_equal(got[i], want[0]), (step, i)
+    torch.cuda.synchronize()
+    a, b = caches
+    assert a.length == b.length and a.pages == b.pages
+    assert torch.equal(a.block_table, b.block_table)
+    assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    assert torch.equal(a.digits, b.digits)
+    dg.close()
