@@ -291,7 +291,34 @@ def long_context_line(steps: int, warmup: int) -> dict:
     return line
 
 
-def prefill_line(steps: int, warmup: int) -> dict:
+PF_PHASES = {14: "dma_wait", 0: "barrier1", 1: "score_mfma", 2: "rebase_digits", 3: "barrier2_dma_fold",
+             4: "pv_mfma_cert", 5: "cold_path", 6: "exchange", 7: "loop_rest", 15: "prologue", 9: "drain",
+             10: "row_totals", 11: "epochs_recip", 12: "round_normal", 13: "round_general"}
+
+
+def prefill_timers(r: dict, reps: int = 3) -> dict:
+    """Phase clocks of the prefill kernel's TIMERS build (s_memtime cycles summed over waves): per
+    wave and tile for the loop phases, per wave for the prologue and epilogue."""
+    import torch
+    from exactattention_amd.hip import launch_hip
+    tm = torch.zeros(16, dtype=torch.int64, device="cuda:0")
+    for _ in range(reps):
+        launch_hip(r["dp"], r["ab"], timers=tm)
+    torch.cuda.synchronize()
+    tv = tm.cpu().numpy().astype(float)
+    tiles = max(1.0, tv[8])  # tiles counted once per wave
+    g = r["dp"].geom
+    r_seg = g["num_tokens"] * (g["num_q_heads"] // g["num_kv_heads"])
+    waves = reps * 8 * g["num_seqs"] * g["num_kv_heads"] * ((r_seg + 31) // 32) * r["dp"].nsplit
+    loop = [14, 0, 1, 2, 3, 4, 5, 6, 7]
+    tot = sum(tv[i] for i in loop)
+    return {"cycles_per_wave_tile": {PF_PHASES[i]: round(tv[i] / tiles, 1) for i in loop},
+            "loop_share": {PF_PHASES[i]: round(tv[i] / tot, 4) for i in loop},
+            "cycles_per_wave": {PF_PHASES[i]: round(tv[i] / waves, 1) for i in (15, 9, 10, 11, 12, 13)},
+            "wave_tiles": int(tv[8])}
+
+
+def prefill_line(steps: int, warmup: int, timers: bool = False) -> dict:
     """C3 (causal prefill, 4096 tokens) on the int8-MFMA prefill kernel."""
     import torch
     r = run_config("C3", steps, warmup)
@@ -315,6 +342,8 @@ def prefill_line(steps: int, warmup: int) -> dict:
         "input_gen_s": round(r["gen_s"], 1),
     }
     line["kv_digits"] = kv_digits_line(r)
+    if timers:
+        line["phase_clocks"] = prefill_timers(r)
     del r
     torch.cuda.empty_cache()
     return line
@@ -477,7 +506,7 @@ def main():
     from exactattention_amd.hip import launch_hip
 
     if args.only == "C3":
-        print(json.dumps({"prefill": prefill_line(args.steps, args.warmup)}), flush=True)
+        print(json.dumps({"prefill": prefill_line(args.steps, args.warmup, args.timers)}), flush=True)
         return
     if args.only == "C4":
         print(json.dumps({"tree_verify": tree_line(args.steps, args.warmup)}), flush=True)

@@ -962,8 +962,10 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         const uint32_t aMn = PA ? aM0 : aM1;        // metadata of tile it + 1
         const bool k_next = it + 1 < t1;
         tick(7);
-        // every DMA landed: K(it) and its metadata, and V(it - 1) (the P.V of this step reads it)
-        wait_vm<0>();
+        // K(it) and its metadata landed. V(it - 1), issued after them, is first read after B2 and
+        // is waited for there; at the first tile nothing else is in flight.
+        if (it > t0) wait_vm<NKI>();
+        else wait_vm<0>();
         tick(14);
         pf_bar();      // B1
         tick(0);
@@ -993,8 +995,9 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         tick(1);
         if (it > t0) rebase_digits(evp);
         tick(2);
-        // every wave has read the K planes of tile it and written the weight digits of tile it - 1:
-        // K(it + 1) with its metadata and V(it) start loading
+        // every wave has read the K planes of tile it and written the weight digits of tile it - 1,
+        // and V(it - 1) has landed: K(it + 1) with its metadata and V(it) start loading
+        wait_vm<0>();
         pf_bar();
         if (k_next) issue_k(it + 1, aMn);
         issue_v(it, aVc);
