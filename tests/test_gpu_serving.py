@@ -89,8 +89,9 @@ def test_serving_session_matches_oracle(gpu):
 
 def test_forward_mixed_batches_match_oracle(gpu):
     """ExactAttentionBackend.forward on flattened mixed batches: prefill chunks and decode tokens
-    of several sequences in one call (the int8 prefill kernel reading the digit-tile cache when the
-    slots are contiguous, slicing on its own when not), decode-only batches, bf16 tensor inputs."""
+    of several sequences in one call, decode-only batches, bf16 tensor inputs. The int8 prefill
+    kernel reads every batch's K/V tiles from the digit-tile cache through the slot map
+    (ea_options.kv_digits_slot), so the out-of-order and non-zero-slot batches check that map."""
     import torch
     from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
     rng = np.random.default_rng(72)
@@ -122,8 +123,8 @@ def test_forward_mixed_batches_match_oracle(gpu):
 
     step([0, 1, 2], [70, 1, 5])           # T = 70: int8 prefill kernel, digits read from the cache
     step([0, 1, 2], [1, 1, 1])            # decode batch
-    step([2, 0], [66, 3])                 # slots out of order: prefill slices its own tiles
-    step([1, 3], [64, 9], as_bf16=True)   # contiguous again, bf16 tensors, a fresh slot
+    step([2, 0], [66, 3])                 # slots out of order: tiles read through the slot map
+    step([1, 3], [64, 9], as_bf16=True)   # non-zero slots, bf16 tensors, a fresh slot
     step([0, 1, 2, 3], [1, 1, 1, 1])
     cache.drop_sequence(1)
     assert cache.add_sequence() == 1
