@@ -490,9 +490,9 @@ int exact_row(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, in
     const bool a_neg = (ab >> 31) != 0;
     const int32_t ae = (af ? af : 1) - 150;
 
-    // ---- scores, logits, weights
-    std::vector<uint32_t> wM((size_t)n);
-    std::vector<i128> wE((size_t)n);
+    // ---- scores and logits
+    std::vector<int32_t> tmv((size_t)n), tev((size_t)n);
+    std::vector<uint32_t> tbv((size_t)n);
     for (int64_t j = 0; j < n; ++j) {
         // exact score at the fixed exponent -266 (the smallest product exponent of two bf16s):
         // every product is |m| < 2^16 at an offset below 2^9
@@ -518,18 +518,41 @@ int exact_row(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, in
             te = (int32_t)r.qe;
             tbits = encode(r, tneg, 1);
         }
-        uint32_t M;
-        i128 E;
-        if (!weight_exact(tm, te, &M, &E)) return EAX_REFUSED;
+        tmv[(size_t)j] = tm;
+        tev[(size_t)j] = te;
+        tbv[(size_t)j] = tbits;
+    }
+    // Logits of magnitude 2^100 or more (fp32 field >= 227): weight exponents t - 23 need more than
+    // 128 bits near 2^128. Distinct such logits differ by at least 2^76, beyond the exponent-spread
+    // limit (the reference refuses those rows too, reference.py:109-110); equal ones give equal
+    // weights, whose common factor 2^t cancels in N / Z, so every weight is taken as 1.
+    bool huge = false, same = true;
+    for (int64_t j = 0; j < n; ++j) {
+        huge |= ((tbv[(size_t)j] >> 23) & 0xFF) >= 227;
+        same &= tbv[(size_t)j] == tbv[0];
+    }
+    if (huge && !same) return EAX_REFUSED;
+
+    // ---- weights
+    std::vector<uint32_t> wM((size_t)n);
+    std::vector<i128> wE((size_t)n);
+    const i128 lim = (i128)1 << 62;  // trace exponents are clamped to +-2^62
+    for (int64_t j = 0; j < n; ++j) {
+        uint32_t M = 1u << 23;
+        i128 E = -23;
+        int64_t we_trace;
+        if (huge) {
+            we_trace = (tmv[(size_t)j] < 0) ? -lim : lim;  // t - 23 for |t| >= 2^100
+        } else {
+            if (!weight_exact(tmv[(size_t)j], tev[(size_t)j], &M, &E)) return EAX_REFUSED;
+            we_trace = (int64_t)(E > lim ? lim : (E < -lim ? -lim : E));
+        }
         wM[(size_t)j] = M;
         wE[(size_t)j] = E;
         if (tr) {
-            if (tr->t_bits) tr->t_bits[j] = tbits;
+            if (tr->t_bits) tr->t_bits[j] = tbv[(size_t)j];
             if (tr->wm) tr->wm[j] = (int32_t)M;
-            if (tr->we) {
-                const i128 lim = (i128)1 << 62;
-                tr->we[j] = (int64_t)(E > lim ? lim : (E < -lim ? -lim : E));
-            }
+            if (tr->we) tr->we[j] = we_trace;
         }
     }
     uint16_t* o16 = (uint16_t*)out;

@@ -132,6 +132,39 @@ def test_exact_row_huge_logits():
         assert np.array_equal(hip.exact_row(q, k, v, ab), want), trial
 
 
+def test_exact_row_logits_near_the_fp32_limit():
+    """Logits t = RN32(alpha s) of 1.5 * 2^127, whose weight exponents t - 23 pass the 128-bit
+    range: keys with one such logit have equal weights (N / Z is the exact mean of v, as the oracle
+    computes with Python integers), and two distinct logits that large lie at least 2^76 apart,
+    past the exponent-spread limit, so the row is refused as the reference refuses it."""
+    hip = _hip()
+    from oracle import exact
+    rng = np.random.default_rng(11)
+    q = np.zeros(8, np.uint16)
+    q[0] = 0x5D80                        # 2^60
+    k = np.zeros((3, 8), np.uint16)
+    k[:, 0] = 0x5D80                     # s = 2^120 for every key
+    v = bf16(rng, (3, 5))
+    ab = int(np.float32(192.0).view(np.uint32))  # t = 1.5 * 2^127
+    for out in ("bf16", "fp32"):
+        want = exact.attention_row(q, k, v, ab, out)
+        assert np.array_equal(hip.exact_row(q, k, v, ab, out), want), out
+    k2 = k.copy()
+    k2[1, 0] = 0x5D81                    # a second, larger logit
+    with pytest.raises(ExactAttentionDomainError):
+        hip.exact_row(q, k2, v, ab)
+    with pytest.raises(exact.DomainError):
+        exact.attention_row(q, k2, v, ab)
+    # one such logit beside t = 0: 2^t overwhelms the other weight, but its exponent does not fit
+    # 128 bits (a wrapped exponent would make it the lightest key and return the other key's v)
+    k3 = k.copy()
+    k3[1, 0] = 0
+    with pytest.raises(ExactAttentionDomainError):
+        hip.exact_row(q, k3, v, ab)
+    with pytest.raises(exact.DomainError):
+        exact.attention_row(q, k3, v, ab)
+
+
 def test_exact_row_spread_beyond_the_reference_limit():
     """Weights 2^(2^21) apart. When the rounding is decided without the lightest key (its term
     cannot move the quotient off +0) the tier returns the bits; where the reference's exact sums
