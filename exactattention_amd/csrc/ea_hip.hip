@@ -631,8 +631,11 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
         const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
         const int hk = hq / P.grp;
         const int64_t tok = b * T + t;
-        const int64_t L = P.kv_len[tok];
-        const uint64_t mask = P.tree_mask ? P.tree_mask[tok] : 0ull;
+        // the row's visible keys (vis_prefix, vis_tree_bits: the set tier 1 attends)
+        const int64_t slen = P.seq_len[b];
+        const int64_t L = vis_prefix(P.kv_len[tok], slen);
+        const uint64_t mask =
+            P.tree_mask ? vis_tree_bits(P.tree_mask[tok], (int64_t)P.tree_base[b], L, slen) : 0ull;
         const int64_t nkeys = L + __popcll(mask);
         const int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
         if (tid == 0) S.flag = 0;
@@ -940,17 +943,18 @@ __global__ void __launch_bounds__(256) ea_list_all(Params P) {
 }
 
 // The host exact tier's input for one row: its q row, then the K rows and the V rows of its
-// visible keys (the kv_len prefix, then the tree keys in bit order), packed in dst as
-// [q d][K nkeys x d][V nkeys x dv], one element per thread.
+// visible keys (the prefix, then the tree keys in bit order: vis_prefix, vis_tree_bits), packed in
+// dst as [q d][K nkeys x d][V nkeys x dv], one element per thread.
 __global__ void __launch_bounds__(256) ea_gather_row(Params P, int64_t row, int64_t nkeys, uint16_t* dst) {
     const int d = P.g.head_dim, dv = P.g.head_dim_v, T = P.g.num_tokens, Hq = P.g.num_q_heads;
     const int64_t b = row / ((int64_t)T * Hq);
     const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
     const int hk = hq / P.grp;
     const int64_t tok = b * T + t;
-    const int64_t L = P.kv_len[tok];
-    const uint64_t mask = P.tree_mask ? P.tree_mask[tok] : 0ull;
+    const int64_t slen = P.seq_len[b];
+    const int64_t L = vis_prefix(P.kv_len[tok], slen);
     const int64_t tb = P.tree_mask ? P.tree_base[b] : 0;
+    const uint64_t mask = P.tree_mask ? vis_tree_bits(P.tree_mask[tok], tb, L, slen) : 0ull;
     const int64_t total = d + nkeys * (int64_t)(d + dv);
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         if (i < d) {
@@ -1354,7 +1358,7 @@ int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_optio
     Plan pl;
     int rc = make_plan(g, o, &pl);
     if (rc) return rc;
-    if (!bf || !bf->q || !bf->k || !bf->v || !bf->kv_len || !bf->out || !bf->flags) return -1;
+    if (!bf || !bf->q || !bf->k || !bf->v || !bf->seq_len || !bf->kv_len || !bf->out || !bf->flags) return -1;
     if (bf->tree_mask && !bf->tree_base) return -1;
     if (((o->alpha_bits >> 23) & 0xFF) == 0xFF) return -3;
     if (pl.rows == 0) return 0;
@@ -1375,18 +1379,21 @@ int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_optio
     P.tree_mask = bf->tree_mask; P.tree_base = bf->tree_base;
     P.grp = pl.grp; P.pshift = pl.pshift; P.rows = pl.rows;
     const int d = g->head_dim, dv = g->head_dim_v, T = g->num_tokens, Hq = g->num_q_heads;
-    // visible keys per listed row: the kv_len prefix plus the tree keys
+    // visible keys per listed row: the prefix plus the tree keys (vis_prefix, vis_tree_bits)
     std::vector<int64_t> nk(todo.size());
     int64_t maxk = 0;
     for (size_t i = 0; i < todo.size(); ++i) {
         const int64_t row = todo[i], b = row / ((int64_t)T * Hq), t = (row / Hq) % T, tok = b * T + t;
-        int32_t L = 0;
+        int32_t L = 0, sl = 0, tb = 0;
         uint64_t m = 0;
         if ((e = hipMemcpy(&L, bf->kv_len + tok, 4, hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
-        if (bf->tree_mask && (e = hipMemcpy(&m, bf->tree_mask + tok, 8, hipMemcpyDeviceToHost)) != hipSuccess)
-            return herr(e);
-        if (L < 0) return -1;
-        nk[i] = (int64_t)L + __builtin_popcountll(m);
+        if ((e = hipMemcpy(&sl, bf->seq_len + b, 4, hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
+        if (bf->tree_mask) {
+            if ((e = hipMemcpy(&m, bf->tree_mask + tok, 8, hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
+            if ((e = hipMemcpy(&tb, bf->tree_base + b, 4, hipMemcpyDeviceToHost)) != hipSuccess) return herr(e);
+        }
+        const int64_t Lc = vis_prefix(L, sl);
+        nk[i] = Lc + __builtin_popcountll(bf->tree_mask ? vis_tree_bits(m, tb, Lc, sl) : 0ull);
         maxk = nk[i] > maxk ? nk[i] : maxk;
     }
     const size_t cap = (size_t)(d + maxk * (int64_t)(d + dv));

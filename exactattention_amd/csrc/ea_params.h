@@ -104,6 +104,23 @@ __device__ __forceinline__ bool visible(const Params& P, int64_t tok, int64_t b,
     return false;
 }
 
+// The visible keys of a query token, the set every tier attends: the prefix n < Lc with
+// Lc = min(kv_len, seq_len) (0 when kv_len < 0), and the tree keys tree_base + i (bit i of the tree
+// mask) at or past Lc and below seq_len, so a key in both counts once. vis_tree_bits keeps those
+// tree bits; the prefix clip is the caller's. Host and device.
+__host__ __device__ inline uint64_t vis_tree_bits(uint64_t mask, int64_t tb, int64_t Lc, int64_t slen) {
+    int64_t lo = Lc - tb, hi = slen - tb;  // keep bits i with lo <= i < hi
+    lo = lo < 0 ? 0 : (lo > 64 ? 64 : lo);
+    hi = hi < 0 ? 0 : (hi > 64 ? 64 : hi);
+    if (hi <= lo) return 0;
+    const uint64_t below_hi = hi >= 64 ? ~0ull : ((1ull << hi) - 1);
+    const uint64_t below_lo = lo >= 64 ? ~0ull : ((1ull << lo) - 1);
+    return mask & below_hi & ~below_lo;
+}
+__host__ __device__ inline int64_t vis_prefix(int64_t kv_len, int64_t slen) {
+    return kv_len < 0 ? 0 : (kv_len < slen ? kv_len : slen);
+}
+
 // end of the visible key range of a query token
 __device__ __forceinline__ int64_t vis_end(const Params& P, int64_t tok, int64_t b) {
     int64_t e = P.kv_len[tok];

@@ -43,8 +43,9 @@ typedef struct ihipStream_t* ea_stream_t; /* = hipStream_t */
  *                     off_b = block_table_offset ? block_table_offset[b] : b*block_table_stride
  *   K[b, n, hk, i]    = k + page*k_page_stride + slot*k_slot_stride + hk*k_head_stride + i  (V alike)
  * Row (b, t, h) attends keys n < kv_len[b*T + t], plus, with tree_mask, keys tree_base[b] + i for
- * every set bit i of tree_mask[b*T + t] (speculative tree verification). Causal prefill, chunked
- * prefill, decode and verification chains are all kv_len prefixes.
+ * every set bit i of tree_mask[b*T + t] (speculative tree verification); only keys below
+ * seq_len[b] count, and a key in both parts counts once (every tier attends this same set).
+ * Causal prefill, chunked prefill, decode and verification chains are all kv_len prefixes.
  */
 typedef struct ea_geometry {
     int32_t num_seqs, num_tokens, num_q_heads, num_kv_heads, head_dim, head_dim_v;

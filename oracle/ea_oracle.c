@@ -970,8 +970,22 @@ static void* geom_worker(void* arg) {
         i64 b = r / ((i64)T * Hq), t = (r / Hq) % T, hq = r % Hq;
         int hk = (int)(hq / grp);
         i64 tok = b * T + t;
+        /* visible keys: the prefix below min(kv_len, seq_len) and the tree keys at or past it and
+           below seq_len, each key once (the serving geometry's definition) */
+        i64 slen = Bf->seq_len[b];
         i64 L = Bf->kv_len[tok];
-        uint64_t mask = Bf->tree_mask ? Bf->tree_mask[tok] : 0;
+        L = L < 0 ? 0 : (L < slen ? L : slen);
+        uint64_t mask = 0;
+        if (Bf->tree_mask) {
+            i64 tb = Bf->tree_base[b], lo = L - tb, hi = slen - tb;
+            lo = lo < 0 ? 0 : (lo > 64 ? 64 : lo);
+            hi = hi < 0 ? 0 : (hi > 64 ? 64 : hi);
+            if (hi > lo) {
+                uint64_t below_hi = hi >= 64 ? ~0ull : ((1ull << hi) - 1);
+                uint64_t below_lo = lo >= 64 ? ~0ull : ((1ull << lo) - 1);
+                mask = Bf->tree_mask[tok] & below_hi & ~below_lo;
+            }
+        }
         i64 n = L + __builtin_popcountll(mask);
         if (!scratch_reserve(&s, g, n)) { J->ok = 0; break; }
         if (n > cap) {

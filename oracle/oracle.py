@@ -180,11 +180,15 @@ def row_keys(prob: dict, row: int):
     b, t, hq = row // (T * Hq), (row // Hq) % T, row % Hq
     hk = hq // grp
     tok = b * T + t
-    L = int(prob["kv_len"][tok])
+    # visible keys: the prefix below min(kv_len, seq_len), then the tree keys at or past it and
+    # below seq_len, each key once
+    slen = int(prob["seq_len"][b])
+    L = max(0, min(int(prob["kv_len"][tok]), slen))
     keys = list(range(L))
     if prob.get("tree_mask") is not None:
         m = int(prob["tree_mask"][tok])
-        keys += [int(prob["tree_base"][b]) + i for i in range(64) if (m >> i) & 1]
+        tb = int(prob["tree_base"][b])
+        keys += [tb + i for i in range(64) if (m >> i) & 1 and L <= tb + i < slen]
     kflat, vflat, qflat = prob["k"].reshape(-1), prob["v"].reshape(-1), prob["q"].reshape(-1)
     d, dv = gm["head_dim"], gm["head_dim_v"]
 

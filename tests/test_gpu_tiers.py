@@ -141,6 +141,47 @@ def _cancellation_problem(B=1):
     return problem.contiguous(q, k, v, np.full((B, 1), 3)), 0x3F800000
 
 
+def _overlap_problem(rng, B, T, Hq, Hkv, S, d, dv):
+    """Visible sets built from overlapping pieces: kv_len past seq_len on some tokens, and tree masks
+    whose keys start inside the prefix and run past seq_len (the storage holds S keys, seq_len is
+    shorter, so the keys past it are never read)."""
+    q, k, v = bf16(rng, (B, T, Hq, d)), bf16(rng, (B, Hkv, S, d)), bf16(rng, (B, Hkv, S, dv))
+    seq = np.array([S - 9 - 17 * b for b in range(B)], dtype=np.int32)
+    kv = rng.integers(0, S + 1, size=(B, T))
+    tb = (seq - 40).astype(np.int32)
+    tm = rng.integers(0, 2 ** 63, size=(B, T), dtype=np.int64).astype(np.uint64) | np.uint64(1 << 63)
+    return problem.contiguous(q, k, v, kv, seq_len=seq, tree_mask=tm, tree_base=tb)
+
+
+@pytest.mark.parametrize("kernel", list(KERNEL_SHAPES))
+def test_visible_set_is_a_union_below_seq_len(gpu, kernel):
+    """Every tier attends one set per row: the prefix below min(kv_len, seq_len) and the tree keys
+    at or past it and below seq_len, each key once. Tier 1 on each kernel, tier 2 forced on every
+    row, and the host exact tier on every row (flags set to 1 before ea_hip_exact_rows) all equal
+    the oracle's bits."""
+    import torch
+    from exactattention_amd.hip import DeviceProblem, exact_rows, launch_hip
+    shp = dict(KERNEL_SHAPES[kernel])
+    shp["S"] = 200
+    prob = _overlap_problem(np.random.default_rng(41), **shp)
+    ab = default_alpha_bits(shp["d"])
+    want, _ = _oracle(prob, ab)
+    got, flags, st = _run(prob, ab, kernel=kernel)
+    assert not flags.any(), st
+    assert np.array_equal(got, want)
+    got2, flags2, st2 = _run(prob, ab, kernel=kernel, force_tier2=True)
+    assert not flags2.any() and st2["tier2_certified"] == st2["rows"], st2
+    assert np.array_equal(got2, want)
+    dp = DeviceProblem(prob, "bf16", 0, "cuda:0", kernel)
+    launch_hip(dp, ab)
+    dp.flags.fill_(1)
+    dp.out.zero_()
+    exact_rows(dp, ab)
+    torch.cuda.synchronize()
+    assert not dp.flags.any().item()
+    assert np.array_equal(dp.out.cpu().numpy().view(np.uint16).reshape(want.shape), want)
+
+
 def test_host_exact_tier_finishes_rows_the_device_cannot(gpu):
     from exactattention_amd.hip import attention_problem
     prob, ab = _cancellation_problem()
