@@ -347,13 +347,14 @@ __global__ void __launch_bounds__(256) ea_pf_kvslice(Params P) {
 //   B1    K(it), its metadata and V(it-1) landed; the row maxima of tile it-1 are in sX
 //         score MFMAs of tile it (K planes and q digits from LDS); while they run, the base move
 //         (epoch fold when a base moves) and the weight digits of tile it-1 to sWD
-//   B2    every wave has read the K planes of tile it and written its digits: K(it+1) with its
-//         metadata and V(it) start loading; fp64 scores; P.V MFMAs of tile it-1 (digits from
-//         sWD), certification of tile it, cold path; row maxima of tile it to sX
+//   B2    every wave has read the K planes of tile it and written its digits: row group 0's
+//         waves issue the DMAs of K(it+1) with its metadata and of V(it) while row group 1's go
+//         on; fp64 scores; P.V MFMAs of tile it-1 (digits from sWD), certification of tile it,
+//         cold path; row maxima of tile it to sX
 // V and the metadata are double-buffered (the two parities are two copies of the step). The DMAs
 // are issued as inline asm, so the compiler adds no waits of its own; barriers are s_barrier after
-// lgkmcnt(0) (no vmcnt(0): DMAs stay in flight across them) and the only DMA wait is the vmcnt(0)
-// before B1.
+// lgkmcnt(0) (no vmcnt(0): DMAs stay in flight across them) and the DMA waits are vmcnt(NKI)
+// before B1 (K(it) and its metadata) and vmcnt(0) before B2 (V(it-1)).
 // ------------------------------------------------------------------------------------------------
 struct PfX {
     int32_t a, b;
@@ -400,7 +401,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     constexpr int RPB = 16 * NWB / SPLIT;  // rows per block (32)
     constexpr int NKT = 4 / SPLIT;         // key groups of 16 per wave
     constexpr int NCT = 8 / SPLIT;         // channel tiles of 16 per wave
-    constexpr int NKI = 32 / NWB;          // K (and V) DMA instructions per wave and tile
+    constexpr int NKI = 64 / NWB;          // K (and V) DMA instructions per issuing wave and tile
     extern __shared__ __align__(16) unsigned char smem[];
     uint8_t* const sK = smem + PF_OFF_K;     // K planes of the current tile
     uint8_t* const sV0 = smem + PF_OFF_V0;   // V planes, even tiles
@@ -502,9 +503,13 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     const double* const T1s = sT1;
     const double* const T2 = sT2;
 
-    // tile DMA: per wave NKI instructions of 1 KB for the K (or V) planes, one for the metadata.
-    // Issued through pf_dma (inline asm), so the compiler inserts no waits of its own before the
-    // LDS reads: every read of a DMA'd buffer follows an explicit vmcnt wait for that buffer.
+    // tile DMA: only the SPLIT waves of row group 0 issue, each NKI instructions of 1 KB for the K
+    // (or V) planes and its share of the 4 KB of metadata. A wave stalls at a DMA instruction until
+    // the texture path accepts it (about 2,000 cycles for a tile's 68 instructions); with one
+    // issuing wave per SIMD the other wave on that SIMD, of row group 1, runs its P.V and
+    // certification meanwhile instead of stalling beside it. Issued through pf_dma (inline asm),
+    // so the compiler inserts no waits of its own before the LDS reads: every read of a DMA'd
+    // buffer follows an explicit vmcnt wait for that buffer (row group 1 has nothing in flight).
     auto rsrc = [&](int tile) __attribute__((always_inline)) {
         const uint64_t src = (uint64_t)(P.pfkv + (kseg * P.pf_ntiles + tile) * EA_PF_TILE_BYTES);
         v4i r = {(int)(uint32_t)src, (int)((uint32_t)(src >> 32) & 0xFFFFu), EA_PF_TILE_BYTES, 0x00020000};
@@ -516,19 +521,22 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
     const uint32_t aK = lds_addr(sK), aV0 = lds_addr(sV0), aV1 = lds_addr(sV1), aM0 = lds_addr(sM0),
                    aM1 = lds_addr(sM1);
     auto issue_k = [&](int tile, uint32_t mdst) __attribute__((always_inline)) {
+        if (rg != 0) return;
         const v4i rs = rsrc(tile);
 #pragma unroll
         for (int q = 0; q < NKI; ++q) {
-            const int off = (q * NWB + w) * 1024;
+            const int off = (q * SPLIT + hh) * 1024;
             pf_dma(rs, aK + off, vlane, off);
         }
-        if (w < 4) pf_dma(rs, mdst + w * 1024, vlane, EA_PF_META_OFF + w * 1024);  // 4 KB of metadata
+#pragma unroll
+        for (int m = hh; m < 4; m += SPLIT) pf_dma(rs, mdst + m * 1024, vlane, EA_PF_META_OFF + m * 1024);
     };
     auto issue_v = [&](int tile, uint32_t vdst) __attribute__((always_inline)) {
+        if (rg != 0) return;
         const v4i rs = rsrc(tile);
 #pragma unroll
         for (int q = 0; q < NKI; ++q) {
-            const int off = (q * NWB + w) * 1024;
+            const int off = (q * SPLIT + hh) * 1024;
             pf_dma(rs, vdst + off, vlane, 32768 + off);
         }
     };
