@@ -1202,6 +1202,14 @@ int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* byt
     return 0;
 }
 
+int ea_hip_reads_kv_digits(const ea_geometry* g, const ea_options* o, int32_t* reads) {
+    Plan pl;
+    int rc = make_plan(g, o, &pl);
+    if (rc) return rc;
+    if (reads) *reads = (pl.prefill && o->kv_digits) ? 1 : 0;  // the test ea_hip_attention makes
+    return 0;
+}
+
 int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, void* workspace,
                      size_t workspace_bytes, ea_stream_t stream) {
     Plan pl;

@@ -73,6 +73,9 @@ def load():
         lib.ea_hip_workspace_size.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Options),
                                               ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_int32)]
         lib.ea_hip_workspace_size.restype = ctypes.c_int
+        lib.ea_hip_reads_kv_digits.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Options),
+                                               ctypes.POINTER(ctypes.c_int32)]
+        lib.ea_hip_reads_kv_digits.restype = ctypes.c_int
         lib.ea_hip_attention.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), ctypes.POINTER(Options),
                                          P, ctypes.c_size_t, P]
         lib.ea_hip_attention.restype = ctypes.c_int

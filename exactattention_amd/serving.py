@@ -10,8 +10,11 @@ management to that script. Here the cache lives on the device:
   * K and V pools in NHD pages [num_pages, page_size, Hkv, d] of bf16 bits, pages handed out from a
     free list; block table [max_seqs, max_pages_per_seq] int32, one row per sequence slot;
   * optionally the int8 digit tiles of the prefill path (the KV slice format, exactattn_hip.h
-    ea_hip_kv_digits_update), re-sliced for exactly the tiles an append touches, so a prefill
-    chunk reads its K/V tiles instead of slicing the whole prefix again.
+    ea_hip_kv_digits_update), so a prefill chunk or a tree verification reads its K/V tiles
+    instead of slicing the whole prefix again. They are re-sliced lazily: an append or a truncation
+    only marks the slot's tiles stale from its first changed key, and the stale tiles of every slot
+    are re-sliced in one update right before a call that reads the cache (the library says which
+    calls do: ea_hip_reads_kv_digits). Decode steps, which read the bf16 cache, slice nothing.
 
 Every call enqueues on torch's current stream and copies its result to the host (the caller sees
 (out bits, flags) like the reference's backends).
@@ -103,6 +106,8 @@ class PagedKVCache:
         self.pages = [[] for _ in range(max_seqs)]
         self.length = [0] * max_seqs
         self.live = [False] * max_seqs
+        # first key whose digit tile is out of date, per slot (None: every tile is current)
+        self.stale = [None] * max_seqs
         self.tiles = (max_seq_len + TILE - 1) // TILE
         self.digits = None
         if digits and head_dim == 128:
@@ -114,7 +119,7 @@ class PagedKVCache:
     def add_sequence(self) -> int:
         for s in range(self.max_seqs):
             if not self.live[s]:
-                self.live[s], self.length[s], self.pages[s] = True, 0, []
+                self.live[s], self.length[s], self.pages[s], self.stale[s] = True, 0, [], None
                 return s
         raise RuntimeError("no free sequence slot")
 
@@ -130,7 +135,7 @@ class PagedKVCache:
 
     def drop_sequence(self, s: int) -> None:
         self.free.extend(self.pages[s][::-1])
-        self.pages[s], self.length[s], self.live[s] = [], 0, False
+        self.pages[s], self.length[s], self.live[s], self.stale[s] = [], 0, False, None
 
     def _digit_base(self, s: int) -> int:
         return self.digits.data_ptr() + s * self.Hkv * self.tiles * hip.EA_PF_TILE_BYTES
@@ -153,8 +158,8 @@ class PagedKVCache:
 
     def append_batch(self, seqs, counts, k_bits, v_bits) -> None:
         """Append counts[i] keys to slot seqs[i] for every i, the keys flattened in that order
-        (k_bits, v_bits: (sum(counts), Hkv, d)); one device scatter for the batch, then one
-        digit re-slice over every slot the batch touched."""
+        (k_bits, v_bits: (sum(counts), Hkv, d)); one device scatter for the batch. The digit tiles
+        the keys land in are marked stale (flush re-slices them)."""
         plan = self._plan_append(seqs, counts, k_bits, v_bits)
         if plan is not None:
             self._apply_append(plan, self.stage.put(*plan["arrays"]))
@@ -193,29 +198,26 @@ class PagedKVCache:
         b_of = np.repeat(np.arange(len(seqs)), cnt)
         pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
         idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
-        kb = np.zeros(self.max_seqs, dtype=np.int32)
-        ke = np.zeros(self.max_seqs, dtype=np.int32)
-        kb[sa], ke[sa] = L, L + cnt
-        for s, e in zip(seqs, (L + cnt).tolist()):
+        for s, a, e in zip(seqs, L.tolist(), (L + cnt).tolist()):
             self.length[s] = e
+            self._mark_stale(s, a)
         arrays = [idx]
         if grown:
             arrays += [np.asarray(grown, dtype=np.int64), self.bt_host[grown]]
-        if self.digits is not None:
-            arrays += [np.asarray(self.length, dtype=np.int32), kb, ke]
-        return {"k": k_new, "v": v_new, "grown": bool(grown), "span": max(counts), "arrays": arrays}
+        return {"k": k_new, "v": v_new, "grown": bool(grown), "arrays": arrays}
 
-    def _apply_append(self, plan, dev, stream=None) -> None:
-        """Device half of an append: block-table rows, the K/V scatter, the digit re-slice."""
-        idx_d, i = dev[0], 1
+    def _apply_append(self, plan, dev) -> None:
+        """Device half of an append: block-table rows and the K/V scatter."""
+        idx_d = dev[0]
         if plan["grown"]:
             self.block_table.index_copy_(0, dev[1], dev[2])
-            i = 3
         H, d = self.Hkv, self.d
         self.k.view(-1, H, d).index_copy_(0, idx_d, plan["k"].reshape(-1, H, d))
         self.v.view(-1, H, d).index_copy_(0, idx_d, plan["v"].reshape(-1, H, d))
+
+    def _mark_stale(self, s: int, key: int) -> None:
         if self.digits is not None:
-            self._reslice_all(dev[i], dev[i + 1], dev[i + 2], plan["span"], stream)
+            self.stale[s] = key if self.stale[s] is None else min(self.stale[s], key)
 
     def truncate(self, s: int, length: int) -> None:
         """Drop the keys at or past `length` (rejected draft nodes); the tile holding the new end is
@@ -227,8 +229,26 @@ class PagedKVCache:
         keep = (length + self.P - 1) // self.P
         self.free.extend(self.pages[s][keep:][::-1])
         self.pages[s] = self.pages[s][:keep]
+        if self.stale[s] is not None and self.stale[s] >= length:
+            self.stale[s] = None  # the stale keys are gone
         if length % TILE:
-            self._reslice(s, length - 1, length)
+            self._mark_stale(s, length - 1)  # the tile holding the new end: its tail is now empty
+
+    def flush(self, stream=None) -> None:
+        """Re-slice the stale digit tiles of every slot (keys stale[s] .. length[s] - 1), in one
+        ea_hip_kv_digits_update on `stream` (torch's current stream by default)."""
+        if self.digits is None:
+            return
+        dirty = [(s, a) for s, a in enumerate(self.stale) if a is not None and a < self.length[s]]
+        self.stale = [None] * self.max_seqs
+        if not dirty:
+            return
+        kb = np.zeros(self.max_seqs, dtype=np.int32)
+        ke = np.zeros(self.max_seqs, dtype=np.int32)
+        for s, a in dirty:
+            kb[s], ke[s] = a, self.length[s]
+        seq_d, kb_d, ke_d = self.stage.put(np.asarray(self.length, dtype=np.int32), kb, ke)
+        self._reslice_all(seq_d, kb_d, ke_d, int((ke - kb).max()), stream)
 
     def _reslice_all(self, seq_d, kb_d, ke_d, span: int, stream=None) -> None:
         """Re-slice keys kb[s]..ke[s]-1 of every slot s (device int32 vectors over all max_seqs
@@ -244,21 +264,6 @@ class PagedKVCache:
         hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(gc), ctypes.byref(b), kb_d.data_ptr(), ke_d.data_ptr(), span,
                                                ctypes.c_void_p(self.digits.data_ptr()), self.tiles,
                                                stream or hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
-
-    def _reslice(self, s: int, a: int, e: int) -> None:
-        if self.digits is None or e <= a:
-            return
-        torch = self.torch
-        lib = hip.load()
-        g = hip.geometry(self._geom1(s, 1, self.Hkv, self.length[s]))
-        seq, kb, ke, off = self.stage.put(np.array([self.length[s]], dtype=np.int32), np.array([a], dtype=np.int32),
-                                          np.array([e], dtype=np.int32), np.array([s * self.max_pages], dtype=np.int64))
-        b = hip.Buffers(q=None, k=self.k.data_ptr(), v=self.v.data_ptr(), seq_len=seq.data_ptr(), kv_len=None,
-                        block_table=self.block_table.data_ptr(), block_table_offset=off.data_ptr(), tree_mask=None,
-                        tree_base=None, out=None, flags=None)
-        hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(g), ctypes.byref(b), kb.data_ptr(), ke.data_ptr(), e - a,
-                                               ctypes.c_void_p(self._digit_base(s)), self.tiles,
-                                               hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
 
 
 class ExactAttentionBackend:
@@ -306,6 +311,11 @@ class ExactAttentionBackend:
                 # slot map: sequence b's tiles live at cache slot seqs[b]
                 o.kv_digits = ctypes.c_void_p(c.digits.data_ptr())
                 o.kv_digits_slot = staged[2].data_ptr()
+            reads = ctypes.c_int32(0)
+            hip._check(lib.ea_hip_reads_kv_digits(ctypes.byref(gc), ctypes.byref(o), ctypes.byref(reads)),
+                       "ea_hip_reads_kv_digits")
+            if reads.value:
+                c.flush(stream)  # the stale tiles, re-sliced ahead of the call in stream order
         nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
         hip._check(lib.ea_hip_workspace_size(ctypes.byref(gc), ctypes.byref(o), ctypes.byref(nb), ctypes.byref(ns)),
                    "ea_hip_workspace_size")
@@ -382,7 +392,7 @@ class ExactAttentionBackend:
         n_app = len(plan["arrays"])
         dev = c.stage.put(*plan["arrays"], *mine)
         st = hip._stream_ptr(torch)
-        c._apply_append(plan, dev[:n_app], st)
+        c._apply_append(plan, dev[:n_app])
         kvl, staged = dev[n_app], (dev[n_app + 1], dev[n_app + 2], dev[n_app + 3])
         row = dev[n_app + 4] if T > 1 else None
         q16 = query.view(torch.int16) if query.dtype != torch.int16 else query
@@ -458,7 +468,8 @@ class ExactAttentionBackend:
                 m |= 1 << j
                 j = parents[j]
             mask[0, i] = m
-        res, fl = self._run([s], np.asarray(q)[None], np.full((1, N), L), tree_mask=mask, tree_base=[L])
+        res, fl = self._run([s], np.asarray(q)[None], np.full((1, N), L), tree_mask=mask, tree_base=[L],
+                            digits_slot=s)
         return res[0], fl
 
     def accept(self, s: int, prefix_len: int, path, k, v) -> None:
@@ -472,8 +483,9 @@ class ExactAttentionBackend:
 
 class DecodeGraph:
     """One decode step of a fixed batch of sequence slots (one new token each), captured once in a
-    HIP graph and replayed per step: the block-table update, the K/V scatter into the paged pools,
-    the digit re-slice of the touched tiles and the certified attention launch. Per step the host
+    HIP graph and replayed per step: the block-table update, the K/V scatter into the paged pools
+    and the certified attention launch (the decode kernel reads the bf16 cache; the digit tiles the
+    new keys land in are only marked stale, for the next call that reads them). Per step the host
     plans the appends (page allocation, scatter slots, lengths) into a pinned buffer, enqueues one
     copy of it and one graph launch on torch's current stream; there is no host synchronisation.
 
@@ -491,7 +503,7 @@ class DecodeGraph:
         self.be, self.c, self.torch = backend, c, torch
         c._check_slots(seqs)
         self.seqs = np.asarray(seqs, dtype=np.int64)
-        B, Hq, Hkv, d, ms = len(seqs), backend.Hq, c.Hkv, c.d, c.max_seqs
+        B, Hq, Hkv, d = len(seqs), backend.Hq, c.Hkv, c.d
         self.B = B
         self.max_len = int(min(max_len or c.max_seq_len, c.max_seq_len))
         if max(c.length[s] for s in seqs) + 1 > self.max_len:
@@ -503,13 +515,11 @@ class DecodeGraph:
         fp32 = backend.out == "fp32"
         self.out = torch.empty((B, 1, Hq, d), dtype=torch.int32 if fp32 else torch.int16, device=dev)
         self.flags = torch.empty(B * Hq, dtype=torch.uint8, device=dev)
-        # metadata layout (bytes): idx, bt_pos, bt_off (B int64); bt_val, kvl (B int32); kb, ke,
-        # lens (max_seqs int32)
+        # metadata layout (bytes): idx, bt_pos, bt_off (B int64); bt_val, kvl (B int32)
         lay = {}
         at = 0
         for name, n, dt in (("idx", B, np.int64), ("bt_pos", B, np.int64), ("bt_off", B, np.int64),
-                            ("bt_val", B, np.int32), ("kvl", B, np.int32), ("kb", ms, np.int32),
-                            ("ke", ms, np.int32), ("lens", ms, np.int32)):
+                            ("bt_val", B, np.int32), ("kvl", B, np.int32)):
             lay[name] = (at, n, dt)
             at += (n * np.dtype(dt).itemsize + 255) // 256 * 256
         self._nbytes = at
@@ -550,13 +560,6 @@ class DecodeGraph:
                                 block_table=c.block_table.data_ptr(), block_table_offset=self.dv["bt_off"].data_ptr(),
                                 tree_mask=None, tree_base=None, out=self.out.data_ptr(),
                                 flags=self.flags.data_ptr())
-        if c.digits is not None:
-            gd = c._geom1(0, 1, Hkv, c.max_seq_len)
-            gd["num_seqs"] = ms
-            self.gd = hip.geometry(gd)
-            self.bd = hip.Buffers(q=None, k=c.k.data_ptr(), v=c.v.data_ptr(), seq_len=self.dv["lens"].data_ptr(),
-                                  kv_len=None, block_table=c.block_table.data_ptr(), block_table_offset=None,
-                                  tree_mask=None, tree_base=None, out=None, flags=None)
         # captured on a side stream (capture records the work without running it); replayed on
         # torch's current stream, right after the step's metadata copy
         self.graph = HipGraph()
@@ -573,10 +576,6 @@ class DecodeGraph:
         H, dd = c.Hkv, c.d
         c.k.view(-1, H, dd).index_copy_(0, d["idx"], self.k)
         c.v.view(-1, H, dd).index_copy_(0, d["idx"], self.v)
-        if c.digits is not None:
-            hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(self.gd), ctypes.byref(self.bd), d["kb"].data_ptr(),
-                                                   d["ke"].data_ptr(), 1, ctypes.c_void_p(c.digits.data_ptr()),
-                                                   c.tiles, st), "ea_hip_kv_digits_update")
         hip._check(lib.ea_hip_attention(ctypes.byref(self.gc), ctypes.byref(self.bufs), ctypes.byref(self.o),
                                         self.ws.data_ptr(), self.ws_bytes, st), "ea_hip_attention")
 
@@ -607,13 +606,9 @@ class DecodeGraph:
         hv["bt_pos"][:] = seqs * c.max_pages + pg
         L += 1
         hv["kvl"][:] = L
-        hv["kb"][:] = 0
-        hv["ke"][:] = 0
-        hv["kb"][seqs] = L - 1
-        hv["ke"][seqs] = L
         for s, n in zip(seqs.tolist(), L.tolist()):
             c.length[s] = n
-        hv["lens"][:] = c.length
+            c._mark_stale(s, n - 1)  # the digit tiles are re-sliced when a call reads them
         return i
 
     def step(self):

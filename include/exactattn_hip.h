@@ -135,6 +135,14 @@ typedef struct ea_options {
  * partial buffers itself, src/exactattn/triton_kernels.py:1411-1448). */
 int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* bytes, int32_t* nsplit);
 
+/* Whether ea_hip_attention with this geometry and these options reads o->kv_digits: *reads = 1
+ * when kv_digits is set and the step takes the int8 prefill path, else 0. A caller that re-slices
+ * its digit-tile cache lazily (only the tiles appends made stale, and only when they are read)
+ * brings the cache up to date before exactly these calls. Returns 0 or the negative codes of
+ * ea_hip_workspace_size. Reference counterpart: none (the reference slices the whole cache at
+ * every launch, src/exactattn/triton_kernels.py:1255-1280). */
+int ea_hip_reads_kv_digits(const ea_geometry* g, const ea_options* o, int32_t* reads);
+
 /* Enqueue one certified attention step on `stream`: q prep, tier-1 split kernel, combine with
  * certified rounding, device tier 2 for rows tier 1 could not certify. No host transfer, no
  * synchronisation, fixed grids: capturable in a hipGraph. The caller owns every buffer; the

@@ -241,11 +241,17 @@ def test_forward_fp32_output_matches_oracle(gpu):
 
 
 def test_decode_graph_equals_forward_and_oracle(gpu):
-    """DecodeGraph (block-table update, K/V scatter, digit re-slice and attention captured in one
-    HIP graph, replayed per step) against ExactAttentionBackend.forward on a twin cache: the same
-    bits and flags every step, the same pools, block tables and digit tiles afterwards, every
-    replay's rows equal to the oracle's on the logical history, kernels only in the graph."""
+    """DecodeGraph (block-table update, K/V scatter and attention captured in one HIP graph,
+    replayed per step) against ExactAttentionBackend.forward on a twin cache: the same bits and
+    flags every step, the same pools and block tables afterwards, every replay's rows equal to the
+    oracle's on the logical history, kernels only in the graph. Neither path slices digit tiles
+    during the decode steps; the stale tiles they leave are re-sliced by a flush (both caches then
+    equal a third cache sliced in one update) and by the next call that reads them (a 64-token
+    chunk through the int8 prefill kernel after the graph's steps, against the oracle)."""
+    import ctypes
+
     import torch
+    from exactattention_amd import hip
     from exactattention_amd.graph import NODE_KERNEL
     from exactattention_amd.serving import DecodeGraph, ExactAttentionBackend, PagedKVCache
     rng = np.random.default_rng(72)
@@ -290,9 +296,30 @@ def test_decode_graph_equals_forward_and_oracle(gpu):
                 want = _oracle_rows(q[i:i + 1], *hist[i], [len(hist[i][0])], ab)
                 assert np.array_equal(got[i], want[0]), (step, i)
     torch.cuda.synchronize()
+    dg.close()
     a, b = caches
     assert a.length == b.length and a.pages == b.pages
     assert torch.equal(a.block_table, b.block_table)
     assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
-    assert torch.equal(a.digits, b.digits)
-    dg.close()
+    # a chunk that reads the graph cache's tiles (the int8 prefill kernel) re-slices the stale ones
+    T, s0 = 64, slots[0][0]
+    L = len(hist[0][0])
+    q, k, v = bf16(rng, (T, Hq, d)), bf16(rng, (T, Hkv, d)), bf16(rng, (T, Hkv, d))
+    out, fl = backs[0].forward(torch.from_numpy(q.view(np.int16)).cuda(), torch.from_numpy(k.view(np.int16)).cuda(),
+                               torch.from_numpy(v.view(np.int16)).cuda(), [s0], [T])
+    backs[0].check_flags(fl)
+    hist[0] = (np.concatenate([hist[0][0], k]), np.concatenate([hist[0][1], v]))
+    gc, _, o = backs[0]._last["args"]
+    reads = ctypes.c_int32(0)
+    assert hip.load().ea_hip_reads_kv_digits(ctypes.byref(gc), ctypes.byref(o), ctypes.byref(reads)) == 0
+    assert reads.value == 1  # the call read the cache's tiles
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), _oracle_rows(q, *hist[0], L + 1 + np.arange(T), ab))
+    b.append(slots[1][0], k, v)
+    # after a flush both caches hold the tiles of one whole-history slicing
+    c = PagedKVCache(num_pages=64, page_size=P, num_kv_heads=Hkv, head_dim=d, max_seqs=6, max_seq_len=160)
+    for i, s in enumerate(c.add_sequence() for _ in lens0):
+        c.append(s, *hist[i])
+    for x in (a, b, c):
+        x.flush()
+    torch.cuda.synchronize()
+    assert torch.equal(a.digits, b.digits) and torch.equal(a.digits, c.digits)
