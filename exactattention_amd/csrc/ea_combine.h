@@ -130,36 +130,49 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
                 else o16[obase + c] = (uint16_t)bits;
             }
         }
-        for (int c = lane; c < dv && !pre; c += 64) {
-            uint32_t bits = 0;
+        if (!pre) {
+            // more than 8 splits (or a caller's order): both lane channels of 16 splits requested
+            // per round, so a row of 32 splits waits for 2 load latencies, of 64 for 4
+            double N[2] = {0.0, 0.0};
+            float vmaxf[2] = {0.0f, 0.0f};
             if (!flag) {
-                double N = 0.0;
-                float vmaxf = 0.0f;
-                for (int i0 = 0; i0 < ns; i0 += 8) {
-                    double pn8[8];
-                    float pv8[8];
-                    int sh8[8];
+                for (int i0 = 0; i0 < ns; i0 += 16) {
+                    double pn[2][16];
+                    float pv[2][16];
+                    int sh[16];
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
+                    for (int k = 0; k < 16; ++k) {
                         const int i = i0 + k;
                         const int s = __shfl(si, i & 63, 64), n = __shfl(n_i, i & 63, 64);
-                        sh8[k] = __shfl(dsh_i, i & 63, 64);
+                        sh[k] = __shfl(dsh_i, i & 63, 64);
                         const bool use = i < ns && n > 0;
                         const int64_t o = (int64_t)s * P.rows + row;
-                        pn8[k] = use ? P.pN[o * dv + c] : 0.0;
-                        pv8[k] = use ? P.pV[(((int64_t)s * P.nseg + seg) * P.nrb + rbk) * dv + c] : 0.0f;
+#pragma unroll
+                        for (int ci = 0; ci < 2; ++ci) {
+                            const int c = lane + 64 * ci;
+                            const bool in = use && c < dv;
+                            pn[ci][k] = in ? P.pN[o * dv + c] : 0.0;
+                            pv[ci][k] = in ? P.pV[(((int64_t)s * P.nseg + seg) * P.nrb + rbk) * dv + c] : 0.0f;
+                        }
                     }
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        N += ldexp(pn8[k], max(sh8[k], -1000));
-                        vmaxf = fmaxf(vmaxf, pv8[k]);
-                        if (!(pv8[k] <= 3.4028235e38f)) vmaxf = __builtin_inff();
-                    }
+                    for (int k = 0; k < 16; ++k)
+#pragma unroll
+                        for (int ci = 0; ci < 2; ++ci) {
+                            N[ci] += ldexp(pn[ci][k], max(sh[k], -1000));
+                            vmaxf[ci] = fmaxf(vmaxf[ci], pv[ci][k]);
+                            if (!(pv[ci][k] <= 3.4028235e38f)) vmaxf[ci] = __builtin_inff();
+                        }
                 }
-                bits = finish(c, N, vmaxf);
             }
-            if (P.out_fp32) o32[obase + c] = bits;
-            else o16[obase + c] = (uint16_t)bits;
+#pragma unroll
+            for (int ci = 0; ci < 2; ++ci) {
+                const int c = lane + 64 * ci;
+                if (c >= dv) continue;
+                const uint32_t bits = flag ? 0u : finish(c, N[ci], vmaxf[ci]);
+                if (P.out_fp32) o32[obase + c] = bits;
+                else o16[obase + c] = (uint16_t)bits;
+            }
         }
         const int bad = wave_max_i(ok ? 0 : 1);
         if (lane == 0) {
