@@ -1082,10 +1082,11 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
         int64_t items = (int64_t)pl->nseg * pl->nrb;
         ns = 1;
         while (items * ns < 1024 && (int64_t)maxlen / (ns * 2) >= 256) ns *= 2;
-        // and splits of at most 4096 keys: with sequence lengths that differ (only their maximum
+        // and splits of at most 2048 keys: with sequence lengths that differ (only their maximum
         // is known here), long splits leave the blocks of short sequences idle while the longest
-        // block runs (C5, 8K-131K keys: 8 splits 1.36 ms, 32 splits 1.25 ms)
-        while ((int64_t)maxlen / ns > 4096 && ns < 1024) ns *= 2;
+        // block runs, and the last round of blocks is sparse (C5, 8K-131K keys: 8 splits 1.36 ms,
+        // 32 splits 1.19-1.21 ms, 63 splits 1.16-1.19 ms per step)
+        while ((int64_t)maxlen / ns > 2048 && ns < 1024) ns *= 2;
     }
     int sl = (maxlen + ns - 1) / ns;
     sl = (sl + EA_TILE - 1) / EA_TILE * EA_TILE;

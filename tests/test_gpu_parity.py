@@ -295,6 +295,30 @@ def test_d128_rows_match_oracle_and_split_invariance(gpu, out):
         assert np.array_equal(got, want), splits
 
 
+@pytest.mark.parametrize("kernel", ["decode", "general"])
+def test_more_than_64_splits(gpu, kernel):
+    """Split counts past one wave's 64 lanes (the combine takes them in slabs of 64): 71 and 141
+    splits of 64 keys, ragged lengths, bf16 and fp32, with and without a caller's merge order,
+    against the oracle and against 4 splits."""
+    rng = np.random.default_rng(77)
+    B, T, Hq, Hkv, d = 3, 1, 4, 2, 128
+    seq = np.array([9000, 5003, 1])
+    q = bf16(rng, (B, T, Hq, d))
+    k = bf16(rng, (B, Hkv, 9000, d), "outlier")
+    v = bf16(rng, (B, Hkv, 9000, d))
+    prob = problem.contiguous(q, k, v, seq.reshape(B, 1), seq_len=seq)
+    ab = default_alpha_bits(d)
+    for out in ("bf16", "fp32"):
+        want, _ = _oracle(prob, ab, out)
+        ref, flags, _ = _run(prob, ab, out, splits=4, kernel=kernel)
+        assert not np.any(flags) and np.array_equal(ref, want), out
+        for splits, order in ((1000, None), (80, list(range(200))[::-1])):
+            got, flags, st = _run(prob, ab, out, splits=splits, merge_order=order, kernel=kernel)
+            assert st["nsplit"] > 64, st
+            assert not np.any(flags), (out, splits, st)
+            assert np.array_equal(got, want), (out, splits, st["nsplit"])
+
+
 def test_paged_layouts_and_page_sizes_same_bits(gpu):
     rng = np.random.default_rng(12)
     base = _rand_problem(rng, "outlier", "normal", B=3, T=1, Hq=8, Hkv=4, S=333, d=128, dv=128, causal=False)
