@@ -978,6 +978,31 @@ __global__ void __launch_bounds__(256) ea_gather_row(Params P, int64_t row, int6
 }
 
 // ------------------------------------------------------------------------------------------------
+// KV append: new key rows scattered into the paged pools and block-table entries written, in one
+// launch (grid-stride, U = 16-byte chunks when every row is 16-byte aligned, else uint16).
+// Destinations outside the pool or the table are skipped.
+// ------------------------------------------------------------------------------------------------
+template <typename U>
+__global__ void __launch_bounds__(256) ea_kv_append(U* kp, U* vp, int64_t pool_rows, int64_t row_u, const U* kn,
+                                                    const U* vn, const int64_t* dst, int64_t n, int32_t* bt,
+                                                    int64_t bt_entries, const int64_t* bt_pos, const int32_t* bt_val,
+                                                    int64_t nbt) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t x0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t x = x0; x < n * row_u; x += stride) {
+        const int64_t i = x / row_u, c = x - i * row_u;
+        const int64_t d = dst[i];
+        if (d < 0 || d >= pool_rows) continue;
+        kp[d * row_u + c] = kn[x];
+        vp[d * row_u + c] = vn[x];
+    }
+    for (int64_t j = x0; j < nbt; j += stride) {
+        const int64_t pos = bt_pos[j];
+        if (pos >= 0 && pos < bt_entries) bt[pos] = bt_val[j];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Known-answer kernels over the device helpers
 // ------------------------------------------------------------------------------------------------
 __global__ void ea_kat_weight(int64_t n, const uint32_t* t, int32_t* M, int64_t* E, int32_t* st, int32_t* M2,
@@ -1584,6 +1609,30 @@ done:
 #undef EA_TRY
     if (rc) return rc;
     return herr(e);
+}
+
+int ea_hip_kv_append(uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, int64_t row_elems, const uint16_t* k_new,
+                     const uint16_t* v_new, const int64_t* dst_rows, int64_t n, int32_t* block_table,
+                     int64_t block_table_entries, const int64_t* bt_pos, const int32_t* bt_val, int64_t n_bt,
+                     ea_stream_t stream) {
+    if (n < 0 || n_bt < 0 || pool_rows < 0 || row_elems <= 0 || block_table_entries < 0) return -1;
+    if (n > 0 && (!k_pool || !v_pool || !k_new || !v_new || !dst_rows)) return -1;
+    if (n_bt > 0 && (!block_table || !bt_pos || !bt_val)) return -1;
+    if (n == 0 && n_bt == 0) return 0;
+    const hipStream_t st = (hipStream_t)stream;
+    const bool wide = row_elems % 8 == 0 &&
+                      ((uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0;
+    const int64_t row_u = wide ? row_elems / 8 : row_elems;
+    const int64_t work = std::max(n * row_u, n_bt);
+    const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 1024);
+    if (wide)
+        hipLaunchKernelGGL(ea_kv_append<uint4>, dim3(grid), dim3(256), 0, st, (uint4*)k_pool, (uint4*)v_pool,
+                           pool_rows, row_u, (const uint4*)k_new, (const uint4*)v_new, dst_rows, n, block_table,
+                           block_table_entries, bt_pos, bt_val, n_bt);
+    else
+        hipLaunchKernelGGL(ea_kv_append<uint16_t>, dim3(grid), dim3(256), 0, st, k_pool, v_pool, pool_rows, row_u,
+                           k_new, v_new, dst_rows, n, block_table, block_table_entries, bt_pos, bt_val, n_bt);
+    return herr(hipGetLastError());
 }
 
 size_t ea_hip_kv_digits_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t tiles_per_seq) {

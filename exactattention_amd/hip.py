@@ -98,6 +98,9 @@ def load():
         lib.ea_hip_kat_round.restype = ctypes.c_int
         lib.ea_hip_kat_round_ratio.argtypes = [ctypes.c_int64] + [P] * 6 + [ctypes.c_int32, P, P, P]
         lib.ea_hip_kat_round_ratio.restype = ctypes.c_int
+        lib.ea_hip_kv_append.argtypes = [P, P, ctypes.c_int64, ctypes.c_int64, P, P, P, ctypes.c_int64, P,
+                                         ctypes.c_int64, P, P, ctypes.c_int64, P]
+        lib.ea_hip_kv_append.restype = ctypes.c_int
         lib.ea_hip_kv_digits_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
         lib.ea_hip_kv_digits_bytes.restype = ctypes.c_size_t
         lib.ea_hip_kv_digits_update.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), P, P,

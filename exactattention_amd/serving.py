@@ -189,12 +189,14 @@ class PagedKVCache:
         need = np.maximum(0, (L + cnt + self.P - 1) // self.P - have)
         if int(need.sum()) > len(self.free):
             raise RuntimeError("out of pages")
-        grown = []
+        bt_pos, bt_val = [], []  # block-table entries of the new pages
         for i in np.flatnonzero(need):
             s = seqs[i]
             self.pages[s].extend(self.free.pop() for _ in range(int(need[i])))
             self.bt_host[s, :len(self.pages[s])] = self.pages[s]
-            grown.append(s)
+            for p in range(int(have[i]), len(self.pages[s])):
+                bt_pos.append(s * self.max_pages + p)
+                bt_val.append(self.pages[s][p])
         b_of = np.repeat(np.arange(len(seqs)), cnt)
         pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
         idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
@@ -202,18 +204,32 @@ class PagedKVCache:
             self.length[s] = e
             self._mark_stale(s, a)
         arrays = [idx]
-        if grown:
-            arrays += [np.asarray(grown, dtype=np.int64), self.bt_host[grown]]
-        return {"k": k_new, "v": v_new, "grown": bool(grown), "arrays": arrays}
+        if bt_pos:
+            arrays += [np.asarray(bt_pos, dtype=np.int64), np.asarray(bt_val, dtype=np.int32)]
+        return {"k": k_new.contiguous(), "v": v_new.contiguous(), "grown": bool(bt_pos), "arrays": arrays}
 
     def _apply_append(self, plan, dev) -> None:
-        """Device half of an append: block-table rows and the K/V scatter."""
-        idx_d = dev[0]
-        if plan["grown"]:
-            self.block_table.index_copy_(0, dev[1], dev[2])
-        H, d = self.Hkv, self.d
-        self.k.view(-1, H, d).index_copy_(0, idx_d, plan["k"].reshape(-1, H, d))
-        self.v.view(-1, H, d).index_copy_(0, idx_d, plan["v"].reshape(-1, H, d))
+        """Device half of an append: the K/V scatter and the new pages' block-table entries, in
+        one ea_hip_kv_append launch on torch's current stream."""
+        self._kv_append(plan["k"], plan["v"], dev[0], int(dev[0].numel()),
+                        dev[1] if plan["grown"] else None, dev[2] if plan["grown"] else None,
+                        int(dev[1].numel()) if plan["grown"] else 0)
+
+    def _kv_append(self, k_new, v_new, dst, n, bt_pos, bt_val, n_bt, stream=None) -> None:
+        if self.dev.type != "cuda":
+            # a host-resident cache (bookkeeping without a GPU): plain tensor copies
+            H, d = self.Hkv, self.d
+            if n_bt:
+                self.block_table.view(-1).index_copy_(0, bt_pos, bt_val)
+            self.k.view(-1, H, d).index_copy_(0, dst, k_new.reshape(-1, H, d))
+            self.v.view(-1, H, d).index_copy_(0, dst, v_new.reshape(-1, H, d))
+            return
+        rows = self.k.shape[0] * self.P
+        hip._check(hip.load().ea_hip_kv_append(
+            self.k.data_ptr(), self.v.data_ptr(), rows, self.Hkv * self.d, k_new.data_ptr(), v_new.data_ptr(),
+            dst.data_ptr(), n, self.block_table.data_ptr(), self.block_table.numel(),
+            None if bt_pos is None else bt_pos.data_ptr(), None if bt_val is None else bt_val.data_ptr(), n_bt,
+            stream or hip._stream_ptr(self.torch)), "ea_hip_kv_append")
 
     def _mark_stale(self, s: int, key: int) -> None:
         if self.digits is not None:
@@ -572,10 +588,7 @@ class DecodeGraph:
     def _enqueue(self, stream) -> None:
         c, lib, d = self.c, hip.load(), self.dv
         st = ctypes.c_void_p(stream.cuda_stream)
-        c.block_table.view(-1).index_copy_(0, d["bt_pos"], d["bt_val"])
-        H, dd = c.Hkv, c.d
-        c.k.view(-1, H, dd).index_copy_(0, d["idx"], self.k)
-        c.v.view(-1, H, dd).index_copy_(0, d["idx"], self.v)
+        c._kv_append(self.k, self.v, d["idx"], self.B, d["bt_pos"], d["bt_val"], self.B, st)
         hip._check(lib.ea_hip_attention(ctypes.byref(self.gc), ctypes.byref(self.bufs), ctypes.byref(self.o),
                                         self.ws.data_ptr(), self.ws_bytes, st), "ea_hip_attention")
 

@@ -247,6 +247,20 @@ int ea_hip_kat_rn32_prod(int64_t n, const int32_t* am, const int64_t* x_hi, cons
  * tc_v_slices_device (src/exactattn/triton_kernels.py:1255-1280), which the reference reruns on
  * the whole cache at every launch. */
 size_t ea_hip_kv_digits_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t tiles_per_seq);
+
+/* KV append in one launch: rows i < n of k_new / v_new (row_elems uint16 each) written to rows
+ * dst_rows[i] of the K and V pools (pool_rows rows of row_elems: a paged pool [pages, page_size,
+ * Hkv, d] has rows of Hkv*d elements, row = page*page_size + slot), and block_table[bt_pos[j]] =
+ * bt_val[j] for j < n_bt (entries at or past block_table_entries, and rows outside the pool, are
+ * skipped). All pointers are device memory; dst_rows, bt_pos int64, bt_val int32. Enqueue only;
+ * returns 0, -1 on bad arguments, -100 - e on a HIP error. A serving loop's append before its
+ * attention call (with ea_hip_kv_digits_update when the digit cache is kept). Reference
+ * counterpart: none; the reference's demo leaves its cache to transformers' DynamicCache
+ * (scripts/spec_decode_demo.py:116-125). */
+int ea_hip_kv_append(uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, int64_t row_elems, const uint16_t* k_new,
+                     const uint16_t* v_new, const int64_t* dst_rows, int64_t n, int32_t* block_table,
+                     int64_t block_table_entries, const int64_t* bt_pos, const int32_t* bt_val, int64_t n_bt,
+                     ea_stream_t stream);
 int ea_hip_kv_digits_update(const ea_geometry* g, const ea_buffers* b, const int32_t* key_begin,
                             const int32_t* key_end, int32_t max_new_keys, void* kv_digits, int32_t tiles_per_seq,
                             ea_stream_t stream);

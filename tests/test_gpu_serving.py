@@ -323,3 +323,40 @@ def test_decode_graph_equals_forward_and_oracle(gpu):
         x.flush()
     torch.cuda.synchronize()
     assert torch.equal(a.digits, b.digits) and torch.equal(a.digits, c.digits)
+
+
+@pytest.mark.parametrize("row_elems", [1024, 14])
+def test_kv_append_scatter(gpu, row_elems):
+    """ea_hip_kv_append against numpy: rows scattered into both pools (16-byte chunks for a
+    1024-element row, elements for a 14-element one), block-table entries written, destinations
+    outside the pool or the table skipped, nothing else touched."""
+    import ctypes
+
+    import torch
+    from exactattention_amd import hip
+    rng = np.random.default_rng(row_elems)
+    rows, n, entries = 40, 9, 24
+    kp = rng.integers(0, 1 << 16, size=(rows, row_elems), dtype=np.uint16)
+    vp = rng.integers(0, 1 << 16, size=(rows, row_elems), dtype=np.uint16)
+    kn = rng.integers(0, 1 << 16, size=(n, row_elems), dtype=np.uint16)
+    vn = rng.integers(0, 1 << 16, size=(n, row_elems), dtype=np.uint16)
+    dst = rng.permutation(rows)[:n].astype(np.int64)
+    dst[3] = rows + 5  # outside the pool: skipped
+    bt = rng.integers(0, 100, size=entries, dtype=np.int32)
+    pos = np.array([0, 7, 23, 24, -1], dtype=np.int64)  # the last two are outside the table
+    val = np.array([11, 12, 13, 14, 15], dtype=np.int32)
+    dev = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+    kpd, vpd, btd = dev(kp.copy()), dev(vp.copy()), dev(bt.copy())
+    kd, vd, dd, pd, vald = dev(kn), dev(vn), dev(dst), dev(pos), dev(val)
+    rc = hip.load().ea_hip_kv_append(kpd.data_ptr(), vpd.data_ptr(), rows, row_elems, kd.data_ptr(), vd.data_ptr(),
+                                     dd.data_ptr(), n, btd.data_ptr(), entries, pd.data_ptr(), vald.data_ptr(),
+                                     len(pos), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    ok = dst < rows
+    kp[dst[ok]] = kn[ok]
+    vp[dst[ok]] = vn[ok]
+    bt[pos[:3]] = val[:3]
+    assert np.array_equal(kpd.cpu().numpy().view(np.uint16), kp)
+    assert np.array_equal(vpd.cpu().numpy().view(np.uint16), vp)
+    assert np.array_equal(btd.cpu().numpy(), bt)
