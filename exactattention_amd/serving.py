@@ -152,8 +152,8 @@ class PagedKVCache:
 
     # ---- writes
     def append(self, s: int, k_bits, v_bits) -> None:
-        """Append n keys (k_bits, v_bits: (n, Hkv, d) uint16 arrays or int16 device tensors) to slot s,
-        then re-slice the digit tiles they touch."""
+        """Append n keys (k_bits, v_bits: (n, Hkv, d) uint16 arrays or int16 device tensors) to slot s;
+        the digit tiles they touch are marked stale (flush re-slices them)."""
         self.append_batch([s], [len(k_bits)], k_bits, v_bits)
 
     def append_batch(self, seqs, counts, k_bits, v_bits) -> None:
