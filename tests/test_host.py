@@ -103,6 +103,47 @@ def test_attention_validates_before_any_device_work():
     assert rc == -3
 
 
+def _reads_digits(g, kv_digits, **opt):
+    from exactattention_amd import hip
+    o = hip.Options(tier2=1, kv_digits=kv_digits, kv_digits_tiles=(g["max_seq_len"] + 63) // 64, **opt)
+    r = ctypes.c_int32(-7)
+    rc = _lib().ea_hip_reads_kv_digits(ctypes.byref(hip.geometry(g)), ctypes.byref(o), ctypes.byref(r))
+    return rc, r.value
+
+
+def test_reads_kv_digits_follows_the_kernel_choice():
+    """ea_hip_reads_kv_digits (host logic only): 1 exactly when the call takes the int8 prefill path
+    with a digit cache set; C2's decode geometry (2 rows per KV head) reads the bf16 cache."""
+    fake = 4096
+    prefill = _c2_geom(num_tokens=64, q_tok_stride=16 * 128, q_seq_stride=64 * 16 * 128,
+                       o_tok_stride=16 * 128, o_seq_stride=64 * 16 * 128)
+    assert _reads_digits(prefill, fake) == (0, 1)
+    assert _reads_digits(prefill, None) == (0, 0)                     # no cache given
+    assert _reads_digits(prefill, fake, kernel=2) == (0, 0)           # EA_KERNEL_DECODE
+    assert _reads_digits(_c2_geom(), fake) == (0, 0)                  # decode geometry
+    assert _reads_digits(_c2_geom(), fake, kernel=1) == (0, 1)        # EA_KERNEL_PREFILL forces it
+    assert _reads_digits(prefill, fake, splits=-1)[0] == -2           # the plan's own checks
+    assert _reads_digits(_c2_geom(head_dim=100), fake)[0] == -1
+
+
+def test_kv_append_validates_before_any_device_work():
+    """ea_hip_kv_append returns -1 on bad arguments and 0 for an empty append, launching nothing."""
+    lib = _lib()
+    fake = 4096
+    call = lambda **a: lib.ea_hip_kv_append(a.get("kp", fake), a.get("vp", fake), a.get("rows", 10),
+                                            a.get("row", 1024), a.get("kn", fake), a.get("vn", fake),
+                                            a.get("dst", fake), a.get("n", 1), a.get("bt", fake),
+                                            a.get("bte", 8), a.get("pos", fake), a.get("val", fake),
+                                            a.get("nbt", 0), None)
+    assert call(n=0, nbt=0) == 0
+    assert call(n=-1) == -1
+    assert call(row=0) == -1
+    assert call(kp=None) == -1
+    assert call(dst=None) == -1
+    assert call(n=0, nbt=2, bt=None) == -1
+    assert call(n=0, nbt=-1) == -1
+
+
 def test_to_paged_preserves_every_key():
     rng = np.random.default_rng(3)
     q = rng.integers(0, 0x3F80, (2, 1, 4, 16), dtype=np.uint16)
