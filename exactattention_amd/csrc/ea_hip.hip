@@ -1120,7 +1120,7 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->nsplit = (maxlen + sl - 1) / sl;
     if (pl->nsplit < 1) pl->nsplit = 1;
     int64_t R = pl->rows;
-    int dv = g->head_dim_v, d = g->head_dim;
+    int dv = g->head_dim_v;
     size_t off = 0;
     pl->off_q64 = off; off = align_up(off + (size_t)R * EA_MAXD * 8);
     pl->off_qinfo = off; off = align_up(off + (size_t)R * 5 * 4);
