@@ -499,7 +499,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by sequence x KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the path would shard by sequence x KV head, with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch
