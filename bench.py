@@ -239,6 +239,7 @@ def tree_line(steps: int, warmup: int) -> dict:
     q + out bytes; the digit tiles the kernel actually streams are 69,632 B per 64 keys and KV
     head (2.125x the bf16 bytes), reported beside it."""
     import torch
+    from exactattention_amd import hip
     r = run_config("C4", steps, warmup, digits=True)
     prob, st, dp = r["prob"], r["stats"], r["dp"]
     nbytes = algorithmic_bytes(prob)
@@ -253,7 +254,7 @@ def tree_line(steps: int, warmup: int) -> dict:
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(C4_TRAFFIC),
                          "kernel": "ea_pf_main", "kernel_ms": round(main_ms, 5),
                          "basis": "algorithmic bf16 bytes over the kernel's mean HIP-event duration on its stream"},
-            "digit_tile_gbs": round(tiles * 69632 / (main_ms * 1e-3) / 1e9, 1),
+            "digit_tile_gbs": round(tiles * hip.EA_PF_TILE_BYTES / (main_ms * 1e-3) / 1e9, 1),
             "kernels_ms": {"q_slice": round(sl, 5), "ea_pf_main": round(mk, 5), "ea_pf_combine": round(cb, 5),
                            "tier2": round(t2, 5)},
             "key_splits": dp.nsplit, "algorithmic_bytes_per_step": nbytes,

@@ -113,6 +113,7 @@ class PagedKVCache:
         if digits and head_dim == 128:
             lib = hip.load()
             n = lib.ea_hip_kv_digits_bytes(max_seqs, num_kv_heads, self.tiles)
+            self.digit_stride = lib.ea_hip_kv_digits_bytes(1, num_kv_heads, self.tiles)  # bytes per slot
             self.digits = torch.zeros(n, dtype=torch.uint8, device=self.dev)
 
     # ---- sequence slots
@@ -138,7 +139,7 @@ class PagedKVCache:
         self.pages[s], self.length[s], self.live[s], self.stale[s] = [], 0, False, None
 
     def _digit_base(self, s: int) -> int:
-        return self.digits.data_ptr() + s * self.Hkv * self.tiles * hip.EA_PF_TILE_BYTES
+        return self.digits.data_ptr() + s * self.digit_stride
 
     def _geom1(self, s: int, T: int, Hq: int, seq_len: int) -> dict:
         """Serving geometry of one sequence slot (b = 0) over the shared pools."""
