@@ -319,6 +319,36 @@ def test_more_than_64_splits(gpu, kernel):
             assert np.array_equal(got, want), (out, splits, st["nsplit"])
 
 
+@pytest.mark.parametrize("kernel", ["decode", "prefill", "general"])
+def test_batch_equals_separate_launches(gpu, kernel):
+    """One launch over a ragged batch gives each sequence the bits and flags it gets launched
+    alone (batch composition never changes bits; the reference's segments-versus-separate-launches
+    check, tests/test_triton.py:314-361)."""
+    rng = np.random.default_rng(hash(("batch", kernel)) % (1 << 32))
+    B, Hq, Hkv, S, d = 3, 4, 2, 260, 128
+    T = 24 if kernel == "prefill" else 2
+    q = bf16(rng, (B, T, Hq, d), "outlier")
+    k = bf16(rng, (B, Hkv, S, d), "normal")
+    v = bf16(rng, (B, Hkv, S, d), "wide")
+    seq = np.array([260, 97, 181])
+    kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    ab = default_alpha_bits(d)
+    batch = problem.to_paged(problem.contiguous(q, k, v, kv, seq_len=seq), 16, np.random.default_rng(9), "NHD")
+    got, flags, st = _run(batch, ab, kernel=kernel)
+    want, _ = _oracle(batch, ab)
+    assert np.array_equal(got, want) and not np.any(flags), st
+    key = {"decode": "decode_kernel_rows", "prefill": "prefill_kernel_rows"}.get(kernel)
+    if key:
+        assert st[key] == _rows(batch), st
+    rows = T * Hq
+    for b in range(B):
+        one = problem.contiguous(q[b:b + 1], k[b:b + 1, :, :seq[b]], v[b:b + 1, :, :seq[b]], kv[b:b + 1],
+                                 seq_len=seq[b:b + 1])
+        alone, fl1, _ = _run(one, ab, kernel=kernel)
+        assert np.array_equal(got[b], alone[0]), b
+        assert np.array_equal(flags[b * rows:(b + 1) * rows], fl1), b
+
+
 def test_paged_layouts_and_page_sizes_same_bits(gpu):
     rng = np.random.default_rng(12)
     base = _rand_problem(rng, "outlier", "normal", B=3, T=1, Hq=8, Hkv=4, S=333, d=128, dv=128, causal=False)
