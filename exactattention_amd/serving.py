@@ -47,8 +47,9 @@ class _Stager:
         self.nbytes = nbytes
         self.i = 0
 
-    def put(self, *arrays):
-        """Device tensors holding copies of the numpy arrays (same dtypes and shapes)."""
+    def put(self, *arrays, stream=None):
+        """Device tensors holding copies of the numpy arrays (same dtypes and shapes), copied on
+        `stream` (a torch stream; torch's current stream by default)."""
         torch = self.torch
         arrays = [np.ascontiguousarray(a) for a in arrays]
         if not self.cuda:
@@ -70,9 +71,9 @@ class _Stager:
             h[o:o + a.nbytes] = a.view(np.uint8).reshape(-1)
         d = self.devb[i]
         d[:at].copy_(self.host[i][:at], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self.ev[i] = ev
+        if self.ev[i] is None:
+            self.ev[i] = torch.cuda.Event()
+        self.ev[i].record(stream)
         return [d[o:o + a.nbytes].view(_TORCH_DTYPE[a.dtype.str[1:]]).view(a.shape) for a, o in zip(arrays, offs)]
 
 
@@ -126,12 +127,14 @@ class PagedKVCache:
 
     def _check_slots(self, seqs) -> None:
         """Every slot an in-range, live sequence, and each at most once (nothing has changed yet)."""
+        live, n, seen = self.live, self.max_seqs, set()
         for s in seqs:
-            if not isinstance(s, (int, np.integer)) or not 0 <= int(s) < self.max_seqs:
-                raise ValueError(f"sequence slot {s!r} is outside [0, {self.max_seqs})")
-            if not self.live[int(s)]:
+            if not isinstance(s, (int, np.integer)) or not 0 <= s < n:
+                raise ValueError(f"sequence slot {s!r} is outside [0, {n})")
+            if not live[s]:
                 raise ValueError(f"sequence slot {int(s)} holds no live sequence")
-        if len(set(int(s) for s in seqs)) != len(seqs):
+            seen.add(int(s))
+        if len(seen) != len(seqs):
             raise ValueError("a slot may appear once per batch")
 
     def drop_sequence(self, s: int) -> None:
@@ -165,11 +168,11 @@ class PagedKVCache:
         if plan is not None:
             self._apply_append(plan, self.stage.put(*plan["arrays"]))
 
-    def _plan_append(self, seqs, counts, k_bits, v_bits):
+    def _plan_append(self, seqs, counts, k_bits, v_bits, checked: bool = False):
         """Host half of an append: checks, page allocation, block-table mirror and lengths. Returns
         None for an empty append, else a plan whose "arrays" the caller uploads (in one staged copy
         with its own arrays appended) and hands, as device tensors in the same order, to
-        _apply_append."""
+        _apply_append. checked: the caller has run _check_slots on seqs already."""
         torch = self.torch
         k_new = _dev16(torch, k_bits, self.dev)
         v_new = _dev16(torch, v_bits, self.dev)
@@ -178,7 +181,8 @@ class PagedKVCache:
             raise ValueError("one count per sequence slot")
         if k_new.shape[0] != sum(counts) or v_new.shape[0] != sum(counts):
             raise ValueError("k/v must hold sum(counts) keys")
-        self._check_slots(seqs)
+        if not checked:
+            self._check_slots(seqs)
         if sum(counts) == 0:
             return None
         sa = np.asarray(seqs, dtype=np.int64)
@@ -198,23 +202,28 @@ class PagedKVCache:
             for p in range(int(have[i]), len(self.pages[s])):
                 bt_pos.append(s * self.max_pages + p)
                 bt_val.append(self.pages[s][p])
-        b_of = np.repeat(np.arange(len(seqs)), cnt)
-        pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
-        idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
+        if np.all(cnt == 1):  # one key per sequence (a decode step): it lands at position L
+            idx = self.bt_host[sa, L // self.P].astype(np.int64) * self.P + L % self.P
+        else:
+            b_of = np.repeat(np.arange(len(seqs)), cnt)
+            pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
+            idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
+        stale, track = self.stale, self.digits is not None
         for s, a, e in zip(seqs, L.tolist(), (L + cnt).tolist()):
             self.length[s] = e
-            self._mark_stale(s, a)
+            if track:
+                stale[s] = a if stale[s] is None else min(stale[s], a)
         arrays = [idx]
         if bt_pos:
             arrays += [np.asarray(bt_pos, dtype=np.int64), np.asarray(bt_val, dtype=np.int32)]
         return {"k": k_new.contiguous(), "v": v_new.contiguous(), "grown": bool(bt_pos), "arrays": arrays}
 
-    def _apply_append(self, plan, dev) -> None:
+    def _apply_append(self, plan, dev, stream=None) -> None:
         """Device half of an append: the K/V scatter and the new pages' block-table entries, in
-        one ea_hip_kv_append launch on torch's current stream."""
+        one ea_hip_kv_append launch on `stream` (torch's current stream by default)."""
         self._kv_append(plan["k"], plan["v"], dev[0], int(dev[0].numel()),
                         dev[1] if plan["grown"] else None, dev[2] if plan["grown"] else None,
-                        int(dev[1].numel()) if plan["grown"] else 0)
+                        int(dev[1].numel()) if plan["grown"] else 0, stream)
 
     def _kv_append(self, k_new, v_new, dst, n, bt_pos, bt_val, n_bt, stream=None) -> None:
         if self.dev.type != "cuda":
@@ -230,7 +239,7 @@ class PagedKVCache:
             self.k.data_ptr(), self.v.data_ptr(), rows, self.Hkv * self.d, k_new.data_ptr(), v_new.data_ptr(),
             dst.data_ptr(), n, self.block_table.data_ptr(), self.block_table.numel(),
             None if bt_pos is None else bt_pos.data_ptr(), None if bt_val is None else bt_val.data_ptr(), n_bt,
-            stream or hip._stream_ptr(self.torch)), "ea_hip_kv_append")
+            stream if stream is not None else hip._stream_ptr(self.torch)), "ea_hip_kv_append")
 
     def _mark_stale(self, s: int, key: int) -> None:
         if self.digits is not None:
@@ -278,9 +287,10 @@ class PagedKVCache:
         b = hip.Buffers(q=None, k=self.k.data_ptr(), v=self.v.data_ptr(), seq_len=seq_d.data_ptr(), kv_len=None,
                         block_table=self.block_table.data_ptr(), block_table_offset=None, tree_mask=None,
                         tree_base=None, out=None, flags=None)
+        st = stream if stream is not None else hip._stream_ptr(torch)
         hip._check(lib.ea_hip_kv_digits_update(ctypes.byref(gc), ctypes.byref(b), kb_d.data_ptr(), ke_d.data_ptr(), span,
-                                               ctypes.c_void_p(self.digits.data_ptr()), self.tiles,
-                                               stream or hip._stream_ptr(torch)), "ea_hip_kv_digits_update")
+                                               ctypes.c_void_p(self.digits.data_ptr()), self.tiles, st),
+                   "ea_hip_kv_digits_update")
 
 
 class ExactAttentionBackend:
@@ -291,6 +301,7 @@ class ExactAttentionBackend:
         self.alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
         self.ws = None
         self._last = None  # the latest launch: its ea_* arguments and the tensors they point at
+        self._geoms = {}   # ea_geometry per (B, T): only max_seq_len changes between launches
 
     def _launch(self, seqs, qd, kvl, tree_mask=None, tree_base=None, digits_slot=None, staged=None, stream=None):
         """Enqueue one ea_hip_attention call over sequences `seqs` on torch's current stream.
@@ -303,9 +314,12 @@ class ExactAttentionBackend:
         lib = hip.load()
         B, T, Hq, d = qd.shape
         lens = [c.length[s] for s in seqs]
-        g = c._geom1(seqs[0], T, Hq, max(lens))
-        g["num_seqs"] = B
-        gc = hip.geometry(g)
+        gc = self._geoms.get((B, T, Hq))
+        if gc is None:
+            g = c._geom1(seqs[0], T, Hq, 1)
+            g["num_seqs"] = B
+            gc = self._geoms[(B, T, Hq)] = hip.geometry(g)
+        gc.max_seq_len = max(1, max(lens))
         out = torch.empty((B, T, Hq, d), dtype=torch.int32 if self.out == "fp32" else torch.int16, device=c.dev)
         flags = torch.empty(B * T * Hq, dtype=torch.uint8, device=c.dev)
         tm = tb = None
@@ -343,8 +357,9 @@ class ExactAttentionBackend:
                         kv_len=kvl.data_ptr(), block_table=c.block_table.data_ptr(), block_table_offset=off.data_ptr(),
                         tree_mask=None if tm is None else tm.data_ptr(), tree_base=None if tb is None else tb.data_ptr(),
                         out=out.data_ptr(), flags=flags.data_ptr())
+        st = stream if stream is not None else hip._stream_ptr(torch)
         hip._check(lib.ea_hip_attention(ctypes.byref(gc), ctypes.byref(b), ctypes.byref(o), ws.data_ptr(), int(nb.value),
-                                        stream or hip._stream_ptr(torch)), "ea_hip_attention")
+                                        st), "ea_hip_attention")
         self._last = {"args": (gc, b, o), "keep": (qd, kvl, seq, off, tm, tb, staged), "out": out, "flags": flags,
                       "ret": None}
         return out, flags
@@ -395,21 +410,25 @@ class ExactAttentionBackend:
         if query.shape[0] != ntok or key.shape[0] != ntok or value.shape[0] != ntok:
             raise ValueError("query/key/value must hold sum(query_lens) tokens")
         B, T, Hq, d = len(ql), max(ql), query.shape[1], query.shape[2]
-        start = np.concatenate([[0], np.cumsum(ql)])
         prefix = [c.length[s] for s in seqs]
-        plan = c._plan_append(seqs, ql, key, value)
-        b_of = np.repeat(np.arange(B), ql)
-        j_of = np.arange(ntok) - start[b_of]
-        kvl_h = np.zeros(B * T, dtype=np.int32)
-        kvl_h[b_of * T + j_of] = np.asarray(prefix)[b_of] + j_of + 1
-        mine = [kvl_h, np.asarray([c.length[s] for s in seqs], dtype=np.int32),
-                np.asarray([s * c.max_pages for s in seqs], dtype=np.int64), np.asarray(seqs, dtype=np.int32)]
+        plan = c._plan_append(seqs, ql, key, value, checked=True)
+        lens = np.asarray([c.length[s] for s in seqs], dtype=np.int32)
+        if T == 1:
+            kvl_h = lens  # one token per sequence: it sees the whole sequence
+        else:
+            start = np.concatenate([[0], np.cumsum(ql)])
+            b_of = np.repeat(np.arange(B), ql)
+            j_of = np.arange(ntok) - start[b_of]
+            kvl_h = np.zeros(B * T, dtype=np.int32)
+            kvl_h[b_of * T + j_of] = np.asarray(prefix)[b_of] + j_of + 1
+        mine = [kvl_h, lens, np.asarray(seqs, dtype=np.int64) * c.max_pages, np.asarray(seqs, dtype=np.int32)]
         if T > 1:
             mine.append((b_of * T + j_of).astype(np.int64))
         n_app = len(plan["arrays"])
-        dev = c.stage.put(*plan["arrays"], *mine)
-        st = hip._stream_ptr(torch)
-        c._apply_append(plan, dev[:n_app])
+        ts = torch.cuda.current_stream(c.dev)
+        st = ctypes.c_void_p(ts.cuda_stream)
+        dev = c.stage.put(*plan["arrays"], *mine, stream=ts)
+        c._apply_append(plan, dev[:n_app], st)
         kvl, staged = dev[n_app], (dev[n_app + 1], dev[n_app + 2], dev[n_app + 3])
         row = dev[n_app + 4] if T > 1 else None
         q16 = query.view(torch.int16) if query.dtype != torch.int16 else query
