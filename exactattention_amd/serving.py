@@ -185,6 +185,8 @@ class PagedKVCache:
             self._check_slots(seqs)
         if sum(counts) == 0:
             return None
+        if all(n == 1 for n in counts):
+            return self._plan_one_each(seqs, k_new, v_new)
         sa = np.asarray(seqs, dtype=np.int64)
         cnt = np.asarray(counts, dtype=np.int64)
         L = np.asarray(self.length, dtype=np.int64)[sa]
@@ -202,18 +204,45 @@ class PagedKVCache:
             for p in range(int(have[i]), len(self.pages[s])):
                 bt_pos.append(s * self.max_pages + p)
                 bt_val.append(self.pages[s][p])
-        if np.all(cnt == 1):  # one key per sequence (a decode step): it lands at position L
-            idx = self.bt_host[sa, L // self.P].astype(np.int64) * self.P + L % self.P
-        else:
-            b_of = np.repeat(np.arange(len(seqs)), cnt)
-            pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
-            idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
+        b_of = np.repeat(np.arange(len(seqs)), cnt)
+        pos = np.arange(int(cnt.sum())) - np.repeat(np.cumsum(cnt) - cnt - L, cnt)
+        idx = self.bt_host[sa[b_of], pos // self.P].astype(np.int64) * self.P + pos % self.P
         stale, track = self.stale, self.digits is not None
         for s, a, e in zip(seqs, L.tolist(), (L + cnt).tolist()):
             self.length[s] = e
             if track:
                 stale[s] = a if stale[s] is None else min(stale[s], a)
         arrays = [idx]
+        if bt_pos:
+            arrays += [np.asarray(bt_pos, dtype=np.int64), np.asarray(bt_val, dtype=np.int32)]
+        return {"k": k_new.contiguous(), "v": v_new.contiguous(), "grown": bool(bt_pos), "arrays": arrays}
+
+    def _plan_one_each(self, seqs, k_new, v_new):
+        """_plan_append for one key per sequence (a decode step), in plain integer arithmetic: the
+        same page allocation order and the same plan as the general path."""
+        P, length, pages, free = self.P, self.length, self.pages, self.free
+        news = 0
+        for s in seqs:
+            if length[s] + 1 > self.max_seq_len:
+                raise ValueError("sequence longer than the cache's max_seq_len")
+            news += length[s] // P >= len(pages[s])
+        if news > len(free):
+            raise RuntimeError("out of pages")
+        idx, bt_pos, bt_val = [], [], []
+        stale, track = self.stale, self.digits is not None
+        for s in seqs:
+            L, pg = length[s], pages[s]
+            if L // P >= len(pg):  # the key opens a new page
+                page = free.pop()
+                pg.append(page)
+                self.bt_host[s, len(pg) - 1] = page
+                bt_pos.append(s * self.max_pages + len(pg) - 1)
+                bt_val.append(page)
+            idx.append(pg[L // P] * P + L % P)
+            length[s] = L + 1
+            if track:
+                stale[s] = L if stale[s] is None else min(stale[s], L)
+        arrays = [np.asarray(idx, dtype=np.int64)]
         if bt_pos:
             arrays += [np.asarray(bt_pos, dtype=np.int64), np.asarray(bt_val, dtype=np.int32)]
         return {"k": k_new.contiguous(), "v": v_new.contiguous(), "grown": bool(bt_pos), "arrays": arrays}
@@ -413,23 +442,22 @@ class ExactAttentionBackend:
         prefix = [c.length[s] for s in seqs]
         plan = c._plan_append(seqs, ql, key, value, checked=True)
         lens = np.asarray([c.length[s] for s in seqs], dtype=np.int32)
-        if T == 1:
-            kvl_h = lens  # one token per sequence: it sees the whole sequence
-        else:
+        mine = [lens, np.asarray(seqs, dtype=np.int64) * c.max_pages, np.asarray(seqs, dtype=np.int32)]
+        if T > 1:
             start = np.concatenate([[0], np.cumsum(ql)])
             b_of = np.repeat(np.arange(B), ql)
             j_of = np.arange(ntok) - start[b_of]
             kvl_h = np.zeros(B * T, dtype=np.int32)
             kvl_h[b_of * T + j_of] = np.asarray(prefix)[b_of] + j_of + 1
-        mine = [kvl_h, lens, np.asarray(seqs, dtype=np.int64) * c.max_pages, np.asarray(seqs, dtype=np.int32)]
-        if T > 1:
-            mine.append((b_of * T + j_of).astype(np.int64))
+            mine += [kvl_h, (b_of * T + j_of).astype(np.int64)]
         n_app = len(plan["arrays"])
         ts = torch.cuda.current_stream(c.dev)
         st = ctypes.c_void_p(ts.cuda_stream)
         dev = c.stage.put(*plan["arrays"], *mine, stream=ts)
         c._apply_append(plan, dev[:n_app], st)
-        kvl, staged = dev[n_app], (dev[n_app + 1], dev[n_app + 2], dev[n_app + 3])
+        staged = (dev[n_app], dev[n_app + 1], dev[n_app + 2])
+        # one token per sequence sees the whole sequence: its visible length is the sequence's
+        kvl = dev[n_app + 3] if T > 1 else dev[n_app]
         row = dev[n_app + 4] if T > 1 else None
         q16 = query.view(torch.int16) if query.dtype != torch.int16 else query
         if T == 1:
