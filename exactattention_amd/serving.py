@@ -187,6 +187,10 @@ class PagedKVCache:
             return None
         if all(n == 1 for n in counts):
             return self._plan_one_each(seqs, k_new, v_new)
+        return self._plan_general(seqs, counts, k_new, v_new)
+
+    def _plan_general(self, seqs, counts, k_new, v_new):
+        """_plan_append after its checks, for any counts (at least one key in all)."""
         sa = np.asarray(seqs, dtype=np.int64)
         cnt = np.asarray(counts, dtype=np.int64)
         L = np.asarray(self.length, dtype=np.int64)[sa]

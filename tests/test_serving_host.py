@@ -54,6 +54,40 @@ def test_paged_cache_bookkeeping():
     assert len(c.free) == 20 - len(c.pages[a])
 
 
+def test_one_key_appends_plan_like_the_general_path():
+    """Decode appends (one key per sequence) take a plain-integer planner; it must leave the same
+    plan (scatter rows, new block-table entries) and the same pages, block tables, free list,
+    lengths and stale marks as the general planner, including keys that open a new page and slot
+    orders that differ from allocation order."""
+    from exactattention_amd.serving import PagedKVCache
+    rng = np.random.default_rng(8)
+    Hkv, d = 2, 16
+    k0, v0 = bf16(rng, (14, Hkv, d)), bf16(rng, (14, Hkv, d))
+
+    def fresh():
+        c = PagedKVCache(num_pages=40, page_size=4, num_kv_heads=Hkv, head_dim=d, max_seqs=4, max_seq_len=64,
+                         digits=False, device="cpu")
+        seqs = [c.add_sequence() for _ in range(4)]
+        c.append_batch(seqs, [3, 4, 0, 7], k0, v0)
+        c.digits = True  # the planners only test for a digit cache: stale marks are kept
+        c.stale = [None, 2, None, 5]
+        return c
+
+    fast, slow = fresh(), fresh()
+    for step in range(7):
+        seqs = [3, 0, 2, 1] if step % 2 else [1, 2, 3, 0]
+        kd, vd = (fast.torch.from_numpy(bf16(rng, (4, Hkv, d)).view(np.int16)) for _ in range(2))
+        a = fast._plan_one_each(seqs, kd, vd)
+        b = slow._plan_general(seqs, [1, 1, 1, 1], kd, vd)
+        assert a["grown"] == b["grown"] and len(a["arrays"]) == len(b["arrays"]), step
+        for x, y in zip(a["arrays"], b["arrays"]):
+            assert x.dtype == y.dtype and np.array_equal(x, y), step
+        assert fast.pages == slow.pages and fast.free == slow.free, step
+        assert np.array_equal(fast.bt_host, slow.bt_host), step
+        assert fast.length == slow.length and fast.stale == slow.stale, step
+    assert any(len(p) > 2 for p in fast.pages)  # new pages were opened on the way
+
+
 def test_paged_cache_rejects():
     from exactattention_amd.serving import PagedKVCache
     rng = np.random.default_rng(6)
