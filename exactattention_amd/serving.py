@@ -349,6 +349,8 @@ class ExactAttentionBackend:
         lens = [c.length[s] for s in seqs]
         gc = self._geoms.get((B, T, Hq))
         if gc is None:
+            if len(self._geoms) >= 256:
+                self._geoms.clear()  # batch shapes vary without bound in a long run: keep the cache small
             g = c._geom1(seqs[0], T, Hq, 1)
             g["num_seqs"] = B
             gc = self._geoms[(B, T, Hq)] = hip.geometry(g)
