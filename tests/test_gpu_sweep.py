@@ -1,6 +1,7 @@
 """GPU parity sweep: seeded random geometries through the public problem path, against the oracle.
 
-Each case draws its own combination of the factors the other GPU tests vary one or two at a time:
+Each case draws its own combination of the factors the other GPU tests vary one or two at a time
+(every eighth case with long rows of 2,000 to 20,000 keys):
 kernel request (auto, decode, prefill, general: an ineligible request falls back, which is part of
 what is checked), head dims, GQA group, tokens per sequence, ragged sequence lengths, prefix /
 causal / tree masks (tree keys overlapping the prefix and running past seq_len), input kinds, page
@@ -24,8 +25,42 @@ pytestmark = pytest.mark.gpu
 NCASES = int(os.environ.get("EA_SWEEP_CASES", "1024"))
 
 
+def _long_case(i, rng):
+    """Every eighth case: long rows (2,000 to 20,000 keys) for a few rows, so that rows span many
+    tiles and key splits, and prefill rows pass 256 tiles (epoch folds)."""
+    kernel = ["auto", "decode", "prefill", "general"][(i // 8) % 4]
+    Hkv = int(rng.choice([1, 2]))
+    grp = int(rng.choice([1, 2]))
+    T = int(rng.choice([1, 2, 16])) if kernel == "prefill" else int(rng.choice([1, 2]))
+    B = int(rng.integers(1, 3))
+    S = int(rng.integers(2000, 20001))
+    seq = rng.integers(S // 2, S + 1, size=B)
+    mode = str(rng.choice(["causal", "prefix", "full"]))
+    if mode == "causal":
+        kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    elif mode == "prefix":
+        kv = np.stack([rng.integers(0, seq[b] + 1, size=T) for b in range(B)])
+    else:
+        kv = np.repeat(seq[:, None], T, axis=1)
+    kq, kk, kv_kind = (str(x) for x in rng.choice(KINDS, size=3))
+    q = bf16(rng, (B, T, Hkv * grp, 128), kq)
+    k = bf16(rng, (B, Hkv, S, 128), kk)
+    v = bf16(rng, (B, Hkv, S, 128), kv_kind)
+    prob = problem.contiguous(q, k, v, kv, seq_len=seq)
+    ps = int(rng.choice([0, 16, 64]))
+    if ps:
+        prob = problem.to_paged(prob, ps, np.random.default_rng(i), "NHD")
+    out = str(rng.choice(["bf16", "fp32"]))
+    splits = int(rng.choice([0, 0, 3, 7, 16]))
+    desc = (f"case {i} (long rows): kernel={kernel} B={B} T={T} Hq={Hkv * grp} Hkv={Hkv} S={S} seq={seq.tolist()} "
+            f"mode={mode} kinds=({kq},{kk},{kv_kind}) page={ps} out={out} splits={splits}")
+    return prob, kernel, 128, out, splits, desc
+
+
 def _case(i):
     rng = np.random.default_rng(90_000 + i)
+    if i % 8 == 7:
+        return _long_case(i, rng)
     kernel = ["auto", "decode", "prefill", "general"][i % 4]
     full = kernel in ("decode", "prefill") or rng.random() < 0.4
     d = 128 if full else int(rng.choice([8, 16, 40, 64, 96, 120, 128]))
