@@ -132,6 +132,75 @@ def test_forward_mixed_batches_match_oracle(gpu):
     step([0, 1, 2, 3], [2, 80, 1, 1])     # the re-used slot restarts at key 0
 
 
+@pytest.mark.parametrize("seed", [2024, 7, 99])
+def test_random_serving_sessions_match_oracle(gpu, seed):
+    """Random interleavings of the cache and backend operations a serving loop issues: sequences
+    added and dropped (slots re-used), prefill chunks (short ones on the decode kernel, long ones
+    on the int8 prefill kernel through the digit-tile cache) and decode tokens mixed in one
+    forward, in random slot order, and truncations (rejected drafts, the tile holding the new end
+    re-sliced lazily). Every forward's output equals the oracle on each sequence's logical K/V
+    history; lengths and page counts follow the history."""
+    import torch
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    rng = np.random.default_rng(seed)
+    Hq, Hkv, d, P = 4, 2, 128, 16
+    ab = default_alpha_bits(d)
+    cache = PagedKVCache(num_pages=200, page_size=P, num_kv_heads=Hkv, head_dim=d, max_seqs=5, max_seq_len=700)
+    be = ExactAttentionBackend(cache, Hq, ab)
+    dev = torch.device("cuda")
+    empty = np.zeros((0, Hkv, d), np.uint16)
+    hist = {}
+    counts = {"forward": 0, "prefill_rows": 0, "truncate": 0, "drop": 0}
+    for step in range(150):
+        live = sorted(hist)
+        op = rng.choice(["add", "forward", "forward", "forward", "forward", "truncate", "drop"])
+        if op == "add" or not live:
+            if len(hist) < cache.max_seqs:
+                hist[cache.add_sequence()] = (empty, empty)
+            continue
+        if op == "drop" and len(live) > 1:
+            s = int(rng.choice(live))
+            cache.drop_sequence(s)
+            del hist[s]
+            counts["drop"] += 1
+            continue
+        if op == "truncate":
+            s = int(rng.choice(live))
+            n = len(hist[s][0])
+            if n:
+                m = int(rng.integers(0, n))
+                cache.truncate(s, m)
+                hist[s] = (hist[s][0][:m], hist[s][1][:m])
+                counts["truncate"] += 1
+            continue
+        # forward over a random subset of live slots in random order, each a decode token or a chunk
+        seqs = [int(x) for x in rng.permutation(live)[:int(rng.integers(1, len(live) + 1))]]
+        lens = [int(rng.choice([1, 1, 1, 3, 17, 64, 90])) for _ in seqs]
+        lens = [min(n, cache.max_seq_len - len(hist[s][0])) for s, n in zip(seqs, lens)]
+        if min(lens) <= 0:
+            continue
+        n = sum(lens)
+        q, k, v = bf16(rng, (n, Hq, d), "outlier"), bf16(rng, (n, Hkv, d)), bf16(rng, (n, Hkv, d), "wide")
+        t = lambda a: torch.from_numpy(a.view(np.int16)).to(dev)
+        out, fl = be.forward(t(q), t(k), t(v), seqs, lens)
+        be.check_flags(fl)
+        got = out.cpu().numpy().view(np.uint16)
+        assert not fl.any().item(), (step, seqs, lens)
+        at = 0
+        for s, T in zip(seqs, lens):
+            L = len(hist[s][0])
+            hist[s] = (np.concatenate([hist[s][0], k[at:at + T]]), np.concatenate([hist[s][1], v[at:at + T]]))
+            want = _oracle_rows(q[at:at + T], *hist[s], L + 1 + np.arange(T), ab)
+            assert np.array_equal(got[at:at + T], want), (step, seqs, lens, s)
+            at += T
+        counts["forward"] += 1
+        counts["prefill_rows"] += sum(T for T in lens if T >= 64)
+        for s in hist:
+            assert cache.length[s] == len(hist[s][0])
+            assert len(cache.pages[s]) == -(-cache.length[s] // P)
+    assert counts["forward"] >= 50 and counts["truncate"] >= 8 and counts["prefill_rows"] > 0, counts
+
+
 @pytest.mark.parametrize("B,H,Hkv,ql,kl,transposed", [(2, 4, 2, 5, 70, False), (1, 4, 2, 96, 96, True),
                                                     (1, 2, 2, 1, 300, False), (3, 4, 1, 64, 130, True)])
 def test_hf_attention_matches_oracle(gpu, B, H, Hkv, ql, kl, transposed):
