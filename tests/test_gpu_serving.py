@@ -138,8 +138,8 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
     added and dropped (slots re-used), prefill chunks (short ones on the decode kernel, long ones
     on the int8 prefill kernel through the digit-tile cache) and decode tokens mixed in one
     forward, in random slot order, and truncations (rejected drafts, the tile holding the new end
-    re-sliced lazily). Every forward's output equals the oracle on each sequence's logical K/V
-    history; lengths and page counts follow the history."""
+    re-sliced lazily), and draft trees verified then cut to one accepted path. Every output equals
+    the oracle on each sequence's logical K/V history; lengths and page counts follow the history."""
     import torch
     from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
     rng = np.random.default_rng(seed)
@@ -150,10 +150,10 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
     dev = torch.device("cuda")
     empty = np.zeros((0, Hkv, d), np.uint16)
     hist = {}
-    counts = {"forward": 0, "prefill_rows": 0, "truncate": 0, "drop": 0}
+    counts = {"forward": 0, "prefill_rows": 0, "truncate": 0, "drop": 0, "tree": 0}
     for step in range(150):
         live = sorted(hist)
-        op = rng.choice(["add", "forward", "forward", "forward", "forward", "truncate", "drop"])
+        op = rng.choice(["add", "forward", "forward", "forward", "forward", "truncate", "drop", "tree"])
         if op == "add" or not live:
             if len(hist) < cache.max_seqs:
                 hist[cache.add_sequence()] = (empty, empty)
@@ -163,6 +163,25 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
             cache.drop_sequence(s)
             del hist[s]
             counts["drop"] += 1
+            continue
+        if op == "tree":
+            # verify a random draft tree after the prefix, then keep one root-to-node path
+            s = int(rng.choice(live))
+            L, N = len(hist[s][0]), int(rng.integers(2, 40))
+            if L + N > cache.max_seq_len:
+                continue
+            parents = configs.draft_tree(rng, N)
+            q, k, v = bf16(rng, (N, Hq, d)), bf16(rng, (N, Hkv, d)), bf16(rng, (N, Hkv, d), "outlier")
+            got, fl = be.verify_tree(s, q, k, v, parents)
+            assert not np.any(fl), (step, s, N)
+            mask = np.array([sum(1 << a for a in configs.path_of(parents, i)) for i in range(N)], dtype=np.uint64)
+            want = _oracle_rows(q, np.concatenate([hist[s][0], k]), np.concatenate([hist[s][1], v]), np.full(N, L),
+                                ab, tree_mask=mask, tree_base=L)
+            assert np.array_equal(got, want), (step, s, N)
+            path = configs.path_of(parents, int(rng.integers(0, N)))
+            be.accept(s, L, path, k, v)
+            hist[s] = (np.concatenate([hist[s][0], k[path]]), np.concatenate([hist[s][1], v[path]]))
+            counts["tree"] += 1
             continue
         if op == "truncate":
             s = int(rng.choice(live))
@@ -198,7 +217,8 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
         for s in hist:
             assert cache.length[s] == len(hist[s][0])
             assert len(cache.pages[s]) == -(-cache.length[s] // P)
-    assert counts["forward"] >= 50 and counts["truncate"] >= 8 and counts["prefill_rows"] > 0, counts
+    assert counts["forward"] >= 40 and counts["truncate"] >= 8 and counts["tree"] >= 8 and counts["prefill_rows"] > 0, \
+        counts
 
 
 @pytest.mark.parametrize("B,H,Hkv,ql,kl,transposed", [(2, 4, 2, 5, 70, False), (1, 4, 2, 96, 96, True),
