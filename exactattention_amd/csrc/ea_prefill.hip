@@ -103,15 +103,43 @@ __device__ __forceinline__ double wave_max_d(double x) {
 
 
 // ------------------------------------------------------------------------------------------------
-// Digits of 32 consecutive bf16 elements held by one lane; the 4 lanes of a quad (lane & 3) cover
-// a 128-element vector. Returns the vector's lsb (quad-uniform) and fills X[32] and the digit
-// bytes (4 planes x 32 bytes, as 8 dwords per plane).
+// Digits of NE consecutive bf16 elements held by one lane; the G = 128 / NE adjacent lanes of a
+// group (lane & (G - 1)) cover a 128-element vector. Returns the vector's lsb (group-uniform) and
+// the digit bytes (4 planes x NE bytes, as NE / 4 dwords per plane). K/V rows take NE = 32 (a quad
+// per key); q rows NE = 8 (16 lanes per row: four times the lanes, a quarter of the chain).
 // ------------------------------------------------------------------------------------------------
-struct Slice32 {
+template <int NE>
+struct SliceN {
     int lsb, bad, inex, need4, xmax;
     double amax, asum;
-    uint32_t dig[4][8];
+    uint32_t dig[4][NE / 4];
 };
+using Slice32 = SliceN<32>;
+
+template <int G>
+__device__ __forceinline__ int grp_max(int x) {
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) x = max(x, __shfl_xor(x, o, 64));
+    return x;
+}
+template <int G>
+__device__ __forceinline__ int grp_sum(int x) {
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+template <int G>
+__device__ __forceinline__ double grp_maxd(double x) {
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) x = fmax(x, __shfl_xor(x, o, 64));
+    return x;
+}
+template <int G>
+__device__ __forceinline__ double grp_sumd(double x) {
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
 
 __device__ __forceinline__ int quad_max(int x) {
     x = max(x, __shfl_xor(x, 1, 64));
@@ -130,17 +158,19 @@ __device__ __forceinline__ double quad_sumd(double x) {
     return x + __shfl_xor(x, 2, 64);
 }
 
-// src: 32 bf16 values (any alignment of 2 bytes); valid = false gives an all-zero vector.
+// src: NE bf16 values (any alignment of 2 bytes); valid = false gives an all-zero vector.
 // lost[c] (optional) receives 1 for each element that is not exact in 30 bits.
-__device__ __forceinline__ void slice32(const uint16_t* src, bool valid, Slice32& S, int* lost = nullptr) {
-    int m[32], e[32];
+template <int NE>
+__device__ __forceinline__ void slice_n(const uint16_t* src, bool valid, SliceN<NE>& S, int* lost = nullptr) {
+    constexpr int G = 128 / NE;
+    int m[NE], e[NE];
     int bad = 0, lead = INT_MIN;
-    // the 64 bytes as four 16-byte loads when they start on a 16-byte boundary (the usual
-    // cache strides), else element by element
-    uint32_t raw[16];
+    // the 2 NE bytes as 16-byte loads when they start on a 16-byte boundary (the usual cache
+    // strides), else element by element
+    uint32_t raw[NE / 2];
     if (valid && ((uintptr_t)src & 15) == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NE / 8; ++i) {
             const uint4 v = ((const uint4*)src)[i];
             raw[4 * i] = v.x;
             raw[4 * i + 1] = v.y;
@@ -149,23 +179,23 @@ __device__ __forceinline__ void slice32(const uint16_t* src, bool valid, Slice32
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < NE / 2; ++i)
             raw[i] = valid ? ((uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 16)) : 0u;
     }
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
+    for (int k = 0; k < NE; ++k) {
         int bk;
         bf16_dec((raw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, &m[k], &e[k], &bk);
         bad |= bk;
         if (m[k] && !bk) lead = max(lead, lead_of(m[k], e[k]));
     }
-    lead = quad_max(lead);
-    bad = quad_max(bad);
+    lead = grp_max<G>(lead);
+    bad = grp_max<G>(bad);
     const int lsb = (lead == INT_MIN) ? 0 : lead - 29;
     int inex = 0, need4 = 0, xmax = 0;
     double amax = 0.0, asum = 0.0;
 #pragma unroll
-    for (int w4 = 0; w4 < 8; ++w4) {
+    for (int w4 = 0; w4 < NE / 4; ++w4) {
         uint32_t u[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -192,38 +222,38 @@ __device__ __forceinline__ void slice32(const uint16_t* src, bool valid, Slice32
     }
     S.lsb = lsb;
     S.bad = bad;
-    S.inex = quad_sum(inex);
-    S.need4 = quad_max(need4);
-    S.xmax = quad_max(xmax);
-    S.amax = quad_maxd(amax);
-    S.asum = quad_sumd(asum);  // integers below 2^41: exact
+    S.inex = grp_sum<G>(inex);
+    S.need4 = grp_max<G>(need4);
+    S.xmax = grp_max<G>(xmax);
+    S.amax = grp_maxd<G>(amax);
+    S.asum = grp_sumd<G>(asum);  // integers below 2^41: exact in any order
+}
+__device__ __forceinline__ void slice32(const uint16_t* src, bool valid, Slice32& S, int* lost = nullptr) {
+    slice_n<32>(src, valid, S, lost);
 }
 
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------
-// q rows -> digit planes: 64 rows per block, 4 lanes per row (32 dims each). Also clears the
-// tier-2 work-list counter (this is the step's first kernel on the prefill path).
+// q rows -> digit planes: 16 rows per block, 16 lanes per row (8 dims each: a short chain per lane,
+// which is what a step of few rows, such as tree verification, waits on). Also clears the tier-2
+// work-list counter (this is the step's first kernel on the prefill path).
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) ea_pf_qslice(Params P) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *P.wl_cnt = 0;
-    const int q4 = threadIdx.x & 3;
-    const int64_t row = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
-    if (row >= P.rows) return;  // whole quads leave together
+    const int q16 = threadIdx.x & 15;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (row >= P.rows) return;  // whole 16-lane groups leave together
     const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
     const int64_t b = row / ((int64_t)T * Hq);
     const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
     const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
-    Slice32 S;
-    slice32(qr + 32 * q4, true, S);
-    uint8_t* dst = P.pfq + row * 512 + 32 * q4;
+    SliceN<8> S;
+    slice_n<8>(qr + 8 * q16, true, S);
+    uint8_t* dst = P.pfq + row * 512 + 8 * q16;
 #pragma unroll
-    for (int sp = 0; sp < 4; ++sp) {
-        uint4* d4 = (uint4*)(dst + 128 * sp);
-        d4[0] = make_uint4(S.dig[sp][0], S.dig[sp][1], S.dig[sp][2], S.dig[sp][3]);
-        d4[1] = make_uint4(S.dig[sp][4], S.dig[sp][5], S.dig[sp][6], S.dig[sp][7]);
-    }
-    if (q4 == 0) {
+    for (int sp = 0; sp < 4; ++sp) *(uint2*)(dst + 128 * sp) = make_uint2(S.dig[sp][0], S.dig[sp][1]);
+    if (q16 == 0) {
         PfQMeta* qm = (PfQMeta*)P.pfqm + row;
         qm->lsb = S.lsb;
         qm->flags = S.need4 | (S.bad << 1) | (min(S.inex, 255) << 8);
@@ -1289,7 +1319,7 @@ int ea::ea_launch_prefill(const Params& P, hipStream_t st) {
     });
     if (attr_err != hipSuccess) return -100 - (int)attr_err;
     Params Pc = P;
-    hipLaunchKernelGGL(ea_pf_qslice, dim3((unsigned)((P.rows + 63) / 64)), dim3(256), 0, st, Pc);
+    hipLaunchKernelGGL(ea_pf_qslice, dim3((unsigned)((P.rows + 15) / 16)), dim3(256), 0, st, Pc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return -100 - (int)e;
     if (P.nseg > 0 && P.pf_ntiles > 0 && !P.pf_kv_cached) {
