@@ -43,34 +43,41 @@ __global__ void __launch_bounds__(256) ea_prep(Params P) {
     int64_t b = row / ((int64_t)T * Hq);
     int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
     const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
-    int bad = 0;
-    for (int blk = 0; blk < 4; ++blk) {
-        int i = blk * 32 + (lane & 31);
-        int fmax = 0, fmin = 0x1FF;
-        double aq = 0.0;
-        if (lane < 32 && i < d) {
-            uint32_t x = qr[i];
-            double qv = (double)__uint_as_float(x << 16);
+    // the four 32-dim blocks at once: lanes 16 blk .. 16 blk + 15 take dims 32 blk + 2 (lane & 15)
+    // and the next one, and each 16-lane group reduces its block
+    const int blk = lane >> 4;
+    int bad = 0, fmax = 0, fmin = 0x1FF;
+    double aq = 0.0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = blk * 32 + 2 * (lane & 15) + h;
+        if (i < d) {
+            const uint32_t x = qr[i];
+            const double qv = (double)__uint_as_float(x << 16);
             P.q64[row * EA_MAXD + i] = qv;
-            aq = fabs(qv);
-            int f = (x >> 7) & 0xFF;
+            aq += fabs(qv);
+            const int f = (x >> 7) & 0xFF;
             if (f == 0xFF) bad = 1;
             if (x & 0x7FFF) {
-                fmax = f;
-                fmin = max(f, 1);
+                fmax = max(fmax, f);
+                fmin = min(fmin, max(f, 1));
             }
-        } else if (lane < 32 && i < EA_MAXD) {
+        } else {
             P.q64[row * EA_MAXD + i] = 0.0;
         }
-        fmax = wave_max_i(fmax);
-        fmin = wave_min_i(fmin);
-        // sum |q_i| over the block: <= 32 roundings of relative size 2^-53 each, so scaling the
-        // fp64 sum by (1 + 2^-40) gives an upper bound (NaN/inf propagate; the row is flagged)
-        aq = wave_sum(aq);
-        if (lane == 0) {
-            P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
-            P.qn[row * 4 + blk] = aq * (1.0 + 0x1p-40);
-        }
+    }
+    // sum |q_i| over the block: <= 32 roundings of relative size 2^-53 each in any order, so
+    // scaling the fp64 sum by (1 + 2^-40) gives an upper bound (NaN/inf propagate; the row is
+    // flagged)
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        fmax = max(fmax, __shfl_xor(fmax, o, 64));
+        fmin = min(fmin, __shfl_xor(fmin, o, 64));
+        aq += __shfl_xor(aq, o, 64);
+    }
+    if ((lane & 15) == 0) {
+        P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
+        P.qn[row * 4 + blk] = aq * (1.0 + 0x1p-40);
     }
     bad = wave_max_i(bad);
     if (lane == 0) P.qinfo[row * 5 + 4] = bad;
