@@ -48,10 +48,10 @@ def _c2_geom(**over):
     return g
 
 
-def _ws(g, splits=0):
+def _ws(g, splits=0, **opt):
     from exactattention_amd import hip
     lib = _lib()
-    o = hip.Options(splits=splits, tier2=1)
+    o = hip.Options(splits=splits, tier2=1, **opt)
     nb, ns = ctypes.c_size_t(0), ctypes.c_int32(0)
     rc = lib.ea_hip_workspace_size(ctypes.byref(hip.geometry(g)), ctypes.byref(o), ctypes.byref(nb),
                                    ctypes.byref(ns))
@@ -73,7 +73,15 @@ def test_workspace_size_and_split_plan():
     (dict(head_dim=100), -1),                    # not a multiple of 8
     (dict(head_dim_v=127), -1),                  # odd
     (dict(page_size=12), -1),                    # not a power of two
+    (dict(page_size=0), -1),
     (dict(num_tokens=0), -1),
+    (dict(num_seqs=-1), -1),
+    (dict(num_q_heads=0), -1),
+    (dict(num_kv_heads=0), -1),
+    (dict(head_dim=0), -1),
+    (dict(head_dim_v=0), -1),
+    (dict(head_dim_v=130), -1),                  # above 128
+    (dict(max_seq_len=-1), -1),
 ])
 def test_workspace_size_rejects_bad_geometry(bad, code):
     assert _ws(_c2_geom(**bad))[0] == code
@@ -81,6 +89,12 @@ def test_workspace_size_rejects_bad_geometry(bad, code):
 
 def test_negative_splits_is_an_option_error():
     assert _ws(_c2_geom(), splits=-1)[0] == -2
+
+
+@pytest.mark.parametrize("opt", [dict(kernel=-1), dict(kernel=4), dict(prefill_waves=5), dict(prefill_waves=-8)])
+def test_bad_options_are_option_errors(opt):
+    assert _ws(_c2_geom(), **opt)[0] == -2
+    assert _ws(_c2_geom(), **{k: 0 for k in opt})[0] == 0  # the same call with the field at its default
 
 
 def test_attention_validates_before_any_device_work():
