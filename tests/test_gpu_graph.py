@@ -79,3 +79,39 @@ def test_prefill_step_in_a_graph(gpu):
     for o, f in zip(outs, flags):
         assert not f.any()
         assert np.array_equal(o, want)
+
+
+def test_decode_kernel_repeats_back_to_back(gpu):
+    """bench.py times the decode kernel alone, relaunched with the captured step's parameters: the
+    step holds exactly one such node, every repeat runs the decode kernel (its row counter moves by
+    the rows once per launch), and the repeats rewrite the workspace with the same bytes."""
+    import sys
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    rng = np.random.default_rng(5)
+    B, Hkv, Hq, S, d = 4, 2, 4, 700, 128
+    q = bf16(rng, (B, 1, Hq, d), "normal")
+    k = bf16(rng, (B, Hkv, S, d), "normal")
+    v = bf16(rng, (B, Hkv, S, d), "normal")
+    seq = np.array([700, 513, 64, 1])
+    prob = problem.to_paged(problem.contiguous(q, k, v, seq.reshape(B, 1), seq_len=seq), 16, rng, "NHD")
+    ab = default_alpha_bits(d)
+    dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+    launch_hip(dp, ab)
+    torch.cuda.synchronize()
+    out0 = dp.out.cpu().numpy().copy()
+    ws0 = dp.workspace.cpu().numpy().copy()
+    st0 = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    assert st0["decode_kernel_rows"] == B * Hq
+    reps = 3
+    ms = bench.back_to_back_ms(dp, ab, 128, reps)
+    torch.cuda.synchronize()
+    assert ms is not None and ms > 0
+    st1 = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+    # the capture enqueued nothing; reps + 2 decode launches ran
+    assert st1["decode_kernel_rows"] - st0["decode_kernel_rows"] == (reps + 2) * B * Hq
+    assert st1["rows"] == st0["rows"]
+    assert np.array_equal(dp.workspace.cpu().numpy(), ws0)
+    assert np.array_equal(dp.out.cpu().numpy(), out0)
