@@ -832,3 +832,36 @@ def test_prefill_c3_back_to_back(gpu):
     assert st["prefill_kernel_rows"] == steps * _rows(p), st
     assert st["tier1_flagged"] == 0 and st["uncertified_final"] == 0, st
     assert hashlib.sha256(out.tobytes()).hexdigest() == gold, st
+
+
+def _zero_length_problems(kernel):
+    """A batch holding sequences with no keys at all (seq_len 0) beside a 5-key and a multi-tile
+    sequence, contiguous and in NHD / HND pages of 16; T = 64 causal tokens for the prefill kernel,
+    one decode token otherwise."""
+    rng = np.random.default_rng(404)
+    T = 64 if kernel == "prefill" else 1
+    B, Hkv, grp, S, d = 4, 2, 2, 300, 128
+    seq = np.array([0, 5, 300, 0])
+    kv = np.stack([np.clip(seq[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    q = bf16(rng, (B, T, Hkv * grp, d), "normal")
+    k = bf16(rng, (B, Hkv, S, d), "normal")
+    v = bf16(rng, (B, Hkv, S, d), "normal")
+    base = problem.contiguous(q, k, v, kv, seq_len=seq)
+    return [("contiguous", base)] + [(lay, problem.to_paged(base, 16, np.random.default_rng(405), lay))
+                                     for lay in ("NHD", "HND")]
+
+
+@pytest.mark.parametrize("kernel", ["decode", "prefill", "general"])
+def test_sequences_of_length_zero(gpu, kernel):
+    """Rows of a sequence with seq_len 0 see an empty set: +0 with flag 0, as the oracle gives;
+    every other row of the batch stays exact, at the automatic split count and at 3 splits."""
+    ab = default_alpha_bits(128)
+    for name, prob in _zero_length_problems(kernel):
+        want, _ = _oracle(prob, ab)
+        assert not want[[0, 3]].any()
+        for splits in (0, 3):
+            got, flags, st = _run(prob, ab, "bf16", splits, kernel=kernel)
+            assert not flags.any(), (name, splits, st)
+            assert np.array_equal(got, want), (name, splits)
+            if kernel != "general":
+                assert st[f"{kernel}_kernel_rows"] > 0, (name, splits, st)
