@@ -1248,12 +1248,13 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     Plan pl;
     int rc = make_plan(g, o, &pl);
     if (rc) return rc;
+    uint32_t ab = o->alpha_bits;
+    // an empty batch reads and writes nothing: no buffer or workspace is needed for it
+    if (pl.rows == 0) return ((ab >> 23) & 0xFF) == 0xFF ? -3 : 0;
     if (!bf || !bf->q || !bf->k || !bf->v || !bf->seq_len || !bf->kv_len || !bf->out || !bf->flags) return -1;
     if (bf->tree_mask && !bf->tree_base) return -1;
     if (workspace_bytes < pl.total || (!workspace && pl.total)) return -2;
-    uint32_t ab = o->alpha_bits;
     if (((ab >> 23) & 0xFF) == 0xFF) return -3;
-    if (pl.rows == 0) return 0;
     Params P;
     memset(&P, 0, sizeof(P));
     P.g = *g;
@@ -1399,10 +1400,10 @@ int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_optio
     Plan pl;
     int rc = make_plan(g, o, &pl);
     if (rc) return rc;
+    if (pl.rows == 0) return ((o->alpha_bits >> 23) & 0xFF) == 0xFF ? -3 : 0;  // an empty batch
     if (!bf || !bf->q || !bf->k || !bf->v || !bf->seq_len || !bf->kv_len || !bf->out || !bf->flags) return -1;
     if (bf->tree_mask && !bf->tree_base) return -1;
     if (((o->alpha_bits >> 23) & 0xFF) == 0xFF) return -3;
-    if (pl.rows == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e = hipStreamSynchronize(st);
     if (e != hipSuccess) return herr(e);

@@ -148,7 +148,10 @@ int ea_hip_reads_kv_digits(const ea_geometry* g, const ea_options* o, int32_t* r
  * synchronisation, fixed grids: capturable in a hipGraph. The caller owns every buffer; the
  * library retains nothing after the work completes.
  * Replaces launch() of src/exactattn/triton_kernels.py:1324-1519 (split kernel + combine +
- * tier 2), extended with paged KV, GQA segments and tree masks. */
+ * tier 2), extended with paged KV, GQA segments and tree masks. Returns 0; -1 for a bad geometry
+ * or a missing buffer, -2 for bad options or a workspace below ea_hip_workspace_size, -3 for a
+ * non-finite alpha, -100 - e on a HIP error. A batch with no rows (num_seqs 0) enqueues nothing
+ * and returns 0 after the geometry, option and alpha checks, with no buffer or workspace needed. */
 int ea_hip_attention(const ea_geometry* g, const ea_buffers* b, const ea_options* o, void* workspace,
                      size_t workspace_bytes, ea_stream_t stream);
 

@@ -117,6 +117,25 @@ def test_attention_validates_before_any_device_work():
     assert rc == -3
 
 
+def test_empty_batch_needs_no_buffers():
+    """num_seqs 0: nothing to read or write, so no buffer or workspace; the geometry, options and
+    alpha are still checked. The call returns before any device work (no GPU here)."""
+    from exactattention_amd import hip
+    lib = _lib()
+    g0 = dict(_c2_geom(), num_seqs=0)
+    ok = hip.Options(alpha_bits=default_alpha_bits(128), tier2=1)
+    for f in (lib.ea_hip_attention, lambda g, b, o, *rest: lib.ea_hip_exact_rows(g, b, o, None)):
+        assert f(ctypes.byref(hip.geometry(g0)), None, ctypes.byref(ok), None, 0, None) == 0
+        nan = hip.Options(alpha_bits=0x7F800000, tier2=1)
+        assert f(ctypes.byref(hip.geometry(g0)), None, ctypes.byref(nan), None, 0, None) == -3
+        bad = dict(g0, head_dim=0)
+        assert f(ctypes.byref(hip.geometry(bad)), None, ctypes.byref(ok), None, 0, None) == -1
+        assert f(ctypes.byref(hip.geometry(g0)), None, ctypes.byref(hip.Options(alpha_bits=ok.alpha_bits, kernel=9)),
+                 None, 0, None) == -2
+    # with rows, the same null buffers are an error
+    assert lib.ea_hip_attention(ctypes.byref(hip.geometry(_c2_geom())), None, ctypes.byref(ok), None, 0, None) == -1
+
+
 def _reads_digits(g, kv_digits, **opt):
     from exactattention_amd import hip
     o = hip.Options(tier2=1, kv_digits=kv_digits, kv_digits_tiles=(g["max_seq_len"] + 63) // 64, **opt)
