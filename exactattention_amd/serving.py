@@ -444,6 +444,11 @@ class ExactAttentionBackend:
         ntok = sum(ql)
         if query.shape[0] != ntok or key.shape[0] != ntok or value.shape[0] != ntok:
             raise ValueError("query/key/value must hold sum(query_lens) tokens")
+        if not ql:
+            # an empty batch: nothing to append or attend
+            Hq, d = query.shape[1], query.shape[2]
+            return (torch.empty((0, Hq, d), dtype=torch.int32 if self.out == "fp32" else torch.int16, device=c.dev),
+                    torch.empty((0, Hq), dtype=torch.uint8, device=c.dev))
         B, T, Hq, d = len(ql), max(ql), query.shape[1], query.shape[2]
         prefix = [c.length[s] for s in seqs]
         plan = c._plan_append(seqs, ql, key, value, checked=True)

@@ -200,6 +200,23 @@ def test_forward_rejects_bad_batches_without_touching_the_cache():
     assert c.length == [0, 0] and c.pages == [[], []] and len(c.free) == 4
 
 
+def test_forward_of_an_empty_batch_returns_empty_results():
+    """No sequences (a serving loop with nothing scheduled): empty out and flags, the cache as it
+    was, nothing enqueued."""
+    import torch
+    from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
+    c = PagedKVCache(num_pages=4, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
+                     digits=False, device="cpu")
+    be = ExactAttentionBackend(c, 2, 0x3E0293EE)
+    c.add_sequence()
+    z = torch.zeros((0, 2, 8), dtype=torch.int16)
+    out, flags = be.forward(z, z[:, :1], z[:, :1], [], [])
+    assert out.shape == (0, 2, 8) and out.dtype == torch.int16
+    assert flags.shape == (0, 2) and flags.dtype == torch.uint8
+    be.check_flags(flags)
+    assert c.length == [0, 0] and c.pages == [[], []] and len(c.free) == 4
+
+
 def test_check_flags_never_passes_flag_one():
     """A flag-1 row (not certified by the device tiers, output +0) is never handed back as valid:
     check_flags finishes the latest forward's rows with the host exact tier, and for any other
