@@ -61,6 +61,13 @@ def attention_hip(q_bits, k_bits, v_bits, alpha, kv_len=None, row_ptr=None, key_
     k = np.asarray(k_bits, dtype=np.uint16)
     v = np.asarray(v_bits, dtype=np.uint16)
     R, n = q.shape[0], k.shape[0]
+    if R == 0:
+        # no query rows: an empty (0, dv) result, as the reference's attention() returns
+        # (src/exactattn/reference.py:150-161); the library is still required
+        from .hip import load
+        load()
+        empty = np.zeros((0, v.shape[1] if v.ndim == 2 else 0), np.uint32 if out == "fp32" else np.uint16)
+        return _finish(empty, out), np.zeros(0, np.uint8)
     if row_ptr is None:
         # prefix rows: one segment of R tokens over one contiguous cache (shares K/V tiles)
         kv_len = np.full(R, n) if kv_len is None else np.asarray(kv_len, dtype=np.int64).reshape(R)

@@ -13,6 +13,7 @@ import pytest
 
 from exactattention_amd import configs, problem
 from exactattention_amd.formats import default_alpha_bits
+from gen import bf16
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "exactattn_hip.h")
@@ -208,3 +209,21 @@ def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_attention_of_no_query_rows_is_empty():
+    """attention() with zero query rows returns an empty (0, dv) array of the output type, with or
+    without a mask, as the reference's attention() does (src/exactattn/reference.py:150-161);
+    nothing runs on the device, but the library must still be there."""
+    import exactattention_amd as ea
+    _lib()
+    rng = np.random.default_rng(8)
+    k, v = bf16(rng, (5, 16)), bf16(rng, (5, 8))
+    q = np.zeros((0, 16), np.uint16)
+    a = ea.default_alpha(16)
+    r = ea.attention(q, k, v, a)
+    assert r.shape == (0, 8) and r.dtype == np.uint16
+    r = ea.attention(q, k, v, a, out="fp32")
+    assert r.shape == (0, 8) and r.dtype == np.float32
+    r = ea.attention(q, k, v, a, mask=np.zeros((0, 5), bool))
+    assert r.shape == (0, 8) and r.dtype == np.uint16
