@@ -21,8 +21,10 @@ from gen import KINDS, bf16
 
 pytestmark = pytest.mark.gpu
 
-# 1024 cases take about 10 s on an MI355X; EA_SWEEP_CASES=N runs N (20,000 pass in about 130 s)
+# 1024 cases take about 10 s on an MI355X; EA_SWEEP_CASES=N runs N (20,000 pass in about 130 s),
+# starting at case EA_SWEEP_FIRST (default 0), so a longer run can cover indices not run before
 NCASES = int(os.environ.get("EA_SWEEP_CASES", "1024"))
+FIRST = int(os.environ.get("EA_SWEEP_FIRST", "0"))
 
 
 def _long_case(i, rng):
@@ -108,7 +110,7 @@ def test_random_geometries_match_oracle(gpu):
     from exactattention_amd.hip import attention_problem
     from oracle import exact, oracle
     ran = {"decode": 0, "prefill": 0, "general": 0}
-    for i in range(NCASES):
+    for i in range(FIRST, FIRST + NCASES):
         prob, kernel, d, out, splits, desc = _case(i)
         ab = default_alpha_bits(d)
         try:
