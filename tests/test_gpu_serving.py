@@ -2,6 +2,8 @@
 digit-tile cache, batched decode, speculative tree verification, accepted-path compaction): every
 row against the oracle on the logical, contiguous K/V history."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -132,7 +134,13 @@ def test_forward_mixed_batches_match_oracle(gpu):
     step([0, 1, 2, 3], [2, 80, 1, 1])     # the re-used slot restarts at key 0
 
 
-@pytest.mark.parametrize("seed", [2024, 7, 99])
+# EA_SERVING_SEEDS="first:count" adds count further seeds from first on, for a longer run
+_more = os.environ.get("EA_SERVING_SEEDS", "")
+_SEEDS = [2024, 7, 99] + (list(range(int(_more.split(":")[0]), int(_more.split(":")[0]) + int(_more.split(":")[1])))
+                          if _more else [])
+
+
+@pytest.mark.parametrize("seed", _SEEDS)
 def test_random_serving_sessions_match_oracle(gpu, seed):
     """Random interleavings of the cache and backend operations a serving loop issues: sequences
     added and dropped (slots re-used), prefill chunks (short ones on the decode kernel, long ones
@@ -217,8 +225,11 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
         for s in hist:
             assert cache.length[s] == len(hist[s][0])
             assert len(cache.pages[s]) == -(-cache.length[s] // P)
-    assert counts["forward"] >= 40 and counts["truncate"] >= 8 and counts["tree"] >= 8 and counts["prefill_rows"] > 0, \
-        counts
+    # the committed seeds must exercise every operation; further seeds are parity runs only, and a
+    # random session may draw fewer of one kind
+    if seed in (2024, 7, 99):
+        assert counts["forward"] >= 40 and counts["truncate"] >= 8 and counts["tree"] >= 8 \
+            and counts["prefill_rows"] > 0, counts
 
 
 @pytest.mark.parametrize("B,H,Hkv,ql,kl,transposed", [(2, 4, 2, 5, 70, False), (1, 4, 2, 96, 96, True),
