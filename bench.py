@@ -64,7 +64,9 @@ class HipEvents:
         self.ev = (ctypes.c_void_p * n)()
         for i in range(n):
             e = ctypes.c_void_p()
-            assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+            rc = self.h.hipEventCreate(ctypes.byref(e))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreate: {rc}")
             self.ev[i] = e
         self.n = n
 
@@ -72,9 +74,11 @@ class HipEvents:
         return ctypes.cast(ctypes.byref(self.ev, i * ctypes.sizeof(ctypes.c_void_p)), ctypes.c_void_p)
 
     def ms(self, a: int, b: int) -> float:
-        assert self.h.hipEventSynchronize(self.ev[b]) == 0
+        rc = self.h.hipEventSynchronize(self.ev[b])
         t = ctypes.c_float(0)
-        assert self.h.hipEventElapsedTime(ctypes.byref(t), self.ev[a], self.ev[b]) == 0
+        rc = rc or self.h.hipEventElapsedTime(ctypes.byref(t), self.ev[a], self.ev[b])
+        if rc != 0:
+            raise RuntimeError(f"HIP event timing: {rc}")
         return float(t.value)
 
     def close(self):
@@ -246,19 +250,23 @@ def _back_to_back_ms(dp, ab: int, block_x: int, reps: int) -> float | None:
     torch.cuda.synchronize()
     with torch.cuda.stream(s):
         g.capture(s, lambda: launch_hip(dp, ab))
+    def ok(rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what}: {rc}")
+
     try:
         n = ctypes.c_size_t(0)
-        assert h.hipGraphGetNodes(g.graph, None, ctypes.byref(n)) == 0
+        ok(h.hipGraphGetNodes(g.graph, None, ctypes.byref(n)), "hipGraphGetNodes")
         nodes = (ctypes.c_void_p * n.value)()
-        assert h.hipGraphGetNodes(g.graph, nodes, ctypes.byref(n)) == 0
+        ok(h.hipGraphGetNodes(g.graph, nodes, ctypes.byref(n)), "hipGraphGetNodes")
         picked = []
         for i in range(n.value):
             t = ctypes.c_int(-1)
-            assert h.hipGraphNodeGetType(nodes[i], ctypes.byref(t)) == 0
+            ok(h.hipGraphNodeGetType(nodes[i], ctypes.byref(t)), "hipGraphNodeGetType")
             if t.value != 0:
                 continue
             kp = _KernelNodeParams()
-            assert h.hipGraphKernelNodeGetParams(nodes[i], ctypes.byref(kp)) == 0
+            ok(h.hipGraphKernelNodeGetParams(nodes[i], ctypes.byref(kp)), "hipGraphKernelNodeGetParams")
             if kp.blockDim.x == block_x and kp.sharedMemBytes > 0:
                 picked.append(kp)
         if len(picked) != 1:
@@ -269,11 +277,10 @@ def _back_to_back_ms(dp, ab: int, block_x: int, reps: int) -> float | None:
         st = ctypes.c_void_p(s.cuda_stream)
         for i in range(reps + 2):  # two untimed launches first
             if i == 2:
-                assert ev.h.hipEventRecord(ev.ev[0], st) == 0
-            rc = h.hipLaunchKernel(kp.func, kp.gridDim, kp.blockDim, kp.kernelParams, kp.sharedMemBytes, st)
-            if rc != 0:
-                raise RuntimeError(f"hipLaunchKernel: {rc}")
-        assert ev.h.hipEventRecord(ev.ev[1], st) == 0
+                ok(ev.h.hipEventRecord(ev.ev[0], st), "hipEventRecord")
+            ok(h.hipLaunchKernel(kp.func, kp.gridDim, kp.blockDim, kp.kernelParams, kp.sharedMemBytes, st),
+               "hipLaunchKernel")
+        ok(ev.h.hipEventRecord(ev.ev[1], st), "hipEventRecord")
         ms = ev.ms(0, 1) / reps
         s.synchronize()
         ev.close()
@@ -499,7 +506,7 @@ def serving_line(prob: dict, ab: int, steps: int, warmup: int = 3) -> dict:
     extra = 2 * (warmup + steps) + 1
     cache = PagedKVCache(num_pages=B * ((S + extra + P - 1) // P), page_size=P, num_kv_heads=Hkv, head_dim=d,
                          max_seqs=B, max_seq_len=S + extra, device="cuda:0")
-    be = ExactAttentionBackend(cache, Hq, ab)
+    be = ExactAttentionBackend(cache, Hq, alpha_bits=ab)
     seqs = [cache.add_sequence() for _ in range(B)]
     cache.append_batch(seqs, [S - 1] * B, K[:, :S - 1].reshape(-1, Hkv, d), V[:, :S - 1].reshape(-1, Hkv, d))
     dev = torch.device("cuda:0")

@@ -20,9 +20,9 @@ from .formats import (
     ExactAttentionUncertifiedError,
     bf16_bits_to_float32,
     default_alpha,
+    alpha_fp32_bits,
     default_alpha_bits,
     float_to_bf16_bits,
-    fp32_bits,
 )
 
 __all__ = [
@@ -41,22 +41,26 @@ __all__ = [
 ]
 
 
-def _alpha_bits(alpha) -> int:
-    return int(alpha) if isinstance(alpha, (int, np.integer)) and not isinstance(alpha, np.floating) \
-        else fp32_bits(alpha)
+def _alpha_bits(alpha, alpha_bits) -> int:
+    """`alpha` is a value (numpy's float32 conversion, as the reference decodes it); a raw fp32
+    pattern comes only through the keyword `alpha_bits`."""
+    return alpha_fp32_bits(alpha, alpha_bits)
 
 
 def _finish(res: np.ndarray, out: str) -> np.ndarray:
     return res.view(np.float32) if out == "fp32" else res
 
 
-def attention_hip(q_bits, k_bits, v_bits, alpha, kv_len=None, row_ptr=None, key_idx=None, out: str = "bf16",
-                  splits: int = 0, merge_order=None, fallback: bool = True, device: str = "cuda"):
+def attention_hip(q_bits, k_bits, v_bits, alpha=None, kv_len=None, row_ptr=None, key_idx=None, out: str = "bf16",
+                  splits: int = 0, merge_order=None, fallback: bool = True, device: str = "cuda", *,
+                  alpha_bits=None):
     """numpy-level GPU backend (mirrors src/exactattn/triton_kernels.py:1522-1560 and
     src/exactattn/cpu.py:70-109). q (R, d), k (n, d), v (n, dv) bf16 bits. Row r attends keys
     [0, kv_len[r]) (causal, decode, prefill), or key_idx[row_ptr[r]:row_ptr[r+1]] (any mask), or
-    all keys. Returns (out, flags): out uint16 bf16 bits, or float32 for out="fp32"."""
+    all keys. Returns (out, flags): out uint16 bf16 bits, or float32 for out="fp32". `alpha` is
+    the fp32 scale as a value; `alpha_bits=` passes its bit pattern instead."""
     from .hip import attention_problem
+    ab = _alpha_bits(alpha, alpha_bits)
     q = np.asarray(q_bits, dtype=np.uint16)
     k = np.asarray(k_bits, dtype=np.uint16)
     v = np.asarray(v_bits, dtype=np.uint16)
@@ -77,42 +81,45 @@ def attention_hip(q_bits, k_bits, v_bits, alpha, kv_len=None, row_ptr=None, key_
                                   kv_len.reshape(1, R))
     else:
         prob = problem.csr(q, k, v, row_ptr, key_idx)
-    res, flags, _ = attention_problem(prob, _alpha_bits(alpha), out, splits, merge_order, True, fallback, device)
+    res, flags, _ = attention_problem(prob, None, out, splits, merge_order, True, fallback, device, alpha_bits=ab)
     return _finish(res.reshape(R, -1), out), flags
 
 
-def attention_geom(prob: dict, alpha, out: str = "bf16", splits: int = 0, merge_order=None, fallback: bool = True,
-                   device: str = "cuda"):
+def attention_geom(prob: dict, alpha=None, out: str = "bf16", splits: int = 0, merge_order=None,
+                   fallback: bool = True, device: str = "cuda", *, alpha_bits=None):
     """Serving-geometry problem (exactattention_amd.problem) on the GPU -> (out (B,T,Hq,dv), flags, stats)."""
     from .hip import attention_problem
-    res, flags, st = attention_problem(prob, _alpha_bits(alpha), out, splits, merge_order, True, fallback, device)
+    ab = _alpha_bits(alpha, alpha_bits)
+    res, flags, st = attention_problem(prob, None, out, splits, merge_order, True, fallback, device, alpha_bits=ab)
     return _finish(res, out), flags, st
 
 
-def attention(q_bits, k_bits, v_bits, alpha, mask=None, out: str = "bf16") -> np.ndarray:
+def attention(q_bits, k_bits, v_bits, alpha=None, mask=None, out: str = "bf16", *, alpha_bits=None) -> np.ndarray:
     """Batched attention (src/exactattn/reference.py:150-161): q (r, d), k (n, d), v (n, dv),
-    mask (r, n) bool or None. Returns (r, dv) uint16 bf16 bits, or float32 for out="fp32"."""
+    mask (r, n) bool or None. Returns (r, dv) uint16 bf16 bits, or float32 for out="fp32".
+    `alpha` is the fp32 scale as a value; `alpha_bits=` passes its bit pattern instead."""
     q = np.asarray(q_bits, dtype=np.uint16)
     if out not in ("bf16", "fp32"):
         raise ValueError("out must be 'bf16' or 'fp32'")
+    ab = _alpha_bits(alpha, alpha_bits)
     if mask is None:
-        res, _ = attention_hip(q, k_bits, v_bits, alpha, out=out)
+        res, _ = attention_hip(q, k_bits, v_bits, out=out, alpha_bits=ab)
         return res
     mask = np.asarray(mask, dtype=bool)
     counts = mask.sum(axis=1)
     row_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
     key_idx = np.concatenate([np.flatnonzero(m) for m in mask]).astype(np.int64) if mask.size else np.zeros(0, np.int64)
-    res, _ = attention_hip(q, k_bits, v_bits, alpha, row_ptr=row_ptr, key_idx=key_idx, out=out)
+    res, _ = attention_hip(q, k_bits, v_bits, row_ptr=row_ptr, key_idx=key_idx, out=out, alpha_bits=ab)
     return res
 
 
-def attention_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> np.ndarray:
+def attention_row(q_bits, k_bits, v_bits, alpha=None, out: str = "bf16", *, alpha_bits=None) -> np.ndarray:
     """One query row over all given keys (src/exactattn/reference.py:146-147)."""
     q = np.asarray(q_bits, dtype=np.uint16).reshape(1, -1)
     k = np.asarray(k_bits, dtype=np.uint16).reshape(-1, q.shape[1])
     v = np.asarray(v_bits, dtype=np.uint16)
     v = v.reshape(k.shape[0], -1) if v.size else np.zeros((k.shape[0], v.shape[-1] if v.ndim else 0), np.uint16)
-    return attention(q, k, v, alpha, out=out)[0]
+    return attention(q, k, v, alpha, out=out, alpha_bits=alpha_bits)[0]
 
 
 @dataclass
@@ -137,10 +144,16 @@ def _decode(bits: np.ndarray):
     return m, np.where(f != 0, f - 134, -133)
 
 
-def trace_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> RowTrace:
+# The reference's limit on the spread of weight exponents in one row (src/exactattn/reference.py:30)
+MAX_EXPONENT_SPREAD = 1 << 20
+
+
+def trace_row(q_bits, k_bits, v_bits, alpha=None, out: str = "bf16", *, alpha_bits=None) -> RowTrace:
     """One row with every intermediate (src/exactattn/reference.py:82-143). The logits, weights
     and output bits come from the library's host exact tier (ea_exact_row); the exact scores and
-    sums are assembled from them here with Python integers."""
+    sums are assembled from them here with Python integers. Like the reference, a row whose
+    weight exponents spread over more than 2^20 raises ExactAttentionDomainError
+    (src/exactattn/reference.py:109-110), even where the output bits alone are decidable."""
     from .hip import exact_row
     if out not in ("bf16", "fp32"):
         raise ValueError("out must be 'bf16' or 'fp32'")
@@ -151,7 +164,7 @@ def trace_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> RowTrace:
     v = np.asarray(v_bits, dtype=np.uint16)
     dv = v.shape[-1] if v.ndim == 2 else 0
     v = v.reshape(n, dv)
-    res, tb, wm, we = exact_row(q, k, v, _alpha_bits(alpha), out, trace=True)
+    res, tb, wm, we = exact_row(q, k, v, _alpha_bits(alpha, alpha_bits), out, trace=True)
     qm, qe = _decode(q)
     km, ke = _decode(k)
     vm, ve = _decode(v)
@@ -165,7 +178,11 @@ def trace_row(q_bits, k_bits, v_bits, alpha, out: str = "bf16") -> RowTrace:
         e0 = min(e_ for _, e_ in terms)
         s.append((sum(m_ << (e_ - e0) for m_, e_ in terms), e0))
     t = [float(x) for x in np.asarray(tb, dtype=np.uint32).view(np.float32)]
-    w = [(int(a), int(b)) for a, b in zip(wm, we)]
+    # The library saturates weight exponents at +-2^62 (logits of magnitude 2^100 and more); such a
+    # logit is an integer, so its weight is exactly 2^t = 2^23 * 2^(t - 23).
+    w = [(int(a), int(b)) if abs(int(b)) < (1 << 62) else (1 << 23, int(tj) - 23) for a, b, tj in zip(wm, we, t)]
+    if n and max(e_ for _, e_ in w) - min(e_ for _, e_ in w) > MAX_EXPONENT_SPREAD:
+        raise ExactAttentionDomainError("weight exponent spread exceeds reference limit")
     if n == 0:
         return RowTrace(s, t, w, (0, 0), [(0, 0)] * dv, res if out == "bf16" else res.view(np.float32))
     e0 = min(e_ for _, e_ in w)

@@ -12,7 +12,7 @@
 namespace eax {
 
 // Result codes of exact_row.
-enum { EAX_OK = 0, EAX_DOMAIN = 2, EAX_REFUSED = 3 };
+enum { EAX_OK = 0, EAX_DOMAIN = 2, EAX_REFUSED = 3, EAX_NOMEM = 4 };
 
 // Per-key intermediates of a row (optional output of exact_row): t = RN32(alpha s) as fp32 bits,
 // w = RN24(2^t) = wm 2^we (we saturates at +-2^62 for logits beyond that range).
@@ -26,14 +26,15 @@ struct KeyTrace {
 // bits; out: dv bf16 (uint16) or fp32 (uint32) bit patterns, +0 for zero. Returns EAX_OK,
 // EAX_DOMAIN for a NaN/inf input or an fp32 logit overflow (out untouched), or EAX_REFUSED when
 // deciding a rounding would need the exact sums over an exponent spread above 2^20 bits (the
-// reference's own limit, src/exactattn/reference.py:27-30).
+// reference's own limit, src/exactattn/reference.py:27-30), or EAX_NOMEM when the host heap is
+// exhausted (no exception leaves this function).
 int exact_row(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, int64_t n, int dv, uint32_t alpha_bits,
-              int fp32, void* out, const KeyTrace* tr);
+              int fp32, void* out, const KeyTrace* tr) noexcept;
 
 // RN-even of (a / b) * 2^E with a, b given as 128-bit (hi, lo) words, b > 0, into fp32 (p = 24)
 // or bf16 (p = 8) with gradual underflow. Returns the result's bit pattern (negated when neg) and
 // sets *overflow when it exceeds the format's largest finite value (bits are then 0).
 uint32_t round_ratio_bits(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo, int64_t E, int neg, int fp32,
-                          int* overflow);
+                          int* overflow) noexcept;
 
 }  // namespace eax

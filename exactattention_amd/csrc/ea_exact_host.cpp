@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "ea_exact.h"
@@ -180,6 +181,16 @@ Rounded round_ratio(const Big& a, const Big& b, int64_t E, int p, int qmin) {
     Rounded r{0, qmin};
     if (a.zero()) return r;
     const int64_t L = bitlen(a) - bitlen(b);
+    // 2^(L - 1) < a / b < 2^(L + 1). Below half the smallest quantum the value rounds to zero;
+    // far above every format's range it overflows. Both are decided here, before any shift by
+    // E, so that no operand ever grows with |E| (E can be of order 2^40 for a row whose weights
+    // lie that far apart).
+    if (L + 1 + E <= (int64_t)qmin - 1) return r;
+    if (L - 1 + E > 4096) {
+        r.Q = 1u << (p - 1);
+        r.qe = L - 1 + E - (p - 1);
+        return r;
+    }
     const bool ge = L >= 0 ? cmp(a, shl(b, L)) >= 0 : cmp(shl(a, -L), b) >= 0;
     const int64_t lead = ge ? L : L - 1;  // 2^lead <= a / b < 2^(lead + 1)
     int64_t qe = lead + E - (p - 1);
@@ -460,10 +471,13 @@ SBig add_u64(const SBig& a, uint64_t x) {
 
 // bits of RN(num / den * 2^E) for a signed numerator and den > 0
 uint32_t round_signed(const SBig& num, const Big& den, i128 E, int fp32) {
-    // |num / den| < 2^(bitlen(num) + 1 - bitlen(den)): far below the smallest subnormal it rounds
-    // to zero (+0); numerators never sit far above their denominators (E <= 160)
-    if (num.m.zero() || E < -((i128)1 << 40)) return 0;
-    const Rounded r = round_ratio(num.m, den, (int64_t)E, fp32 ? 24 : 8, fp32 ? -149 : -133);
+    // |num / den| 2^E < 2^(bitlen(num) + 1 - bitlen(den) + E): below half the smallest subnormal
+    // it rounds to +0 (round_ratio makes the same test; this one also keeps E within int64).
+    // Numerators never sit far above their denominators (E <= 160).
+    if (num.m.zero()) return 0;
+    const int qmin = fp32 ? -149 : -133;
+    if ((i128)bitlen(num.m) + 1 - bitlen(den) + E <= qmin - 1) return 0;
+    const Rounded r = round_ratio(num.m, den, (int64_t)E, fp32 ? 24 : 8, qmin);
     return encode(r, num.neg, fp32);
 }
 
@@ -471,8 +485,10 @@ const i128 SPREAD_LIMIT = (i128)1 << 20;
 
 }  // namespace
 
-int exact_row(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, int64_t n, int dv, uint32_t alpha_bits,
-              int fp32, void* out, const KeyTrace* tr) {
+namespace {
+
+int exact_row_body(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, int64_t n, int dv,
+                   uint32_t alpha_bits, int fp32, void* out, const KeyTrace* tr) {
     std::vector<int> qm(d), qe(d);
     for (int i = 0; i < d; ++i)
         if (!dec_bf16(q[i], &qm[i], &qe[i])) return EAX_DOMAIN;
@@ -658,17 +674,35 @@ int exact_row(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, in
     return EAX_OK;
 }
 
+}  // namespace
+
+int exact_row(const uint16_t* q, int d, const uint16_t* K, const uint16_t* V, int64_t n, int dv, uint32_t alpha_bits,
+              int fp32, void* out, const KeyTrace* tr) noexcept {
+    try {
+        return exact_row_body(q, d, K, V, n, dv, alpha_bits, fp32, out, tr);
+    } catch (const std::bad_alloc&) {
+        return EAX_NOMEM;
+    } catch (...) {
+        return EAX_NOMEM;
+    }
+}
+
 uint32_t round_ratio_bits(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo, int64_t E, int neg, int fp32,
-                          int* overflow) {
-    const Big a = big_u128(((u128)a_hi << 64) | a_lo), b = big_u128(((u128)b_hi << 64) | b_lo);
+                          int* overflow) noexcept {
     *overflow = 0;
-    if (b.zero() || a.zero()) return 0;
-    const Rounded r = round_ratio(a, b, E, fp32 ? 24 : 8, fp32 ? -149 : -133);
-    if (overflows(r, fp32)) {
+    try {
+        const Big a = big_u128(((u128)a_hi << 64) | a_lo), b = big_u128(((u128)b_hi << 64) | b_lo);
+        if (b.zero() || a.zero()) return 0;
+        const Rounded r = round_ratio(a, b, E, fp32 ? 24 : 8, fp32 ? -149 : -133);
+        if (overflows(r, fp32)) {
+            *overflow = 1;
+            return 0;
+        }
+        return encode(r, neg != 0, fp32);
+    } catch (...) {  // operands are at most 128 bits plus p: only an exhausted heap gets here
         *overflow = 1;
         return 0;
     }
-    return encode(r, neg != 0, fp32);
 }
 
 }  // namespace eax

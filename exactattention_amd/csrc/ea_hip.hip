@@ -1396,7 +1396,7 @@ int ea_hip_attention_noalloc(const ea_geometry* g, const ea_buffers* bf, const e
     return ea_hip_attention(g, bf, o, ws, (size_t)EA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
-int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, ea_stream_t stream) {
+static int exact_rows_impl(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, ea_stream_t stream) {
     Plan pl;
     int rc = make_plan(g, o, &pl);
     if (rc) return rc;
@@ -1456,6 +1456,10 @@ int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_optio
         uint8_t res[EA_MAXDV * 4];  // dv bf16 (uint16) or fp32 (uint32) patterns, as exact_row writes them
         const int x = eax::exact_row(host.data(), d, host.data() + d, host.data() + d + n * d, n, dv, o->alpha_bits,
                                      o->out_fp32, res, nullptr);
+        if (x == eax::EAX_NOMEM) {
+            (void)hipFree(stage);
+            return EA_ERR_HOST_MEMORY;
+        }
         uint8_t flag = x == eax::EAX_OK ? 0 : 2;
         if (x != eax::EAX_OK) memset(res, 0, sizeof(res));
         fixed += x == eax::EAX_OK;
@@ -1479,12 +1483,21 @@ int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_optio
     return 0;
 }
 
+int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* bf, const ea_options* o, ea_stream_t stream) {
+    try {
+        return exact_rows_impl(g, bf, o, stream);
+    } catch (...) {  // host vectors: only an exhausted heap throws
+        return EA_ERR_HOST_MEMORY;
+    }
+}
+
 int ea_exact_row(const uint16_t* q, int d, const uint16_t* k, const uint16_t* v, int64_t n, int dv,
                  uint32_t alpha_bits, int fp32_out, void* out, uint32_t* t_bits, int32_t* w_m, int64_t* w_e) {
     if (!q || !out || d <= 0 || dv <= 0 || n < 0 || (n > 0 && (!k || !v))) return -1;
     eax::KeyTrace tr{t_bits, w_m, w_e};
-    return eax::exact_row(q, d, k, v, n, dv, alpha_bits, fp32_out ? 1 : 0, out,
-                          (t_bits || w_m || w_e) ? &tr : nullptr);
+    const int x = eax::exact_row(q, d, k, v, n, dv, alpha_bits, fp32_out ? 1 : 0, out,
+                                 (t_bits || w_m || w_e) ? &tr : nullptr);
+    return x == eax::EAX_NOMEM ? EA_ERR_HOST_MEMORY : x;
 }
 
 float ea_round_ratio(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo, int E, int neg, int fp32,
@@ -1498,10 +1511,10 @@ float ea_round_ratio(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo,
     return r;
 }
 
-int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
-                     int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
-                     int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
-                     uint8_t* flags, int64_t* stats) {
+static int attention_csr_impl(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v,
+                              int64_t nkeys, int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx,
+                              int fp32_out, int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads,
+                              void* out, uint8_t* flags, int64_t* stats) {
     (void)order_seed; (void)nthreads;
     // the reference's argument checks, in its order (csrc/exact_attention_cpu.cpp:589-592)
     if (d <= 0 || d > EA_MAXD || dv <= 0 || dv > EA_MAXDV || tile <= 0 || splits <= 0) return -1;
@@ -1607,6 +1620,10 @@ int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, 
             char* dst_row = (char*)out + (size_t)r * dv * osz;
             const int x = eax::exact_row(q + r * d, d, kr.data(), vr.data(), n, dv, alpha_bits, fp32_out ? 1 : 0,
                                          dst_row, nullptr);
+            if (x == eax::EAX_NOMEM) {
+                rc = EA_ERR_HOST_MEMORY;
+                goto done;
+            }
             if (x != eax::EAX_OK) memset(dst_row, 0, (size_t)dv * osz);
             flags[r] = x == eax::EAX_OK ? 0 : 2;
         }
@@ -1617,6 +1634,18 @@ done:
 #undef EA_TRY
     if (rc) return rc;
     return herr(e);
+}
+
+int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
+                     int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
+                     int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
+                     uint8_t* flags, int64_t* stats) {
+    try {
+        return attention_csr_impl(q, rows, d, k, v, nkeys, dv, alpha, row_ptr, key_idx, fp32_out, acc_bits, tile,
+                                  splits, order_seed, nthreads, out, flags, stats);
+    } catch (...) {  // host vectors: only an exhausted heap throws (device memory is freed by then)
+        return EA_ERR_HOST_MEMORY;
+    }
 }
 
 int ea_hip_kv_append(uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, int64_t row_elems, const uint16_t* k_new,

@@ -42,6 +42,31 @@ def fp32_bits(x) -> int:
     return int(np.asarray(x, dtype=np.float32).view(np.uint32))
 
 
+def alpha_fp32_bits(alpha=None, alpha_bits=None) -> int:
+    """The fp32 bit pattern of a logit scale. `alpha` is a value of any type numpy converts to
+    float32 (an int 1 or True is 1.0, as src/exactattn/formats.py:120-130 decodes it); a raw
+    pattern is taken only through `alpha_bits`. NaN or infinity raises
+    ExactAttentionDomainError, as the reference's decode_fp32 does."""
+    if alpha_bits is not None:
+        if alpha is not None:
+            raise ValueError("give alpha or alpha_bits, not both")
+        if isinstance(alpha_bits, (bool, np.bool_)) or not isinstance(alpha_bits, (int, np.integer)):
+            raise TypeError("alpha_bits must be an integer fp32 bit pattern")
+        bits = int(alpha_bits)
+        if not 0 <= bits < 1 << 32:
+            raise ValueError("alpha_bits must lie in [0, 2^32)")
+    elif alpha is None:
+        raise TypeError("alpha is required")
+    else:
+        a = np.asarray(alpha, dtype=np.float32)
+        if a.size != 1:
+            raise ValueError("alpha must be a scalar")
+        bits = int(a.reshape(()).view(np.uint32))
+    if (bits >> 23) & 0xFF == 0xFF:
+        raise ExactAttentionDomainError("fp32 NaN or infinity in input")
+    return bits
+
+
 def _ln2_interval(W: int) -> tuple[int, int]:
     # ln 2 = 2 atanh(1/3) = sum_k 2 / ((2k+1) 3^(2k+1)), both ends enclosed at scale 2^W
     lo = hi = 0

@@ -15,7 +15,7 @@ import os
 
 import numpy as np
 
-from .formats import ExactAttentionDomainError, ExactAttentionUncertifiedError, fp32_bits
+from .formats import ExactAttentionDomainError, ExactAttentionUncertifiedError, alpha_fp32_bits
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libexactattn_hip.so")
@@ -255,16 +255,17 @@ def merge_order_tensor(order, nsplit: int, device="cuda"):
     return torch.tensor(full, dtype=torch.int32, device=device)
 
 
-def attention_problem(prob: dict, alpha, out: str = "bf16", splits: int = 0, merge_order=None, tier2: bool = True,
-                      fallback: bool = True, device: str = "cuda", kernel: str = "auto", force_tier2: bool = False,
-                      prefill_waves: int = 0):
+def attention_problem(prob: dict, alpha=None, out: str = "bf16", splits: int = 0, merge_order=None,
+                      tier2: bool = True, fallback: bool = True, device: str = "cuda", kernel: str = "auto",
+                      force_tier2: bool = False, prefill_waves: int = 0, *, alpha_bits=None):
     """Run a problem on the GPU. Returns (out bits shaped (B, T, Hq, dv): uint16 for bf16, uint32
     for fp32; flags (rows,) uint8; stats dict). fallback=False returns the device tiers' flags as
     they are. With fallback=True rows the device tiers leave at flag 1 are recomputed by the host
     exact tier (ea_hip_exact_rows, counted in stats["host_exact_rows"]), and flag 2 raises
-    ExactAttentionDomainError, as the reference's backends do (src/exactattn/cpu.py:103-108)."""
+    ExactAttentionDomainError, as the reference's backends do (src/exactattn/cpu.py:103-108).
+    `alpha` is the fp32 scale as a value; `alpha_bits=` passes its bit pattern instead."""
     import torch
-    alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
+    alpha_bits = alpha_fp32_bits(alpha, alpha_bits)
     dp = DeviceProblem(prob, out, splits, device, kernel, prefill_waves)
     mo = merge_order_tensor(merge_order, dp.nsplit, device) if merge_order is not None else None
     launch_hip(dp, int(alpha_bits), mo, tier2, force_tier2=force_tier2)

@@ -101,7 +101,8 @@ def csr(q, k, v, row_ptr, key_idx):
 def to_paged(prob: dict, page_size: int, rng: np.random.Generator, layout: str = "NHD", extra_pages: int = 3) -> dict:
     """The same problem (same keys per sequence) stored in a shuffled page pool."""
     g = prob["geom"]
-    assert prob["block_table"] is None
+    if prob["block_table"] is not None:
+        raise ValueError("to_paged takes a contiguous problem")
     B, Hkv, d, dv = g["num_seqs"], g["num_kv_heads"], g["head_dim"], g["head_dim_v"]
     S = prob["k"].shape[2]
     k, v = prob["k"], prob["v"]

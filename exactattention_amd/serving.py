@@ -27,7 +27,7 @@ import ctypes
 import numpy as np
 
 from . import hip
-from .formats import ExactAttentionDomainError, ExactAttentionUncertifiedError, alpha_bits_for, fp32_bits
+from .formats import ExactAttentionDomainError, ExactAttentionUncertifiedError, alpha_bits_for, alpha_fp32_bits
 
 TILE = 64  # keys per digit tile
 
@@ -327,11 +327,12 @@ class PagedKVCache:
 
 
 class ExactAttentionBackend:
-    """Certified attention over a PagedKVCache. `alpha` is the base-2 logit scale (fp32)."""
+    """Certified attention over a PagedKVCache. `alpha` is the base-2 logit scale as an fp32
+    value; `alpha_bits=` passes its bit pattern instead."""
 
-    def __init__(self, cache: PagedKVCache, num_q_heads: int, alpha, out: str = "bf16"):
+    def __init__(self, cache: PagedKVCache, num_q_heads: int, alpha=None, out: str = "bf16", *, alpha_bits=None):
         self.cache, self.Hq, self.out = cache, num_q_heads, out
-        self.alpha_bits = alpha if isinstance(alpha, (int, np.integer)) else fp32_bits(alpha)
+        self.alpha_bits = alpha_fp32_bits(alpha, alpha_bits)
         self.ws = None
         self._last = None  # the latest launch: its ea_* arguments and the tensors they point at
         self._geoms = {}   # ea_geometry per (B, T): only max_seq_len changes between launches

@@ -7,7 +7,8 @@
  *
  * Return codes: 0 = success; -1 invalid shape/geometry, -2 invalid option, -3 non-finite alpha
  * (the same convention as the reference's ea_attention_cpu, csrc/exact_attention_cpu.cpp:589-592);
- * -100 - e for a HIP runtime error e. Nothing throws across this ABI.
+ * -5 when the host heap is exhausted (host exact tier and drop-in only); -100 - e for a HIP
+ * runtime error e. Nothing throws across this ABI: every entry point catches on its side.
  *
  * Per-row flags (uint8), the reference's meaning (csrc/exact_attention_cpu.cpp:580-584):
  *   0 = certified (bits equal the definition)
@@ -23,6 +24,9 @@
 
 #include <stddef.h>
 #include <stdint.h>
+
+/* Return code of the host-side entry points when the host heap is exhausted. */
+#define EA_ERR_HOST_MEMORY (-5)
 
 #ifdef __cplusplus
 extern "C" {
@@ -172,7 +176,7 @@ int ea_hip_attention_noalloc(const ea_geometry* g, const ea_buffers* b, const ea
  * exactly on the host (its q, K and V rows gathered on the device into a staging buffer this call
  * allocates and frees), writing the row's bits and flag 0 (flag 2 on a domain error or a refusal,
  * see the flags above). Adds the rows to stats[13] / stats[14] when o->stats is set. Returns 0,
- * -1 on bad arguments, -100 - e on a HIP error. Not capturable (it waits for the device).
+ * -1 on bad arguments, -5 when the host heap is exhausted, -100 - e on a HIP error. Not capturable (it waits for the device).
  * Reference counterpart: the host recompute of flagged rows, src/exactattn/triton_kernels.py:
  * 1553-1559 and src/exactattn/cpu.py:105-108 (reference.attention_row). */
 int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* b, const ea_options* o, ea_stream_t stream);
@@ -181,7 +185,8 @@ int ea_hip_exact_rows(const ea_geometry* g, const ea_buffers* b, const ea_option
  * fp32 bits -> out (dv bf16 or fp32 bits). t_bits, w_m, w_e (optional, n entries each) receive
  * the per-key logits t = RN32(alpha s) and weights w = RN24(2^t) = w_m 2^w_e. Returns 0, 2 for a
  * domain error (NaN/inf input, fp32 logit overflow), 3 when the row needs exact sums over an
- * exponent spread above 2^20 bits, -1 on bad arguments. Runs on the CPU only (no device call).
+ * exponent spread above 2^20 bits, -1 on bad arguments, -5 when the host heap is exhausted.
+ * Runs on the CPU only (no device call).
  * Reference counterpart: reference.trace_row / attention_row (src/exactattn/reference.py:82-147). */
 int ea_exact_row(const uint16_t* q, int d, const uint16_t* k, const uint16_t* v, int64_t n, int dv,
                  uint32_t alpha_bits, int fp32_out, void* out, uint32_t* t_bits, int32_t* w_m, int64_t* w_e);
@@ -190,7 +195,8 @@ int ea_exact_row(const uint16_t* q, int d, const uint16_t* k, const uint16_t* v,
  * list, types and return codes as ea_attention_cpu, host pointers; computes on the current HIP
  * device and returns when done. rc -1 for d or dv outside [1, 128] (this build's head sizes;
  * d a multiple of 8, dv even), tile <= 0 or splits <= 0; -2 for acc_bits other than 64 and 128;
- * -3 for a non-finite alpha; -100 - e for a HIP error. `tile`, `acc_bits`, `order_seed` and
+ * -3 for a non-finite alpha; -5 when the host heap is exhausted; -100 - e for a HIP error.
+ * `tile`, `acc_bits`, `order_seed` and
  * `nthreads` are validated and otherwise ignored (they cannot change certified bits); `splits` is
  * the KV split count. stats[0..2] += tier-1 score, weight and final-rounding fallbacks, as in the
  * reference. Rows the device tiers leave uncertified are recomputed exactly by the host exact

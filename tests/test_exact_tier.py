@@ -256,3 +256,76 @@ def test_drop_in_validates_like_the_reference():
     assert call(key_idx=np.array([0, 1, 2, 4], np.int64)) == -1
     assert call(key_idx=np.array([0, -1, 2, 3], np.int64)) == -1
     assert not st.any()
+
+
+@pytest.mark.parametrize("gap_log2", [33, 38, 39])
+@pytest.mark.parametrize("out", ["bf16", "fp32"])
+def test_exact_row_weights_2_to_the_2_to_the_gap_apart(gap_log2, out):
+    """q = e_0, key 0 with k_0 = 2^gap, key 1 with k = 0, alpha = 1: the weights are 2^(2^gap)
+    and 1. N_c / Z is v_0c within a relative 2^-(2^gap), so it rounds to v_0c, and channels where
+    v_0c = 0 hold v_1c 2^-(2^gap), which rounds to +0. The tier decides both without building
+    operands of 2^gap bits (it once asked for them and aborted with bad_alloc). trace_row refuses
+    the row, as the reference does for any spread past 2^20."""
+    hip = _hip()
+    import exactattention_amd as ea
+    rng = np.random.default_rng(gap_log2)
+    d, dv = 16, 8
+    q = np.zeros(d, np.uint16)
+    q[0] = 0x3F80                                    # 1.0
+    k = np.zeros((2, d), np.uint16)
+    k[0, 0] = (127 + gap_log2) << 7                  # 2^gap
+    v = bf16(rng, (2, dv))
+    v[v == 0] = 0x3F80
+    v[v == 0x8000] = 0x3F80
+    v[0, 3] = 0                                      # a channel the heavy key does not reach
+    v[0, 5] = 0x8000                                 # -0 from the heavy key: the result is +0
+    got = hip.exact_row(q, k, v, 0x3F800000, out)
+    want = v[0].astype(np.uint32) << 16 if out == "fp32" else v[0].copy()
+    want[3] = want[5] = 0
+    assert np.array_equal(got, want)
+    with pytest.raises(ExactAttentionDomainError):
+        ea.trace_row(q, k, v, 1.0, out)
+
+
+def test_round_ratio_far_outside_the_range():
+    """ea_round_ratio with exponents far below and above every format: +0 and an overflow flag,
+    decided without shifting operands by E."""
+    hip = _hip()
+    lib = hip.load()
+    lib.ea_round_ratio.restype = ctypes.c_float
+    lib.ea_round_ratio.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                           ctypes.POINTER(ctypes.c_int)]
+    ov = ctypes.c_int(-1)
+    for E in (-(1 << 30), -(1 << 31), -400, -300):
+        r = lib.ea_round_ratio(0, 3, 0, 1, E, 0, 1, ctypes.byref(ov))
+        assert r == 0.0 and ov.value == 0, E
+    for E in ((1 << 30), (1 << 31) - 1, 5000, 200):
+        r = lib.ea_round_ratio(0, 3, 0, 1, E, 0, 1, ctypes.byref(ov))
+        assert ov.value == 1, E
+    # near the boundaries the exact rounding still runs: 3 * 2^-151 rounds to 2^-149 (fp32), and
+    # 2^-151 is below half the smallest subnormal, so +0
+    r = lib.ea_round_ratio(0, 3, 0, 1, -151, 0, 1, ctypes.byref(ov))
+    assert np.float32(r).view(np.uint32) == 1 and ov.value == 0
+    r = lib.ea_round_ratio(0, 1, 0, 1, -151, 0, 1, ctypes.byref(ov))
+    assert r == 0.0 and ov.value == 0
+
+
+def test_trace_row_of_equal_logits_past_2_to_the_62():
+    """Equal logits t = 1.5 * 2^127 (weights 2^t, exponents past the library's +-2^62 trace
+    range): trace_row's weights and Z carry the exact exponent t - 23, as the reference's
+    RowTrace does, and the output is the mean of v."""
+    hip = _hip()
+    import exactattention_amd as ea
+    from oracle import exact
+    rng = np.random.default_rng(13)
+    q = np.zeros(8, np.uint16)
+    q[0] = 0x5D80                        # 2^60
+    k = np.zeros((3, 8), np.uint16)
+    k[:, 0] = 0x5D80                     # s = 2^120 for every key
+    v = bf16(rng, (3, 5))
+    tr = ea.trace_row(q, k, v, 192.0)    # t = 1.5 * 2^127
+    t = 1.5 * 2.0 ** 127
+    assert tr.t == [t] * 3
+    assert tr.w == [(1 << 23, int(t) - 23)] * 3
+    assert tr.Z == (3 << 23, int(t) - 23)
+    assert np.array_equal(tr.out, exact.attention_row(q, k, v, int(np.float32(192.0).view(np.uint32))))

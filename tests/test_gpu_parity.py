@@ -22,7 +22,7 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden")
 def _run(prob, alpha_bits, out="bf16", splits=0, merge_order=None, **kw):
     """The device tiers only (fallback=False): flags as tier 1 and tier 2 leave them."""
     from exactattention_amd.hip import attention_problem
-    return attention_problem(prob, alpha_bits, out, splits, merge_order, True, False, **kw)
+    return attention_problem(prob, None, out, splits, merge_order, True, False, alpha_bits=alpha_bits, **kw)
 
 
 def _oracle(prob, alpha_bits, out="bf16"):

@@ -30,7 +30,7 @@ def test_serving_session_matches_oracle(gpu):
     Hq, Hkv, d = 4, 2, 128
     ab = default_alpha_bits(d)
     cache = PagedKVCache(num_pages=80, page_size=16, num_kv_heads=Hkv, head_dim=d, max_seqs=3, max_seq_len=400)
-    be = ExactAttentionBackend(cache, Hq, ab)
+    be = ExactAttentionBackend(cache, Hq, alpha_bits=ab)
     slots = [cache.add_sequence(), cache.add_sequence()]
     hist = {s: (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16)) for s in slots}
 
@@ -100,7 +100,7 @@ def test_forward_mixed_batches_match_oracle(gpu):
     Hq, Hkv, d = 4, 2, 128
     ab = default_alpha_bits(d)
     cache = PagedKVCache(num_pages=120, page_size=16, num_kv_heads=Hkv, head_dim=d, max_seqs=4, max_seq_len=512)
-    be = ExactAttentionBackend(cache, Hq, ab)
+    be = ExactAttentionBackend(cache, Hq, alpha_bits=ab)
     slots = [cache.add_sequence() for _ in range(4)]
     hist = {s: (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16)) for s in slots}
     dev = torch.device("cuda")
@@ -154,7 +154,7 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
     Hq, Hkv, d, P = 4, 2, 128, 16
     ab = default_alpha_bits(d)
     cache = PagedKVCache(num_pages=200, page_size=P, num_kv_heads=Hkv, head_dim=d, max_seqs=5, max_seq_len=700)
-    be = ExactAttentionBackend(cache, Hq, ab)
+    be = ExactAttentionBackend(cache, Hq, alpha_bits=ab)
     dev = torch.device("cuda")
     empty = np.zeros((0, Hkv, d), np.uint16)
     hist = {}
@@ -320,7 +320,7 @@ def test_forward_fp32_output_matches_oracle(gpu):
     Hq, Hkv, d = 4, 2, 128
     ab = default_alpha_bits(d)
     cache = PagedKVCache(num_pages=40, page_size=16, num_kv_heads=Hkv, head_dim=d, max_seqs=2, max_seq_len=256)
-    be = ExactAttentionBackend(cache, Hq, ab, out="fp32")
+    be = ExactAttentionBackend(cache, Hq, out="fp32", alpha_bits=ab)
     slots = [cache.add_sequence(), cache.add_sequence()]
     hist = {s: (np.zeros((0, Hkv, d), np.uint16), np.zeros((0, Hkv, d), np.uint16)) for s in slots}
     dev = torch.device("cuda")
@@ -363,7 +363,7 @@ def test_decode_graph_equals_forward_and_oracle(gpu):
     pre = [(bf16(rng, (n, Hkv, d)), bf16(rng, (n, Hkv, d))) for n in lens0]
     for _ in range(2):
         c = PagedKVCache(num_pages=64, page_size=P, num_kv_heads=Hkv, head_dim=d, max_seqs=6, max_seq_len=160)
-        be = ExactAttentionBackend(c, Hq, ab)
+        be = ExactAttentionBackend(c, Hq, alpha_bits=ab)
         ss = [c.add_sequence() for _ in lens0]
         for s, (k, v) in zip(ss, pre):
             c.append(s, k, v)

@@ -120,9 +120,9 @@ def test_random_geometries_match_oracle(gpu):
         print(desc, flush=True)
         if want is None:
             with pytest.raises(ExactAttentionDomainError):
-                attention_problem(prob, ab, out, splits, None, True, True, kernel=kernel)
+                attention_problem(prob, None, out, splits, None, True, True, kernel=kernel, alpha_bits=ab)
             continue
-        got, flags, st = attention_problem(prob, ab, out, splits, None, True, True, kernel=kernel)
+        got, flags, st = attention_problem(prob, None, out, splits, None, True, True, kernel=kernel, alpha_bits=ab)
         assert not np.any(flags), (desc, st)
         assert np.array_equal(got, want), (desc, st)
         if st["decode_kernel_rows"]:

@@ -30,7 +30,7 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden")
 
 def _run(prob, ab, out="bf16", splits=0, **kw):
     from exactattention_amd.hip import attention_problem
-    return attention_problem(prob, ab, out, splits, None, True, False, **kw)
+    return attention_problem(prob, None, out, splits, None, True, False, alpha_bits=ab, **kw)
 
 
 def _oracle(prob, ab, out="bf16"):
@@ -190,7 +190,7 @@ def test_host_exact_tier_finishes_rows_the_device_cannot(gpu):
     for kernel in ("decode", "general"):
         raw, flags, st = _run(prob, ab, kernel=kernel)
         assert flags[0] == 1 and st["uncertified"] == 1, st  # tier 1 and tier 2 cannot decide it
-        got, flags, st = attention_problem(prob, ab, kernel=kernel)  # fallback: the host exact tier
+        got, flags, st = attention_problem(prob, kernel=kernel, alpha_bits=ab)  # fallback: the host exact tier
         assert not flags.any() and st["host_exact_rows"] == 1, st
         assert np.array_equal(got, want)
 

@@ -227,3 +227,76 @@ def test_attention_of_no_query_rows_is_empty():
     assert r.shape == (0, 8) and r.dtype == np.float32
     r = ea.attention(q, k, v, a, mask=np.zeros((0, 5), bool))
     assert r.shape == (0, 8) and r.dtype == np.uint16
+
+
+def test_alpha_is_read_as_a_value():
+    """An alpha given as an int, bool, numpy int or float is the fp32 value numpy converts it to,
+    as the reference's decode_fp32 reads it (src/exactattn/formats.py:120-130); a raw pattern
+    comes only through alpha_bits=, and NaN/inf raise the domain error."""
+    import exactattention_amd as ea
+    from exactattention_amd.formats import alpha_fp32_bits
+    for a in (1, True, np.int32(1), np.int64(1), 1.0, np.float32(1.0), np.float64(1.0), np.array(1.0)):
+        assert alpha_fp32_bits(a) == 0x3F800000, a
+    assert alpha_fp32_bits(np.int32(2)) == 0x40000000
+    assert alpha_fp32_bits(0.1) == int(np.float32(0.1).view(np.uint32))
+    assert alpha_fp32_bits(alpha_bits=0x3E0293EE) == 0x3E0293EE
+    assert alpha_fp32_bits(alpha_bits=np.uint32(1)) == 1
+    with pytest.raises(ValueError):
+        alpha_fp32_bits(1.0, alpha_bits=0x3F800000)
+    with pytest.raises(TypeError):
+        alpha_fp32_bits()
+    with pytest.raises(TypeError):
+        alpha_fp32_bits(alpha_bits=1.0)
+    with pytest.raises(ValueError):
+        alpha_fp32_bits(alpha_bits=1 << 32)
+    for bad in (float("nan"), float("inf"), -np.inf):
+        with pytest.raises(ea.ExactAttentionDomainError):
+            alpha_fp32_bits(bad)
+    with pytest.raises(ea.ExactAttentionDomainError):
+        alpha_fp32_bits(alpha_bits=0x7F800000)
+
+
+def test_public_entry_points_pass_alpha_as_a_value(monkeypatch):
+    """attention / attention_row / attention_hip / attention_geom hand the device launch the fp32
+    pattern of the value (1 -> 0x3F800000, never 2^-149), and alpha_bits= passes a pattern through."""
+    import exactattention_amd as ea
+    from exactattention_amd import hip
+    seen = []
+
+    def fake(prob, alpha=None, out="bf16", *args, alpha_bits=None, **kw):
+        seen.append(hip.alpha_fp32_bits(alpha, alpha_bits))
+        rows = prob["q"].shape[0] * prob["q"].shape[1] * prob["q"].shape[2]
+        dv = prob["v"].shape[-1]
+        res = np.zeros((rows, dv), np.uint16)
+        return res, np.zeros(rows, np.uint8), {}
+
+    monkeypatch.setattr(hip, "attention_problem", fake)
+    rng = np.random.default_rng(9)
+    q, k, v = bf16(rng, (3, 16)), bf16(rng, (5, 16)), bf16(rng, (5, 8))
+    ea.attention(q, k, v, 1)
+    ea.attention(q, k, v, True, mask=np.ones((3, 5), bool))
+    ea.attention_row(q[0], k, v, np.int32(1))
+    ea.attention_hip(q, k, v, 1.0)
+    ea.attention_geom(problem.contiguous(q.reshape(1, 3, 1, 16), k.reshape(1, 1, 5, 16), v.reshape(1, 1, 5, 8),
+                                         np.full((1, 3), 5)), np.float32(1))
+    assert seen == [0x3F800000] * 5
+    ea.attention(q, k, v, alpha_bits=1)
+    assert seen[-1] == 1
+
+
+def test_trace_row_reads_alpha_as_a_value():
+    """trace_row (the host exact tier, no GPU needed) gives the same bits for alpha 1, True,
+    np.int32(1) and np.float32(1.0), equal to the oracle's alpha = 1.0 row and different from
+    the raw-pattern alpha 2^-149."""
+    import exactattention_amd as ea
+    from oracle import exact
+    _lib()
+    rng = np.random.default_rng(10)
+    q, k, v = bf16(rng, (16,)), bf16(rng, (7, 16)), bf16(rng, (7, 8))
+    want = exact.attention_row(q, k, v, 0x3F800000)
+    for a in (1, True, np.int32(1), np.float32(1.0)):
+        assert np.array_equal(ea.trace_row(q, k, v, a).out, want), a
+    assert np.array_equal(ea.trace_row(q, k, v, alpha_bits=0x3F800000).out, want)
+    tiny = exact.attention_row(q, k, v, 1)
+    assert np.array_equal(ea.trace_row(q, k, v, alpha_bits=1).out, tiny)
+    assert not np.array_equal(tiny, want)

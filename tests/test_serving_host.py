@@ -179,7 +179,7 @@ def test_forward_rejects_bad_batches_without_touching_the_cache():
     from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
     c = PagedKVCache(num_pages=4, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
                      digits=False, device="cpu")
-    be = ExactAttentionBackend(c, 2, 0x3E0293EE)
+    be = ExactAttentionBackend(c, 2, alpha_bits=0x3E0293EE)
     a, b = c.add_sequence(), c.add_sequence()
     q, k = torch.zeros((3, 2, 8), dtype=torch.int16), torch.zeros((3, 1, 8), dtype=torch.int16)
     for seqs, lens in (([a, b], [3]), ([a, b], [3, 0]), ([a, b], [1, 1])):
@@ -207,7 +207,7 @@ def test_forward_of_an_empty_batch_returns_empty_results():
     from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
     c = PagedKVCache(num_pages=4, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
                      digits=False, device="cpu")
-    be = ExactAttentionBackend(c, 2, 0x3E0293EE)
+    be = ExactAttentionBackend(c, 2, alpha_bits=0x3E0293EE)
     c.add_sequence()
     z = torch.zeros((0, 2, 8), dtype=torch.int16)
     out, flags = be.forward(z, z[:, :1], z[:, :1], [], [])
@@ -226,7 +226,7 @@ def test_check_flags_never_passes_flag_one():
     from exactattention_amd.serving import ExactAttentionBackend, PagedKVCache
     c = PagedKVCache(num_pages=4, page_size=4, num_kv_heads=1, head_dim=8, max_seqs=2, max_seq_len=16,
                      digits=False, device="cpu")
-    be = ExactAttentionBackend(c, 2, 0x3E0293EE)
+    be = ExactAttentionBackend(c, 2, alpha_bits=0x3E0293EE)
     be.check_flags(torch.zeros((3, 2), dtype=torch.uint8))
     with pytest.raises(ExactAttentionUncertifiedError):
         be.check_flags(torch.tensor([[0, 1], [0, 0]], dtype=torch.uint8))
