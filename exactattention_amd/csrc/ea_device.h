@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ea_quotient.h"
 #include "ea_tables.h"
 
 namespace ea {
@@ -399,132 +400,6 @@ __device__ inline int weight_wide(uint32_t t_bits, int32_t* M, int64_t* E) {
     return 0;
 }
 
-// Multiword unsigned, 32-bit limbs (tier 2 final rounding and logit rounding)
-#define EA_MW 12
-struct mw {
-    uint32_t w[EA_MW];
-};
-__device__ inline void mw_zero(mw& a) {
-#pragma unroll
-    for (int i = 0; i < EA_MW; ++i) a.w[i] = 0;
-}
-__device__ inline void mw_from_u128(mw& a, u128 x) {
-    mw_zero(a);
-    for (int i = 0; i < 4; ++i) a.w[i] = (uint32_t)(x >> (32 * i));
-}
-__device__ inline int mw_bitlen(const mw& a) {
-    for (int i = EA_MW - 1; i >= 0; --i)
-        if (a.w[i]) return 32 * i + (32 - __clz(a.w[i]));
-    return 0;
-}
-__device__ inline void mw_shl(mw& r, const mw& a, int s) {
-    mw t;
-    mw_zero(t);
-    int L = s >> 5, b = s & 31;
-    for (int i = EA_MW - 1; i >= 0; --i) {
-        int src = i - L;
-        if (src < 0) continue;
-        uint64_t v = (uint64_t)a.w[src] << b;
-        if (b && src - 1 >= 0) v |= (uint64_t)a.w[src - 1] >> (32 - b);
-        t.w[i] = (uint32_t)v;
-    }
-    r = t;
-}
-__device__ inline int mw_cmp(const mw& a, const mw& b) {
-    for (int i = EA_MW - 1; i >= 0; --i)
-        if (a.w[i] != b.w[i]) return a.w[i] < b.w[i] ? -1 : 1;
-    return 0;
-}
-__device__ inline void mw_sub(mw& a, const mw& b) {
-    int64_t br = 0;
-    for (int i = 0; i < EA_MW; ++i) {
-        int64_t x = (int64_t)a.w[i] - (int64_t)b.w[i] - br;
-        br = x < 0;
-        a.w[i] = (uint32_t)(x + (br ? ((int64_t)1 << 32) : 0));
-    }
-}
-
-struct rnd {
-    int sign;
-    uint64_t m;
-    int e;
-    int overflow;
-};
-__device__ inline bool rnd_eq(const rnd& a, const rnd& b) {
-    if (a.overflow || b.overflow) return false;
-    if (a.m == 0 && b.m == 0) return true;
-    return a.sign == b.sign && a.m == b.m && a.e == b.e;
-}
-
-// RN-even of (a / b) * 2^E into (p, qmin, emax=127); a, b < 2^128, b > 0.
-__device__ inline rnd round_ratio(u128 a_, u128 b_, int E, int sign, int p, int qmin) {
-    rnd r = {sign, 0, 0, 0};
-    if (a_ == 0) return r;
-    mw a, b, t;
-    mw_from_u128(a, a_);
-    mw_from_u128(b, b_);
-    int k = mw_bitlen(a) - mw_bitlen(b);
-    if (k >= 0) {
-        mw_shl(t, b, k);
-        if (mw_cmp(a, t) < 0) --k;
-    } else {
-        mw_shl(t, a, -k);
-        if (mw_cmp(t, b) < 0) --k;
-    }
-    long K = (long)k + E;
-    if (K < (long)qmin - 1) return r;
-    long qe = K - (p - 1);
-    if (qe < qmin) qe = qmin;
-    long s = (long)E - qe;
-    if (s > 200 || s < -200) {  // outside what 12 limbs hold; K range makes this unreachable
-        r.overflow = 1;
-        return r;
-    }
-    mw n = a, d = b;
-    if (s >= 0) mw_shl(n, a, (int)s);
-    else mw_shl(d, b, (int)-s);
-    uint64_t q = 0;
-    for (int i = p + 1; i >= 0; --i) {
-        mw_shl(t, d, i);
-        if (mw_cmp(n, t) >= 0) {
-            mw_sub(n, t);
-            q |= 1ull << i;
-        }
-    }
-    mw_shl(t, n, 1);
-    int c = mw_cmp(t, d);
-    if (c > 0 || (c == 0 && (q & 1))) ++q;
-    if (q == (1ull << p)) {
-        q >>= 1;
-        ++qe;
-    }
-    if (qe + (63 - __clzll(q)) > 127) r.overflow = 1;
-    r.m = q;
-    r.e = (int)qe;
-    return r;
-}
-
-__device__ inline uint32_t rnd_bits(const rnd& r, int fp32) {
-    if (r.m == 0) return 0;
-    int p = fp32 ? 24 : 8, qmin = fp32 ? -149 : -133;
-    uint64_t m = r.m;
-    int e = r.e;
-    while (m < (1ull << (p - 1)) && e > qmin) {
-        m <<= 1;
-        --e;
-    }
-    uint32_t field, frac;
-    if (m < (1ull << (p - 1))) {
-        field = 0;
-        frac = (uint32_t)m;
-    } else {
-        field = (uint32_t)(e - qmin + 1);
-        frac = (uint32_t)(m - (1ull << (p - 1)));
-    }
-    uint32_t sg = r.sign < 0 ? 1u : 0u;
-    return (sg << (p - 1 + 8)) | (field << (p - 1)) | frac;
-}
-
 // (W >> s) mod 2^64 for the 192-bit W = (w2 : w1 : w0) and s >= 0
 __device__ __forceinline__ uint64_t shr192(uint64_t w2, uint64_t w1, uint64_t w0, int s) {
     if (s >= 192) return 0;
@@ -576,8 +451,7 @@ __device__ inline int rn32_prod(int32_t am, i128 X, int E, uint32_t* bits) {
         ++qe;
     }
     if (q && qe + (63 - __clzll(q)) > 127) return 2;
-    rnd r = {sign, q, (int)qe, 0};
-    *bits = rnd_bits(r, 1);
+    *bits = fmt_bits((uint32_t)q, (int)qe, sign < 0, 1);
     return 0;
 }
 

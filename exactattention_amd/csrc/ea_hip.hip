@@ -888,28 +888,10 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
                         accu += ((u128)S.ahi[q][c] << 64) | S.alo[q][c];
                         err += S.aer[q][c];
                     }
+                    // N_c in [acc, acc + err] 2^base over Z in [z, z + ze] 2^(R - F)
                     const i128 acc = (i128)accu;
-                    // interval [acc, acc+err] * 2^base over [z, z+ze] * 2^(R-F)
-                    i128 Zlo = z, Zhi = z + (i128)ze;
-                    i128 Nlo = acc, Nhi = acc + (i128)err;
-                    i128 ln_, ld, hn, hd;
-                    if (Nlo >= 0) {
-                        ln_ = Nlo; ld = Zhi; hn = Nhi; hd = Zlo;
-                    } else if (Nhi <= 0) {
-                        ln_ = Nlo; ld = Zlo; hn = Nhi; hd = Zhi;
-                    } else {
-                        ln_ = Nlo; ld = Zlo; hn = Nhi; hd = Zlo;
-                    }
-                    int64_t sh = base - (R - F);
-                    int p = P.out_fp32 ? 24 : 8, qmin = P.out_fp32 ? -149 : -133;
-                    if (Zlo <= 0 || sh > 100000 || sh < -100000) {
+                    if (!certify_quotient(acc, acc + (i128)err, z, z + (i128)ze, base - (R - F), P.out_fp32, &bits))
                         ok = false;
-                    } else {
-                        rnd rl = round_ratio(ln_ < 0 ? (u128)(-ln_) : (u128)ln_, (u128)ld, (int)sh, ln_ < 0 ? -1 : 1, p, qmin);
-                        rnd rh = round_ratio(hn < 0 ? (u128)(-hn) : (u128)hn, (u128)hd, (int)sh, hn < 0 ? -1 : 1, p, qmin);
-                        if (!rnd_eq(rl, rh)) ok = false;
-                        else bits = rnd_bits(rl, P.out_fp32);
-                    }
                 }
                 if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = bits;
                 else ((uint16_t*)P.out)[obase + c] = (uint16_t)bits;
@@ -1062,10 +1044,24 @@ __global__ void ea_kat_round_ratio(int64_t n, const uint64_t* ah, const uint64_t
                                    int32_t* ov) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    u128 a = ((u128)ah[i] << 64) | al[i], b = ((u128)bh[i] << 64) | bl[i];
-    rnd r = round_ratio(a, b, E[i], neg[i] ? -1 : 1, fp32 ? 24 : 8, fp32 ? -149 : -133);
-    ov[i] = r.overflow;
-    bits[i] = r.overflow ? 0u : rnd_bits(r, fp32);
+    const u128 a = ((u128)ah[i] << 64) | al[i], b = ((u128)bh[i] << 64) | bl[i];
+    quant y;
+    const int st = rn_quotient(a, b, E[i], fp32 ? 24 : 8, fp32 ? -149 : -133, &y);
+    ov[i] = st;
+    bits[i] = st ? 0u : fmt_bits(y.Q, y.qe, neg[i] != 0, fp32);
+}
+
+// v: per case Nlo, Nhi, Zlo, Zhi as (hi, lo) word pairs, then sh (9 int64)
+__global__ void ea_kat_certify_quotient(int64_t n, const int64_t* v, int32_t fp32, uint32_t* bits, int32_t* ok) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t* c = v + 9 * i;
+    auto s128 = [](int64_t hi, int64_t lo) { return (i128)(((u128)(uint64_t)hi << 64) | (uint64_t)lo); };
+    uint32_t b = 0;
+    ok[i] = certify_quotient(s128(c[0], c[1]), s128(c[2], c[3]), s128(c[4], c[5]), s128(c[6], c[7]), c[8], fp32, &b)
+                ? 1
+                : 0;
+    bits[i] = b;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1738,6 +1734,15 @@ int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo
     if (n <= 0) return n < 0 ? -1 : 0;
     hipLaunchKernelGGL(ea_kat_round_ratio, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, n,
                        a_hi, a_lo, b_hi, b_lo, E, neg, fp32, bits, overflow);
+    return herr(hipGetLastError());
+}
+
+int ea_hip_kat_certify_quotient(int64_t n, const int64_t* cases, int32_t fp32, uint32_t* bits, int32_t* ok,
+                                ea_stream_t stream) {
+    if (n <= 0) return n < 0 ? -1 : 0;
+    if (!cases || !bits || !ok) return -1;
+    hipLaunchKernelGGL(ea_kat_certify_quotient, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       n, cases, fp32, bits, ok);
     return herr(hipGetLastError());
 }
 

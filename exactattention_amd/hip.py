@@ -98,6 +98,8 @@ def load():
         lib.ea_hip_kat_round.restype = ctypes.c_int
         lib.ea_hip_kat_round_ratio.argtypes = [ctypes.c_int64] + [P] * 6 + [ctypes.c_int32, P, P, P]
         lib.ea_hip_kat_round_ratio.restype = ctypes.c_int
+        lib.ea_hip_kat_certify_quotient.argtypes = [ctypes.c_int64, P, ctypes.c_int32, P, P, P]
+        lib.ea_hip_kat_certify_quotient.restype = ctypes.c_int
         lib.ea_hip_kv_append.argtypes = [P, P, ctypes.c_int64, ctypes.c_int64, P, P, P, ctypes.c_int64, P,
                                          ctypes.c_int64, P, P, ctypes.c_int64, P]
         lib.ea_hip_kv_append.restype = ctypes.c_int

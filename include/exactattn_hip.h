@@ -220,7 +220,11 @@ float ea_round_ratio(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo,
  * ea_hip_kat_round: RN of the fp64 interval [x - r, x + r] into bf16/fp32 -> bits, certified.
  *   Reference counterpart: the combine's _ratio_round (src/exactattn/triton_kernels.py:150-195).
  * ea_hip_kat_round_ratio: RN-even of (a/b)*2^E, a,b 128-bit -> bits, overflow.
- *   Reference counterpart: ea_round_ratio (csrc/exact_attention_cpu.cpp:632-638). */
+ *   Reference counterpart: ea_round_ratio (csrc/exact_attention_cpu.cpp:632-638).
+ * ea_hip_kat_certify_quotient: tier 2's certified final rounding of N / Z 2^sh over N in
+ *   [Nlo, Nhi], Z in [Zlo, Zhi]; `cases` holds 9 int64 per case: Nlo, Nhi, Zlo, Zhi as signed
+ *   128-bit (hi, lo) word pairs, then sh -> bits, ok (1 certified). Reference counterpart: the
+ *   interval rounding of finalize (csrc/exact_attention_cpu.cpp:450-490). */
 int ea_hip_kat_weight(int64_t n, const uint32_t* t_bits, int32_t* M, int64_t* E, int32_t* status, int32_t* M2,
                       int64_t* E2, int32_t* status2, ea_stream_t stream);
 int ea_hip_kat_round(int64_t n, const double* x, const double* r, int32_t fp32, uint32_t* bits, int32_t* ok,
@@ -232,6 +236,8 @@ int ea_hip_kat_wave_max(int64_t nwaves, const int32_t* in, int32_t* out, ea_stre
 int ea_hip_kat_round_ratio(int64_t n, const uint64_t* a_hi, const uint64_t* a_lo, const uint64_t* b_hi,
                            const uint64_t* b_lo, const int32_t* E, const int32_t* neg, int32_t fp32, uint32_t* bits,
                            int32_t* overflow, ea_stream_t stream);
+int ea_hip_kat_certify_quotient(int64_t n, const int64_t* cases, int32_t fp32, uint32_t* bits, int32_t* ok,
+                                ea_stream_t stream);
 /* ea_hip_kat_rn32_prod: the exact logit RN32(am * X * 2^E), X a signed 128-bit integer given as
  * (x_hi signed, x_lo) words, |am| < 2^24 -> fp32 bits, status (0 ok, 2 overflow). The prefill
  * kernel's cold path and tier 2 round exact scores with it.
