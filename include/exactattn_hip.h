@@ -164,11 +164,13 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* b, const ea_options
  * reference. The workspace is a fixed array of EA_NOALLOC_SCRATCH_BYTES in device memory that each
  * GPU the library runs on holds until the process ends; the call allocates nothing. Geometries
  * whose ea_hip_workspace_size exceeds it return -4 (decode and verification steps fit: C2 needs
- * about 5 MB; long-context decode of 131K keys about 60 MB; int8 prefill steps usually do not).
- * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
- * threads) race and must be serialised by the caller. Same buffers, options, return codes and
- * stream semantics as ea_hip_attention otherwise (enqueue only, no sync). */
-#define EA_NOALLOC_SCRATCH_BYTES (64u << 20)
+ * about 5 MB, long-context decode of 16 sequences up to 131,072 keys about 72 MB; int8 prefill
+ * steps of many tokens do not). Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, two threads) race and must be serialised by the caller. The first call
+ * on each device resolves the array's device address (hipGetSymbolAddress): make it outside
+ * stream capture; later calls may be captured. Same buffers, options, return codes and stream
+ * semantics as ea_hip_attention otherwise (enqueue only, no sync). */
+#define EA_NOALLOC_SCRATCH_BYTES (128u << 20)
 int ea_hip_attention_noalloc(const ea_geometry* g, const ea_buffers* b, const ea_options* o, ea_stream_t stream);
 
 /* Host exact tier (tier 3) for a step ea_hip_attention enqueued with the same geometry, buffers
