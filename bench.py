@@ -86,10 +86,9 @@ class HipEvents:
             self.h.hipEventDestroy(self.ev[i])
 
 
-def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
-    """The reference's certified CPU kernel (oracle/_ref, compiled from its csrc) on the full
-    C2 workload in its CSR form; the oracle's C restatement when that build is absent."""
-    from oracle import oracle
+def c2_csr(prob: dict):
+    """C2 in the reference CPU ABI's CSR form: q (B*Hq, d); K, V rows of (sequence, KV head) s at
+    s*S .. s*S + len - 1; rows (sequence, query head), each over its sequence's keys."""
     g = prob["geom"]
     B, Hkv, Hq, d, dv = g["num_seqs"], g["num_kv_heads"], g["num_q_heads"], g["head_dim"], g["head_dim_v"]
     P = g["page_size"]
@@ -106,6 +105,15 @@ def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
     L = prob["seq_len"].repeat(Hq).astype(np.int64)
     row_ptr = np.concatenate([[0], np.cumsum(L)]).astype(np.int64)
     key_idx = np.concatenate([s * S + np.arange(l) for s, l in zip(seg, L)]).astype(np.int64)
+    return q, Kf, Vf, row_ptr, key_idx
+
+
+def cpu_baseline(prob: dict, alpha_bits: int, threads: int, csr=None):
+    """The reference's certified CPU kernel (oracle/_ref, compiled from its csrc) on the full
+    C2 workload in its CSR form; the oracle's C restatement when that build is absent."""
+    from oracle import oracle
+    q, Kf, Vf, row_ptr, key_idx = csr if csr is not None else c2_csr(prob)
+    L = np.diff(row_ptr)
     ref = oracle.ref_available()
     kind = "reference" if ref else "port"
     run = lambda: oracle.raw_csr(q, Kf, Vf, alpha_bits, row_ptr, key_idx, "bf16", 64, 64, 8, 0, threads,
@@ -126,6 +134,100 @@ def cpu_baseline(prob: dict, alpha_bits: int, threads: int):
             "sample": f"full C2 step ({pairs} query-key pairs, splits=8, 64-key tiles, int64), median of 3 "
                       f"after 1 warm-up; {pairs / t / 1e6:.2f} M pairs/s; {int((flags != 0).sum())} rows flagged",
             "wall_s": round(t, 3)}, res
+
+
+def drop_in_line(prob: dict, alpha_bits: int, csr, reps: int = 3) -> dict:
+    """The C drop-in ea_attention_hip (the reference's ea_attention_cpu ABI: host arrays in, host
+    arrays out) on C2 in its CSR form, the same arrays and arguments the CPU baseline takes
+    (splits=8, 64-key tiles, int64): wall time per call with the host-to-device copy of q, K, V
+    and the CSR metadata and the copy back, median of `reps` after a warm-up call (which sizes the
+    library's device arena). Throughput over the same algorithmic bytes as the CPU baseline's."""
+    import torch
+    from exactattention_amd import hip
+    q, Kf, Vf, row_ptr, key_idx = csr
+    alpha = np.array([alpha_bits], np.uint32).view(np.float32)[0]
+    lay = hip.csr_layout(row_ptr, key_idx, Kf.shape[0])
+    hip.ea_attention_hip(q, Kf, Vf, alpha, row_ptr, key_idx, splits=8)  # warm-up
+    times = []
+    res = flags = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        res, flags, st = hip.ea_attention_hip(q, Kf, Vf, alpha, row_ptr, key_idx, splits=8)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    # the host-to-device copy of the K and V arrays alone (pageable numpy memory), for scale
+    t0 = time.perf_counter()
+    kd = torch.from_numpy(Kf.view(np.int16)).to("cuda:0")
+    vd = torch.from_numpy(Vf.view(np.int16)).to("cuda:0")
+    torch.cuda.synchronize()
+    h2d = time.perf_counter() - t0
+    del kd, vd
+    torch.cuda.empty_cache()
+    golden = json.load(open(GOLDEN)).get("C2", {}).get("sha256") if os.path.exists(GOLDEN) else None
+    pairs = int(np.diff(row_ptr).sum())
+    return {"workload": "C2 in CSR form through ea_attention_hip (host arrays, the CPU baseline's arguments)",
+            "value": round(algorithmic_bytes(prob) / t / 1e9, 3), "unit": "GB/s", "ms_per_call": round(t * 1e3, 3),
+            "pairs_per_s": round(pairs / t, 1), "h2d_kv_ms": round(h2d * 1e3, 3),
+            "layout": lay, "bit_exact": (hashlib.sha256(res.tobytes()).hexdigest() == golden) if golden else None,
+            "flags_nonzero": int((flags != 0).sum()),
+            "basis": "wall clock per call, median of 3 after a warm-up; includes the host-to-device copies"}
+
+
+# The reference's published ExactAttention step times on one RTX PRO 6000 Blackwell (ms): run 1122
+# (docs/DESIGN.md:1055-1065) and the best per shape of run 1124 (:1228-1229), from
+# scripts/bench_vs_flashinfer.py: 16 query / 8 KV heads, d = 128, bf16, K/V contiguous per
+# (sequence, KV head), decode T = 1 over n keys, verify T = 8 draft tokens causal at the end of n
+# keys, CUDA graphs.
+PUBLISHED_SHAPES = [  # (T, B, n, run 1122 ms, best of run 1124 ms or None)
+    (1, 1, 4096, 0.073, None), (1, 1, 16384, 0.193, 0.177), (1, 1, 65536, 0.534, None),
+    (1, 8, 16384, 0.950, 0.909), (1, 32, 16384, 4.301, 3.668),
+    (8, 1, 4096, 0.303, None), (8, 1, 16384, 0.686, 0.617), (8, 8, 4096, 0.859, 0.820), (8, 8, 16384, 2.591, None)]
+
+
+def published_shapes_line(steps: int, warmup: int) -> dict:
+    """The reference's published shapes (PUBLISHED_SHAPES) on this library: bf16 N(0,1) q, K, V
+    drawn on the device (torch, seed 2024), K/V contiguous per (sequence, KV head) as the
+    reference lays them out, the step captured in a HIP graph and replayed. GB/s counts the bf16 K
+    and V bytes only, as the reference's harness does. Bits: the auto split count's output equals
+    a one-split run's (the certified bits cannot depend on the schedule), 0 rows flagged."""
+    import torch
+    from exactattention_amd import configs, problem
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    ab = configs.alpha_bits()
+    Hq, Hkv, d = 16, 8, 128
+    out = []
+    for T, B, n, ref_ms, ref_best in PUBLISHED_SHAPES:
+        gen = torch.Generator(device="cuda:0").manual_seed(2024)
+        q = torch.randn((B, T, Hq, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        k = torch.randn((B, Hkv, n, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        v = torch.randn((B, Hkv, n, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        kv_len = np.tile(n - T + 1 + np.arange(T), B).astype(np.int32)
+        g = problem._geom(B, T, Hq, Hkv, d, d, (T * Hq * d, Hq * d, d), (T * Hq * d, Hq * d, d),
+                          (Hkv * n * d, d, n * d), (Hkv * n * d, d, n * d), 1, 0, n)
+        prob = dict(geom=g, q=q, k=k, v=v, seq_len=np.full(B, n, np.int32), kv_len=kv_len, block_table=None,
+                    block_table_offset=None, tree_mask=None, tree_base=None, out_shape=(B, T, Hq, d))
+        one = DeviceProblem(prob, "bf16", 1, "cuda:0")
+        launch_hip(one, ab)
+        torch.cuda.synchronize()
+        want = one.out.cpu().numpy().view(np.uint16)
+        del one
+        dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+        ms, got = graph_steps(dp, ab, steps, warmup)
+        st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+        kv_bytes = 2 * B * Hkv * n * d * 2
+        gbs = kv_bytes / (ms * 1e-3) / 1e9
+        kernel = "prefill" if st["prefill_kernel_rows"] else ("decode" if st["decode_kernel_rows"] else "general")
+        out.append({"shape": f"{'decode' if T == 1 else 'verify T=8'} B={B} n={n}", "ms": round(ms, 5),
+                    "kv_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": kernel,
+                    "nsplit": dp.nsplit, "ref_ms_run1122": ref_ms, "ref_ms_best_run1124": ref_best,
+                    "speedup_vs_ref_best": round((ref_best or ref_ms) / ms, 2),
+                    "bits_equal_one_split": bool(np.array_equal(got, want)),
+                    "rows_flagged": int(st["tier1_flagged"])})
+        del dp, prob, q, k, v
+        torch.cuda.empty_cache()
+    return {"basis": "HIP-graph replays (events around them); bf16 K+V bytes only; reference figures from one "
+                     "RTX PRO 6000 Blackwell (about 1.79 TB/s), a different GPU: context, not a like-for-like "
+                     "comparison", "shapes": out}
 
 
 MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, vendor figure (256 CUs, 2.4 GHz)
@@ -584,7 +686,7 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill measurement")
-    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving"), default=None,
+    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving", "shapes", "drop_in"), default=None,
                     help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
                     help="after the timed steps, run 5 steps of the phase-clock build and report it")
@@ -616,6 +718,14 @@ def main():
         return
     if args.only == "C5":
         print(json.dumps({"long_context": long_context_line(args.steps, args.warmup)}), flush=True)
+        return
+    if args.only == "shapes":
+        print(json.dumps({"published_shapes": published_shapes_line(args.steps, args.warmup)}), flush=True)
+        return
+    if args.only == "drop_in":
+        from exactattention_amd import configs
+        p2 = configs.c2()
+        print(json.dumps({"drop_in": drop_in_line(p2, configs.alpha_bits(), c2_csr(p2))}), flush=True)
         return
     if args.only == "serving":
         from exactattention_amd import configs
@@ -674,9 +784,12 @@ def main():
         line["long_context"] = long_context_line(max(5, min(args.steps, 10)), 2)
     if args.only is None:
         line["serving"] = serving_line(prob, ab, max(5, min(args.steps, 20)))
+        line["published_shapes"] = published_shapes_line(max(5, min(args.steps, 20)), 2)
     if args.only is None and not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
-        cb, cres = cpu_baseline(prob, ab, threads)
+        csr = c2_csr(prob)
+        line["drop_in"] = drop_in_line(prob, ab, csr)
+        cb, cres = cpu_baseline(prob, ab, threads, csr)
         line["cpu_baseline"] = cb
         line["cpu_bits_equal"] = bool(np.array_equal(cres.reshape(out.shape), out)) if cres is not None else None
     print(json.dumps(line), flush=True)

@@ -79,10 +79,27 @@ def attention_hip(q_bits, k_bits, v_bits, alpha=None, kv_len=None, row_ptr=None,
             raise ValueError("kv_len must lie in [0, n]")
         prob = problem.contiguous(q.reshape(1, R, 1, -1), k.reshape(1, 1, n, -1), v.reshape(1, 1, n, -1),
                                   kv_len.reshape(1, R))
-    else:
-        prob = problem.csr(q, k, v, row_ptr, key_idx)
-    res, flags, _ = attention_problem(prob, None, out, splits, merge_order, True, fallback, device, alpha_bits=ab)
-    return _finish(res.reshape(R, -1), out), flags
+        res, flags, _ = attention_problem(prob, None, out, splits, merge_order, True, fallback, device, alpha_bits=ab)
+        return _finish(res.reshape(R, -1), out), flags
+    # CSR rows: rows whose key lists are prefixes of one list share a sequence (and its K/V reads),
+    # as the C drop-in ea_attention_hip groups them; rows with no key are +0, certified
+    from .hip import csr_layout
+    row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int64)
+    key_idx = np.ascontiguousarray(key_idx if key_idx is not None else np.zeros(0), dtype=np.int64)
+    if row_ptr.shape != (R + 1,):
+        raise ValueError("row_ptr must have rows + 1 entries")
+    lay = csr_layout(row_ptr, key_idx, n, arrays=True)
+    dv = v.shape[1]
+    res = np.zeros((R, dv), np.uint32 if out == "fp32" else np.uint16)
+    flags = np.zeros(R, np.uint8)
+    if lay["num_seqs"] > 0:
+        prob = problem.csr(q, k, v, lay)
+        r, fl, _ = attention_problem(prob, None, out, splits, merge_order, True, fallback, device, alpha_bits=ab)
+        tok = lay["tok_row"]
+        m = tok >= 0
+        res[tok[m]] = r.reshape(-1, dv)[m]
+        flags[tok[m]] = fl[m]
+    return _finish(res, out), flags
 
 
 def attention_geom(prob: dict, alpha=None, out: str = "bf16", splits: int = 0, merge_order=None,

@@ -6,7 +6,7 @@ import os
 import subprocess
 import sys
 
-SOURCES = ["ea_hip.hip", "ea_decode.hip", "ea_prefill.hip", "ea_exact_host.cpp"]
+SOURCES = ["ea_hip.hip", "ea_decode.hip", "ea_prefill.hip", "ea_exact_host.cpp", "ea_csr.cpp"]
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libexactattn_hip.so")

@@ -1507,143 +1507,6 @@ float ea_round_ratio(uint64_t a_hi, uint64_t a_lo, uint64_t b_hi, uint64_t b_lo,
     return r;
 }
 
-static int attention_csr_impl(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v,
-                              int64_t nkeys, int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx,
-                              int fp32_out, int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads,
-                              void* out, uint8_t* flags, int64_t* stats) {
-    (void)order_seed; (void)nthreads;
-    // the reference's argument checks, in its order (csrc/exact_attention_cpu.cpp:589-592)
-    if (d <= 0 || d > EA_MAXD || dv <= 0 || dv > EA_MAXDV || tile <= 0 || splits <= 0) return -1;
-    if (acc_bits != 64 && acc_bits != 128) return -2;
-    uint32_t alpha_bits;
-    memcpy(&alpha_bits, &alpha, 4);
-    if (((alpha_bits >> 23) & 0xFF) == 0xFF) return -3;
-    if ((d & 7) || (dv & 1) || rows < 0 || nkeys < 0) return -1;
-    if (rows == 0) return 0;
-    if (!q || !row_ptr || !out || !flags || (nkeys > 0 && (!k || !v))) return -1;
-    // Each CSR row is one sequence whose page table is its key list (page size 1).
-    int64_t maxn = 0;
-    if (row_ptr[0] < 0) return -1;
-    for (int64_t r = 0; r < rows; ++r) {
-        const int64_t len = row_ptr[r + 1] - row_ptr[r];
-        if (len < 0) return -1;
-        maxn = len > maxn ? len : maxn;
-    }
-    const int64_t nnz = row_ptr[rows] - row_ptr[0];
-    if (maxn > INT32_MAX / 2 || nkeys > INT32_MAX) return -1;
-    if (nnz > 0 && !key_idx) return -1;
-    for (int64_t j = row_ptr[0]; j < row_ptr[rows]; ++j)
-        if (key_idx[j] < 0 || key_idx[j] >= nkeys) return -1;  // the kernels gather through it
-    ea_geometry g;
-    memset(&g, 0, sizeof(g));
-    g.num_seqs = (int32_t)rows; g.num_tokens = 1; g.num_q_heads = 1; g.num_kv_heads = 1;
-    g.head_dim = d; g.head_dim_v = dv;
-    g.q_seq_stride = d; g.q_tok_stride = 0; g.q_head_stride = 0;
-    g.o_seq_stride = dv; g.o_tok_stride = 0; g.o_head_stride = 0;
-    g.k_page_stride = d; g.k_slot_stride = 0; g.k_head_stride = 0;
-    g.v_page_stride = dv; g.v_slot_stride = 0; g.v_head_stride = 0;
-    g.page_size = 1; g.block_table_stride = 0; g.max_seq_len = (int32_t)maxn;
-    ea_options o;
-    memset(&o, 0, sizeof(o));
-    o.alpha_bits = alpha_bits; o.out_fp32 = fp32_out ? 1 : 0; o.splits = splits; o.tier2 = 1;
-    size_t ws_bytes = 0;
-    int32_t ns = 0;
-    int rc = ea_hip_workspace_size(&g, &o, &ws_bytes, &ns);
-    if (rc) return rc;
-    std::vector<int32_t> bt((size_t)(nnz > 0 ? nnz : 1)), sl((size_t)rows);
-    std::vector<int64_t> bo((size_t)rows);
-    for (int64_t r = 0; r < rows; ++r) {
-        sl[(size_t)r] = (int32_t)(row_ptr[r + 1] - row_ptr[r]);
-        bo[(size_t)r] = row_ptr[r] - row_ptr[0];
-    }
-    for (int64_t j = 0; j < nnz; ++j) bt[(size_t)j] = (int32_t)key_idx[row_ptr[0] + j];
-    const size_t osz = fp32_out ? 4 : 2;
-    void *dq = 0, *dk = 0, *dv_ = 0, *dbt = 0, *dbo = 0, *dsl = 0, *dout = 0, *dfl = 0, *dws = 0, *dst = 0;
-    hipError_t e = hipSuccess;
-#define EA_TRY(x) do { e = (x); if (e != hipSuccess) goto done; } while (0)
-    EA_TRY(hipMalloc(&dq, (size_t)rows * d * 2));
-    EA_TRY(hipMalloc(&dk, (size_t)(nkeys > 0 ? nkeys : 1) * d * 2));
-    EA_TRY(hipMalloc(&dv_, (size_t)(nkeys > 0 ? nkeys : 1) * dv * 2));
-    EA_TRY(hipMalloc(&dbt, bt.size() * 4));
-    EA_TRY(hipMalloc(&dbo, (size_t)rows * 8));
-    EA_TRY(hipMalloc(&dsl, (size_t)rows * 4));
-    EA_TRY(hipMalloc(&dout, (size_t)rows * dv * osz));
-    EA_TRY(hipMalloc(&dfl, (size_t)rows));
-    EA_TRY(hipMalloc(&dws, ws_bytes > 0 ? ws_bytes : 256));
-    EA_TRY(hipMalloc(&dst, 16 * sizeof(int64_t)));
-    EA_TRY(hipMemcpy(dq, q, (size_t)rows * d * 2, hipMemcpyHostToDevice));
-    if (nkeys > 0) {
-        EA_TRY(hipMemcpy(dk, k, (size_t)nkeys * d * 2, hipMemcpyHostToDevice));
-        EA_TRY(hipMemcpy(dv_, v, (size_t)nkeys * dv * 2, hipMemcpyHostToDevice));
-    }
-    EA_TRY(hipMemcpy(dbt, bt.data(), bt.size() * 4, hipMemcpyHostToDevice));
-    EA_TRY(hipMemcpy(dbo, bo.data(), (size_t)rows * 8, hipMemcpyHostToDevice));
-    EA_TRY(hipMemcpy(dsl, sl.data(), (size_t)rows * 4, hipMemcpyHostToDevice));
-    EA_TRY(hipMemset(dst, 0, 16 * sizeof(int64_t)));
-    {
-        ea_buffers b;
-        memset(&b, 0, sizeof(b));
-        b.q = (const uint16_t*)dq; b.k = (const uint16_t*)dk; b.v = (const uint16_t*)dv_;
-        b.seq_len = (const int32_t*)dsl; b.kv_len = (const int32_t*)dsl;
-        b.block_table = (const int32_t*)dbt; b.block_table_offset = (const int64_t*)dbo;
-        b.out = dout; b.flags = (uint8_t*)dfl;
-        o.stats = (int64_t*)dst;
-        rc = ea_hip_attention(&g, &b, &o, dws, ws_bytes, 0);
-        if (rc) goto done;
-    }
-    EA_TRY(hipDeviceSynchronize());
-    EA_TRY(hipMemcpy(out, dout, (size_t)rows * dv * osz, hipMemcpyDeviceToHost));
-    EA_TRY(hipMemcpy(flags, dfl, (size_t)rows, hipMemcpyDeviceToHost));
-    if (stats) {
-        int64_t hs[16];
-        EA_TRY(hipMemcpy(hs, dst, sizeof(hs), hipMemcpyDeviceToHost));
-        stats[0] += hs[5];
-        stats[1] += hs[6];
-        stats[2] += hs[7];
-    }
-    {
-        // rows the device tiers left uncertified: the host exact tier on the caller's arrays
-        std::vector<uint16_t> kr, vr;
-        for (int64_t r = 0; r < rows; ++r) {
-            if (flags[r] != 1) continue;
-            const int64_t j0 = row_ptr[r], n = row_ptr[r + 1] - row_ptr[r];
-            kr.resize((size_t)(n * d));
-            vr.resize((size_t)(n * dv));
-            for (int64_t j = 0; j < n; ++j) {
-                memcpy(&kr[(size_t)(j * d)], k + key_idx[j0 + j] * d, (size_t)d * 2);
-                memcpy(&vr[(size_t)(j * dv)], v + key_idx[j0 + j] * dv, (size_t)dv * 2);
-            }
-            char* dst_row = (char*)out + (size_t)r * dv * osz;
-            const int x = eax::exact_row(q + r * d, d, kr.data(), vr.data(), n, dv, alpha_bits, fp32_out ? 1 : 0,
-                                         dst_row, nullptr);
-            if (x == eax::EAX_NOMEM) {
-                rc = EA_ERR_HOST_MEMORY;
-                goto done;
-            }
-            if (x != eax::EAX_OK) memset(dst_row, 0, (size_t)dv * osz);
-            flags[r] = x == eax::EAX_OK ? 0 : 2;
-        }
-    }
-done:
-    (void)hipFree(dq); (void)hipFree(dk); (void)hipFree(dv_); (void)hipFree(dbt); (void)hipFree(dbo);
-    (void)hipFree(dsl); (void)hipFree(dout); (void)hipFree(dfl); (void)hipFree(dws); (void)hipFree(dst);
-#undef EA_TRY
-    if (rc) return rc;
-    return herr(e);
-}
-
-int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
-                     int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
-                     int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
-                     uint8_t* flags, int64_t* stats) {
-    try {
-        return attention_csr_impl(q, rows, d, k, v, nkeys, dv, alpha, row_ptr, key_idx, fp32_out, acc_bits, tile,
-                                  splits, order_seed, nthreads, out, flags, stats);
-    } catch (...) {  // host vectors: only an exhausted heap throws (device memory is freed by then)
-        return EA_ERR_HOST_MEMORY;
-    }
-}
-
 int ea_hip_kv_append(uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, int64_t row_elems, const uint16_t* k_new,
                      const uint16_t* v_new, const int64_t* dst_rows, int64_t n, int32_t* block_table,
                      int64_t block_table_entries, const int64_t* bt_pos, const int32_t* bt_val, int64_t n_bt,

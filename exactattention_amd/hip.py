@@ -84,6 +84,8 @@ def load():
                                          ctypes.c_float, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_uint64, ctypes.c_int, P, P, P]
         lib.ea_attention_hip.restype = ctypes.c_int
+        lib.ea_csr_layout.argtypes = [ctypes.c_int64, P, P, ctypes.c_int64, P, P, P, P, P, P]
+        lib.ea_csr_layout.restype = ctypes.c_int
         lib.ea_round_ratio.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)]
         lib.ea_round_ratio.restype = ctypes.c_float
         lib.ea_hip_exact_rows.argtypes = [ctypes.POINTER(Geometry), ctypes.POINTER(Buffers), ctypes.POINTER(Options),
@@ -158,6 +160,10 @@ class DeviceProblem:
         def t(a, dt=None):
             if a is None:
                 return None
+            if hasattr(a, "data_ptr"):  # a torch tensor: bf16 as its bit pattern, kept where it is on dev
+                if a.dtype == torch.bfloat16:
+                    a = a.view(torch.int16)
+                return a.to(dev).contiguous()
             a = np.ascontiguousarray(a)
             if a.dtype == np.uint16:
                 a = a.view(np.int16)
@@ -310,6 +316,29 @@ def ea_attention_hip(q, k, v, alpha, row_ptr, key_idx, out="bf16", splits=8, acc
                               acc_bits, tile, splits, 0, 1, res.ctypes.data, flags.ctypes.data, st.ctypes.data)
     _check(rc, "ea_attention_hip")
     return res, flags, st
+
+
+def csr_layout(row_ptr, key_idx, nkeys: int, arrays: bool = False) -> dict:
+    """The serving geometry ea_attention_hip gives a CSR problem (ea_csr_layout): sequences
+    (key-list families), tokens per sequence, page size, longest list; with arrays=True also the
+    token -> row map (-1 padding), visible lengths, sequence lengths, block-table offsets and the
+    block table. Host only."""
+    lib = load()
+    rp = np.ascontiguousarray(row_ptr, dtype=np.int64)
+    ki = np.ascontiguousarray(key_idx, dtype=np.int64)
+    dims = np.zeros(6, np.int64)
+    kp = ki.ctypes.data if ki.size else None
+    _check(lib.ea_csr_layout(rp.shape[0] - 1, rp.ctypes.data, kp, int(nkeys), dims.ctypes.data,
+                             None, None, None, None, None), "ea_csr_layout")
+    B, T, Pg, maxlen, nbt, BT = (int(x) for x in dims)
+    lay = dict(num_seqs=B, num_tokens=T, page_size=Pg, max_seq_len=maxlen)
+    if arrays:
+        lay.update(tok_row=np.zeros(BT, np.int64), kv_len=np.zeros(BT, np.int32), seq_len=np.zeros(B, np.int32),
+                   bt_off=np.zeros(B, np.int64), block_table=np.zeros(max(nbt, 1), np.int32))
+        _check(lib.ea_csr_layout(rp.shape[0] - 1, rp.ctypes.data, kp, int(nkeys), dims.ctypes.data,
+                                 lay["tok_row"].ctypes.data, lay["kv_len"].ctypes.data, lay["seq_len"].ctypes.data,
+                                 lay["bt_off"].ctypes.data, lay["block_table"].ctypes.data), "ea_csr_layout")
+    return lay
 
 
 def exact_row(q, k, v, alpha_bits: int, out: str = "bf16", trace: bool = False):

@@ -78,24 +78,34 @@ def paged(q, k_pages, v_pages, block_table, kv_len, seq_len, layout="NHD", tree_
                 out_shape=(B, T, Hq, dv))
 
 
-def csr(q, k, v, row_ptr, key_idx):
-    """The reference CPU ABI's form (csrc/exact_attention_cpu.cpp:585-588): q (R, d), k (n, d),
-    v (n, dv), row r attends key_idx[row_ptr[r]:row_ptr[r+1]]. Each row becomes a sequence whose
-    page table is its key list (page size 1)."""
+def csr(q, k, v, layout: dict) -> dict:
+    """The reference CPU ABI's form (csrc/exact_attention_cpu.cpp:585-588: q (R, d), k (n, d),
+    v (n, dv), row r attends key_idx[row_ptr[r]:row_ptr[r+1]]) as the serving geometry the
+    library's ea_csr_layout gives it (`layout` from hip.csr_layout(..., arrays=True)): each
+    key-list family is a sequence whose tokens are its rows and whose pages are runs of
+    `page_size` keys of k and v. Token i of the flattened (B, T) grid is CSR row
+    layout["tok_row"][i] (-1: padding, kv_len 0)."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
-    R, d = q.shape
-    dv = v.shape[1]
-    row_ptr = np.asarray(row_ptr, dtype=np.int64)
-    lens = (row_ptr[1:] - row_ptr[:-1]).astype(np.int32)
-    bt = np.ascontiguousarray(np.asarray(key_idx, dtype=np.int32).reshape(-1))
-    if bt.size == 0:
-        bt = np.zeros(1, np.int32)
-    g = _geom(R, 1, 1, 1, d, dv, (d, 0, 0), (dv, 0, 0), (d, 0, 0), (dv, 0, 0), 1, 0, int(lens.max(initial=0)))
-    return dict(geom=g, q=q.reshape(R, 1, 1, d), k=k, v=v, seq_len=lens, kv_len=lens.copy(), block_table=bt,
-                block_table_offset=np.ascontiguousarray(row_ptr[:-1]), tree_mask=None, tree_base=None,
-                out_shape=(R, 1, 1, dv))
+    d, dv = q.shape[1], v.shape[1]
+    B, T, P = layout["num_seqs"], layout["num_tokens"], layout["page_size"]
+    tok = layout["tok_row"]
+    qg = np.zeros((B * T, d), np.uint16)
+    qg[tok >= 0] = q[tok[tok >= 0]]
+    n = k.shape[0]
+    npages = max(1, -(-n // P))
+    kp = np.zeros((npages * P, d), np.uint16)
+    vp = np.zeros((npages * P, dv), np.uint16)
+    kp[:n], vp[:n] = k, v
+    g = _geom(B, T, 1, 1, d, dv, (T * d, d, 0), (T * dv, dv, 0), (P * d, d, 0), (P * dv, dv, 0), P, 0,
+              layout["max_seq_len"])
+    return dict(geom=g, q=qg.reshape(B, T, 1, d), k=kp.reshape(npages, P, 1, d), v=vp.reshape(npages, P, 1, dv),
+                seq_len=np.ascontiguousarray(layout["seq_len"], dtype=np.int32),
+                kv_len=np.ascontiguousarray(layout["kv_len"], dtype=np.int32),
+                block_table=np.ascontiguousarray(layout["block_table"], dtype=np.int32),
+                block_table_offset=np.ascontiguousarray(layout["bt_off"], dtype=np.int64),
+                tree_mask=None, tree_base=None, out_shape=(B, T, 1, dv))
 
 
 def to_paged(prob: dict, page_size: int, rng: np.random.Generator, layout: str = "NHD", extra_pages: int = 3) -> dict:

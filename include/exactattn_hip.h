@@ -202,11 +202,26 @@ int ea_exact_row(const uint16_t* q, int d, const uint16_t* k, const uint16_t* v,
  * `nthreads` are validated and otherwise ignored (they cannot change certified bits); `splits` is
  * the KV split count. stats[0..2] += tier-1 score, weight and final-rounding fallbacks, as in the
  * reference. Rows the device tiers leave uncertified are recomputed exactly by the host exact
- * tier, so flags are 0, or 2 for rows that see a NaN/inf (their output is +0). */
+ * tier, so flags are 0, or 2 for rows that see a NaN/inf (their output is +0).
+ * Rows whose key lists are prefixes of one list form one sequence of a serving geometry (its
+ * cache the caller's K/V viewed as pages of the largest power-of-two run length up to 64 that
+ * every list keeps aligned), so the decode and int8 prefill kernels take them and read each
+ * shared key once (ea_csr_layout reports the grouping). Device buffers come from a per-device
+ * arena kept across calls, on a library stream; calls on one device are serialised. */
 int ea_attention_hip(const uint16_t* q, int64_t rows, int d, const uint16_t* k, const uint16_t* v, int64_t nkeys,
                      int dv, float alpha, const int64_t* row_ptr, const int64_t* key_idx, int fp32_out,
                      int acc_bits, int tile, int splits, uint64_t order_seed, int nthreads, void* out,
                      uint8_t* flags, int64_t* stats);
+
+/* The geometry ea_attention_hip gives a CSR problem (rows with no key are not in it: they are +0).
+ * dims[0..5] = sequences B (key-list families, each cut to at most T rows), tokens per sequence T,
+ * page size P, longest list, block-table entries, B*T. With the optional arrays set, also per
+ * token the CSR row (-1 for padding) and visible length, per sequence its length and block-table
+ * offset, and the block table (page n holds keys n*P .. n*P + P - 1 of the caller's arrays).
+ * Host only. Returns 0, -1 on bad arguments, -5 when the host heap is exhausted. No reference
+ * counterpart. */
+int ea_csr_layout(int64_t rows, const int64_t* row_ptr, const int64_t* key_idx, int64_t nkeys, int64_t* dims,
+                  int64_t* tok_row, int32_t* kv_len, int32_t* seq_len, int64_t* bt_off, int32_t* bt);
 
 /* The reference's test hook (csrc/exact_attention_cpu.cpp:630-638), same signature and result:
  * RN-even of (a / b) * 2^E, a and b as 128-bit (hi, lo) halves, into fp32 (fp32 = 1) or bf16,

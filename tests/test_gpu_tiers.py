@@ -283,6 +283,76 @@ def test_drop_in_with_the_reference_binding(gpu):
         assert np.array_equal(res, want), fp32
 
 
+def _ref_bound_dropin():
+    from exactattention_amd import hip
+    lib = ctypes.CDLL(hip.LIB_PATH)
+    P = ctypes.c_void_p
+    lib.ea_attention_hip.argtypes = [P, ctypes.c_int64, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int,
+                                     ctypes.c_float, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_uint64, ctypes.c_int, P, P, P]
+    lib.ea_attention_hip.restype = ctypes.c_int
+
+    def call(Q, K, V, ab, row_ptr, key_idx, splits=8):
+        R, d = Q.shape
+        dv = V.shape[1]
+        res = np.full((R, dv), 0x5A5A, np.uint16)
+        flags = np.full(R, 9, np.uint8)
+        st = np.zeros(3, np.int64)
+        alpha = float(np.array([ab], np.uint32).view(np.float32)[0])
+        rc = lib.ea_attention_hip(Q.ctypes.data, R, d, K.ctypes.data, V.ctypes.data, K.shape[0], dv,
+                                  ctypes.c_float(alpha), row_ptr.ctypes.data, key_idx.ctypes.data, 0, 64, 64, splits,
+                                  0, 8, res.ctypes.data, flags.ctypes.data, st.ctypes.data)
+        assert rc == 0
+        return res, flags
+    return call
+
+
+def _gqa_decode_csr(rng, B, Hkv, grp, S, lens):
+    """A GQA decode batch in the reference's CSR form (cpu_baseline's layout): K/V rows of
+    (sequence, KV head) s at s * S .. s * S + len - 1; rows (b, query head)."""
+    d = 128
+    q = bf16(rng, (B * Hkv * grp, d))
+    K = bf16(rng, (B * Hkv * S, d), "outlier")
+    V = bf16(rng, (B * Hkv * S, d))
+    seg = (np.arange(B)[:, None] * Hkv + np.arange(Hkv * grp)[None, :] // grp).reshape(-1)
+    L = np.repeat(lens, Hkv * grp)
+    row_ptr = np.concatenate([[0], np.cumsum(L)]).astype(np.int64)
+    key_idx = np.concatenate([s * S + np.arange(l) for s, l in zip(seg, L)]).astype(np.int64)
+    return q, K, V, row_ptr, key_idx
+
+
+def test_csr_families_take_the_tuned_kernels(gpu):
+    """CSR rows grouped into key-list families run on the decode kernel (a GQA decode batch) and
+    on the int8 prefill kernel (a causal prefix over GQA 2), through attention_problem on the
+    layout ea_attention_hip uses: bits equal the oracle's row by row, and the stats name the
+    kernel. The C drop-in gives the same bits on both, called twice (larger, then smaller: its
+    device arena is reused)."""
+    from exactattention_amd import hip
+    from oracle import oracle
+    rng = np.random.default_rng(42)
+    ab = default_alpha_bits(128)
+    dropin = _ref_bound_dropin()
+    q, K, V, row_ptr, key_idx = _gqa_decode_csr(rng, 5, 4, 2, 700, rng.integers(1, 701, size=5))
+    T = 150
+    qc = bf16(rng, (2 * T, 128))
+    Kc, Vc = bf16(rng, (T, 128), "wide"), bf16(rng, (T, 128))
+    rows = [np.arange(t + 1) for t in range(T) for _ in range(2)]
+    rp_c = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+    ki_c = np.concatenate(rows).astype(np.int64)
+    for (Q, Kx, Vx, rp, ki), kernel_stat in (((q, K, V, row_ptr, key_idx), "decode_kernel_rows"),
+                                              ((qc, Kc, Vc, rp_c, ki_c), "prefill_kernel_rows")):
+        want, _ = oracle.attention_csr(Q, Kx, Vx, ab, rp, ki)
+        lay = hip.csr_layout(rp, ki, Kx.shape[0], arrays=True)
+        got, flags, st = _run(problem.csr(Q, Kx, Vx, lay), ab)
+        assert st[kernel_stat] > 0, st
+        tok = lay["tok_row"]
+        g = np.zeros_like(want)
+        g[tok[tok >= 0]] = got.reshape(-1, 128)[tok >= 0]
+        assert not flags.any() and np.array_equal(g, want), kernel_stat
+        res, fl = dropin(Q, Kx, Vx, ab, rp, ki)
+        assert not fl.any() and np.array_equal(res, want), kernel_stat
+
+
 def test_fixture_harness_check(gpu, capsys):
     """`python -m exactattention_amd.fixture check --backend hip:rocm`: the reference's published
     SHA-256 of both Qwen3 heads, every causal row, through attention_hip; exit code 0."""

@@ -300,3 +300,82 @@ def test_trace_row_reads_alpha_as_a_value():
     tiny = exact.attention_row(q, k, v, 1)
     assert np.array_equal(ea.trace_row(q, k, v, alpha_bits=1).out, tiny)
     assert not np.array_equal(tiny, want)
+
+
+def _layout_keys(lay, i):
+    """Keys token i of the CSR layout sees: its sequence's pages, first kv_len keys."""
+    T, P = lay["num_tokens"], lay["page_size"]
+    b = i // T
+    L = int(lay["kv_len"][i])
+    pos = np.arange(L)
+    return lay["block_table"][lay["bt_off"][b] + pos // P].astype(np.int64) * P + pos % P
+
+
+def _check_layout(row_ptr, key_idx, nkeys):
+    from exactattention_amd import hip
+    lay = hip.csr_layout(row_ptr, key_idx, nkeys, arrays=True)
+    R = len(row_ptr) - 1
+    tok = lay["tok_row"]
+    B, T = lay["num_seqs"], lay["num_tokens"]
+    assert tok.shape == (B * T,)
+    lens = np.diff(row_ptr)
+    # every non-empty row appears exactly once, and its token sees exactly its key list
+    real = tok[tok >= 0]
+    assert sorted(real.tolist()) == [r for r in range(R) if lens[r] > 0]
+    for i in np.flatnonzero(tok >= 0):
+        r = tok[i]
+        assert np.array_equal(_layout_keys(lay, i), key_idx[row_ptr[r]:row_ptr[r + 1]]), (i, r)
+        assert lay["kv_len"][i] <= lay["seq_len"][i // T] <= lay["max_seq_len"]
+    assert not lay["kv_len"][tok < 0].any()
+    # the pages hold whole aligned runs of the caller's keys
+    assert lay["page_size"] in (1, 2, 4, 8, 16, 32, 64)
+    return lay
+
+
+def test_csr_layout_groups_rows_into_key_list_families():
+    """ea_csr_layout (the drop-in's grouping): decode rows of a GQA batch pair up per KV head,
+    a causal prefix becomes one sequence with pages of 64, arbitrary lists keep page size 1; every
+    row's token sees exactly its own key list through the block table."""
+    _lib()
+    # C2-like decode in CSR form: B=3 sequences x 2 KV heads x 2 query heads, 320 keys each
+    B, Hkv, grp, S = 3, 2, 2, 320
+    seg = (np.arange(B)[:, None] * Hkv + np.arange(Hkv * grp)[None, :] // grp).reshape(-1)
+    lens = np.array([320, 320, 320, 320, 100, 100, 100, 100, 5, 5, 5, 5])
+    row_ptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    key_idx = np.concatenate([s * S + np.arange(l) for s, l in zip(seg, lens)]).astype(np.int64)
+    lay = _check_layout(row_ptr, key_idx, B * Hkv * S)
+    assert (lay["num_seqs"], lay["num_tokens"], lay["page_size"]) == (6, 2, 64)
+    # causal prefill of 200 tokens over two heads sharing one key range (GQA 2)
+    T = 200
+    rows = [np.arange(t + 1) for t in range(T) for _ in range(2)]
+    row_ptr = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+    lay = _check_layout(row_ptr, np.concatenate(rows).astype(np.int64), T)
+    assert (lay["num_seqs"], lay["num_tokens"], lay["page_size"], lay["max_seq_len"]) == (1, 2 * T, 64, T)
+    # random lists (repeats, any order) and empty rows: one family per row, page size 1
+    rng = np.random.default_rng(11)
+    lens = rng.integers(0, 40, size=30)
+    row_ptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    key_idx = rng.integers(0, 500, size=int(lens.sum())).astype(np.int64)
+    lay = _check_layout(row_ptr, key_idx, 500)
+    assert lay["page_size"] == 1
+    # prefix families of mixed sizes: padding stays within a quarter of the rows (plus 64)
+    rows = []
+    for f in range(12):
+        base = 1000 * f + np.arange(int(rng.integers(50, 300)))
+        for _ in range(int(rng.integers(1, 40))):
+            rows.append(base[:int(rng.integers(1, len(base) + 1))])
+    row_ptr = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+    lay = _check_layout(row_ptr, np.concatenate(rows).astype(np.int64), 12000)
+    assert lay["num_seqs"] * lay["num_tokens"] <= len(rows) * 5 // 4 + 64
+    assert lay["page_size"] == 8  # families start at multiples of 1000 = 8 x 125
+
+
+def test_csr_layout_rejects_bad_lists():
+    from exactattention_amd import hip
+    _lib()
+    with pytest.raises(ValueError):
+        hip.csr_layout(np.array([0, 3]), np.array([0, 1, 7]), 5)       # key past nkeys
+    with pytest.raises(ValueError):
+        hip.csr_layout(np.array([0, 2, 1]), np.array([0, 1]), 5)       # decreasing row_ptr
+    lay = hip.csr_layout(np.array([0, 0, 0]), np.zeros(0, np.int64), 5, arrays=True)
+    assert lay["num_seqs"] == 0
