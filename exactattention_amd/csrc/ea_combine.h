@@ -17,14 +17,23 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
     const int seg = (int)(b * P.g.num_kv_heads + hk);
     const int lr = t * P.grp + gi;
     const int rbk = lr / P.rb;
-    const int ns = P.nsplit;
+    // partials to merge: every split, or with the decode kernel's equal-share plan the pieces of
+    // this row's unit (slots 0 .. npieces - 1; none for a unit without keys). The error bounds
+    // below count nsb = nsplit merged terms either way (at least the number merged).
+    const int nsb = P.nsplit;
+    int ns = nsb;
+    if (P.dq_stream) {
+        const int u = seg * P.nrb + rbk, share = P.dq_plan[1];
+        const int su = P.dq_plan[2 + u], tu = P.dq_plan[3 + u] - su;
+        ns = tu > 0 ? (su + tu - 1) / share - su / share + 1 : 0;
+    }
     const int J = (ns + 63) / 64;  // slabs of 64 splits: split 64 j + lane is this lane's in slab j
 
     // slab 0 may follow the caller's merge order: lane i holds split merge_order[i] when it is a
     // permutation of [0, ns) (ns <= 64); the sums below come from wave reductions, and any
     // summation order gives the same certified bits, so the order fixes only which lane loads what
     int si = lane;
-    bool mo_ok = P.merge_order != nullptr && ns <= 64;
+    bool mo_ok = P.merge_order != nullptr && ns <= 64 && !P.dq_stream;
     if (mo_ok) {
         const int m = lane < ns ? P.merge_order[lane] : 0;
         const uint64_t bit = (lane < ns && m >= 0 && m < ns) ? (1ull << m) : 0ull;
@@ -101,7 +110,7 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
         far |= (n > 0 && dsh < -900) ? 1 : 0;
         const double zs = n > 0 ? ldexp(z, max(dsh, -1000)) : 0.0;
         Z += zs;
-        A += zs * (double)(n + ns + 4);
+        A += zs * (double)(n + nsb + 4);
         nterm += n > 0 ? n : 0;
     };
     add_z(n0, r0, z0);
@@ -118,7 +127,7 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
         A += __shfl_xor(A, o, 64);
         nterm += __shfl_xor(nterm, o, 64);
     }
-    const double tiny = (double)(nterm + 64 * ns + 64) * 0x1p-1074;
+    const double tiny = (double)(nterm + 64 * nsb + 64) * 0x1p-1074;
     const double eZ = A * up + tiny;
     if (!(Z > 2.0 * eZ) || !isfinite(Z)) flag = 1;
     bool ok = !flag;

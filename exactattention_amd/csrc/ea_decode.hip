@@ -63,27 +63,34 @@ __device__ __forceinline__ float absf(float x) { return __builtin_fabsf(x); }
 
 }  // namespace
 
-template <int RB, int PGL>
-__global__ void __launch_bounds__(128) ea_decode(Params P) {
+template <int RB, int PGL, bool STREAM>
+__device__ __forceinline__ void decode_body(Params P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     DecodeSmem<RB>& S = *reinterpret_cast<DecodeSmem<RB>*>(smem_raw);
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, c8 = lane & 15;
-
-    const int item = blockIdx.x;
-    const int seg = item / P.nrb, rbk = item % P.nrb;
-    const int split = blockIdx.y;
-    const int Hkv = P.g.num_kv_heads;
-    const int b = seg / Hkv;
-    const int hk = seg % Hkv;
-    const int row0 = rbk * P.rb;
-    const int nrow = min(RB, P.r_seg - row0);
 
     for (int i = threadIdx.x; i < 256; i += blockDim.x) {
         S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
         S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
     }
+    // the decode kernel takes every row of the problem: one add for the whole grid
+    if constexpr (STREAM)
+        if (threadIdx.x == 0 && P.stats && blockIdx.x == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
 
+    // One piece: keys [kA, kB) of unit `item` (segment, row block), clipped to the unit's visible
+    // end, as partial slot `split`.
+    auto piece = [&](const int item, const int split, const int kA, const int kB) __attribute__((always_inline)) {
+    // lane-derived values are recomputed from an opaque copy of the lane index in every piece, so
+    // that none of them is hoisted out of the piece loop and kept live across it
+    int lane_ = (int)(threadIdx.x & 63);
+    if constexpr (STREAM) asm volatile("" : "+v"(lane_));
+    const int lane = lane_;
+    const int g = lane >> 4, c8 = lane & 15;
+    const int seg = item / P.nrb, rbk = item % P.nrb;
+    const int Hkv = P.g.num_kv_heads;
+    const int b = seg / Hkv;
+    const int hk = seg % Hkv;
+    const int row0 = rbk * P.rb;
+    const int nrow = min(RB, P.r_seg - row0);
     cint_t* kvl4 = (cint_t*)P.kv_len;
     cint_t* qinfo4 = (cint_t*)P.qinfo;
     cdouble_t* qn4 = (cdouble_t*)P.qn;
@@ -111,8 +118,8 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
     }
     const int slen = ((cint_t*)P.seq_len)[b];
     if (kend > slen) kend = slen;
-    const int k0 = split * P.split_len;
-    const int k1 = min(k0 + P.split_len, kend);
+    const int k0 = kA;
+    const int k1 = min(kB, kend);
     const int64_t pbase = (int64_t)split * P.rows;
     cint_t* btb = (cint_t*)P.bt + (P.bt ? (P.bt_off ? P.bt_off[b] : (int64_t)b * P.g.block_table_stride) : 0);
     const int pshift = P.pshift;
@@ -412,8 +419,9 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
                 }
             __syncthreads();  // weights of tile it published; wave B is done with tile it - 1
         }
-        // the decode kernel takes every row of the problem: one add for the whole grid
-        if (lane == 0 && P.stats && item == 0 && split == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
+        if constexpr (!STREAM)
+            if (lane == 0 && P.stats && item == 0 && split == 0)
+                atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
         publish_rows(0, RA);
     } else {
         // ============ wave B: V tiles (double-buffered in VGPRs) and the P.V sums
@@ -559,24 +567,84 @@ __global__ void __launch_bounds__(128) ea_decode(Params P) {
             P.pV[(((int64_t)split * P.nseg + seg) * P.nrb + rbk) * 128 + c] = m;
         }
     }
+    };
+
+    if constexpr (!STREAM) {
+        // uniform splits: block (unit, split) takes keys [split split_len, (split + 1) split_len)
+        const int k0 = (int)blockIdx.y * P.split_len;
+        piece((int)blockIdx.x, (int)blockIdx.y, k0, k0 + P.split_len);
+        return;
+    }
+    // Block g's share of the step's tiles (the plan the prep kernel's planner block wrote): its
+    // intersections with the units, in unit order, one piece each. The first comes from the
+    // block's record (unit, S_u, S_(u+1), share) in one load.
+    const int4 rec = ((const int4*)(P.dq_plan + P.dq_rec_off))[blockIdx.x];
+    const int W = P.dq_plan[0];
+    const int gb = blockIdx.x;
+    int u = rec.x;
+    const int share = rec.w;
+    if (u >= P.dq_units || share <= 0) return;  // past the last share: no tile
+    int start = gb * share;  // < W < 2^30
+    const int end = min(start + share, W);
+    {
+        // the first piece, straight-line: a share inside one unit, the usual case, ends here
+        const int su = rec.y, eu = rec.z;
+        const int slot = gb - su / share;  // < nsplit: share >= dq_min_share
+        if (slot < P.nsplit) piece(u, slot, (start - su) * DT, (min(end, eu) - su) * DT);
+        start = min(end, eu);
+        ++u;
+    }
+    // a share that crosses unit boundaries: one piece per further unit it reaches
+    const int32_t* Su = P.dq_plan + 2;
+    while (start < end && u < P.dq_units) {
+        const int su = Su[u], eu = Su[u + 1];
+        if (eu > start) {
+            const int slot = gb - su / share;
+            __syncthreads();  // the previous piece's LDS reads (K buffers, epilogue) are done
+            if (slot < P.nsplit) piece(u, slot, (start - su) * DT, (min(end, eu) - su) * DT);
+            start = min(end, eu);
+        }
+        ++u;
+    }
 }
 
 // Launches the decode kernel when the geometry allows it; returns 1 if launched, 0 if the caller
 // must use the general split kernel, or a negative HIP error code.
 namespace {
-template <int RB>
+// Uniform splits: one block per (unit, split). Two waves per SIMD for the 1- and 2-row blocks.
+template <int RB, int PGL>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(RB < 4 ? 2 : 1, 2))) ea_decode(Params P) {
+    decode_body<RB, PGL, false>(P);
+}
+
+// The equal-share plan: one block per share, one piece per unit the share reaches. The piece
+// loop adds a few live registers; two waves per SIMD are kept for the 1- and 2-row blocks (the
+// rare exact paths then reload a few values from scratch).
+template <int RB, int PGL>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(RB < 4 ? 2 : 1, 2)))
+ea_decode_stream(Params P) {
+    decode_body<RB, PGL, true>(P);
+}
+
+template <int RB, bool ST>
 const void* decode_fn(int pgl) {
-    if (pgl == 4) return (const void*)ea_decode<RB, 4>;
-    if (pgl == 16) return (const void*)ea_decode<RB, 16>;
-    return (const void*)ea_decode<RB, 64>;
+    if constexpr (ST) {
+        if (pgl == 4) return (const void*)ea_decode_stream<RB, 4>;
+        if (pgl == 16) return (const void*)ea_decode_stream<RB, 16>;
+        return (const void*)ea_decode_stream<RB, 64>;
+    } else {
+        if (pgl == 4) return (const void*)ea_decode<RB, 4>;
+        if (pgl == 16) return (const void*)ea_decode<RB, 16>;
+        return (const void*)ea_decode<RB, 64>;
+    }
 }
 }  // namespace
 
-int ea::ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st) {
+int ea::ea_decode_eligible(const Params& P) {
     const ea_geometry& g = P.g;
     if (g.head_dim != 128 || g.head_dim_v != 128) return 0;
     if (P.bt && P.pshift < 2) return 0;
-    if (rb != 1 && rb != 2 && rb != 4) return 0;
+    if (P.rb != 1 && P.rb != 2 && P.rb != 4) return 0;
     // 16-byte alignment of every K/V row start (dwordx4 loads)
     if (((uintptr_t)P.k | (uintptr_t)P.v) & 15) return 0;
     if ((g.k_page_stride | g.k_slot_stride | g.k_head_stride | g.v_page_stride | g.v_slot_stride | g.v_head_stride) & 7)
@@ -586,28 +654,68 @@ int ea::ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st) {
     const int64_t slots = P.bt ? ((int64_t)1 << P.pshift) : (int64_t)g.max_seq_len + 64;
     if (P.rows >= lim || (int64_t)g.max_seq_len + 64 >= lim) return 0;
     if (slots * 2 * g.k_slot_stride >= lim || slots * 2 * g.v_slot_stride >= lim) return 0;
-    // page lookups every PGL keys, PGL <= page size (one lookup per 64-key tile without a table)
+    return 1;
+}
+
+namespace {
+// page lookups every PGL keys, PGL <= page size (one lookup per 64-key tile without a table)
+const void* decode_fn_for(const Params& P, bool stream) {
     const int pgl = !P.bt ? 64 : (P.pshift >= 6 ? 64 : (P.pshift >= 4 ? 16 : 4));
-    const void* fn = rb == 1 ? decode_fn<1>(pgl) : (rb == 2 ? decode_fn<2>(pgl) : decode_fn<4>(pgl));
-    static std::mutex mu;
-    static bool attr_done = false;
+    if (stream) return P.rb == 1 ? decode_fn<1, true>(pgl) : (P.rb == 2 ? decode_fn<2, true>(pgl) : decode_fn<4, true>(pgl));
+    return P.rb == 1 ? decode_fn<1, false>(pgl) : (P.rb == 2 ? decode_fn<2, false>(pgl) : decode_fn<4, false>(pgl));
+}
+size_t decode_lds(int rb) {
+    return rb == 1 ? sizeof(DecodeSmem<1>) : (rb == 2 ? sizeof(DecodeSmem<2>) : sizeof(DecodeSmem<4>));
+}
+hipError_t decode_attrs() {
+    static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
-    {
-        std::lock_guard<std::mutex> lk(mu);
-        if (!attr_done) {
-            const void* fns[9] = {decode_fn<1>(4), decode_fn<1>(16), decode_fn<1>(64), decode_fn<2>(4), decode_fn<2>(16),
-                                  decode_fn<2>(64), decode_fn<4>(4), decode_fn<4>(16), decode_fn<4>(64)};
-            for (const void* f : fns) {
-                hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem<4>));
-                if (e != hipSuccess) attr_err = e;
-            }
-            attr_done = true;
+    std::call_once(once, [] {
+        const void* fns[18] = {decode_fn<1, false>(4), decode_fn<1, false>(16), decode_fn<1, false>(64),
+                               decode_fn<2, false>(4), decode_fn<2, false>(16), decode_fn<2, false>(64),
+                               decode_fn<4, false>(4), decode_fn<4, false>(16), decode_fn<4, false>(64),
+                               decode_fn<1, true>(4),  decode_fn<1, true>(16),  decode_fn<1, true>(64),
+                               decode_fn<2, true>(4),  decode_fn<2, true>(16),  decode_fn<2, true>(64),
+                               decode_fn<4, true>(4),  decode_fn<4, true>(16),  decode_fn<4, true>(64)};
+        for (const void* f : fns) {
+            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem<4>));
+            if (e != hipSuccess) attr_err = e;
         }
+    });
+    return attr_err;
+}
+}  // namespace
+
+int ea::ea_decode_slots(const Params& P, int* slots) {
+    // blocks of the decode kernel resident on the current device at once (CUs x blocks per CU),
+    // cached per device and row-block size
+    static std::mutex mu;
+    static int cache[64][3] = {};
+    hipError_t e = decode_attrs();
+    if (e != hipSuccess) return -100 - (int)e;
+    int dev = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return -100 - (int)e;
+    const int ri = P.rb == 1 ? 0 : (P.rb == 2 ? 1 : 2);
+    std::lock_guard<std::mutex> lk(mu);
+    if (dev < 0 || dev >= 64) return -1;
+    if (!cache[dev][ri]) {
+        int cus = 0, per = 0;
+        if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return -100 - (int)e;
+        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, decode_fn_for(P, true), 128, decode_lds(P.rb))) !=
+            hipSuccess)
+            return -100 - (int)e;
+        cache[dev][ri] = (cus > 0 ? cus : 1) * (per > 0 ? per : 1);
     }
-    if (attr_err != hipSuccess) return -100 - (int)attr_err;
+    *slots = cache[dev][ri];
+    return 0;
+}
+
+int ea::ea_launch_decode(const Params& P, hipStream_t st) {
+    hipError_t e = decode_attrs();
+    if (e != hipSuccess) return -100 - (int)e;
     Params Pc = P;
     void* args[] = {&Pc};
-    const size_t lds = rb == 1 ? sizeof(DecodeSmem<1>) : (rb == 2 ? sizeof(DecodeSmem<2>) : sizeof(DecodeSmem<4>));
-    hipError_t e = hipLaunchKernel(fn, grid, dim3(128), args, lds, st);
-    return e == hipSuccess ? 1 : -100 - (int)e;
+    const dim3 grid = P.dq_stream ? dim3((unsigned)P.dq_blocks) : dim3((unsigned)(P.nseg * P.nrb), (unsigned)P.nsplit);
+    e = hipLaunchKernel(decode_fn_for(P, P.dq_stream != 0), grid, dim3(128), args, decode_lds(P.rb), st);
+    return e == hipSuccess ? 0 : -100 - (int)e;
 }

@@ -34,8 +34,63 @@ using namespace ea;
 // (FQmin' = max(field, 1): a subnormal's lsb is that of field 1), 0x80000000 for an all-zero block;
 // qinfo[row*5 + 4] = 1 when the row holds a NaN/inf.
 // ------------------------------------------------------------------------------------------------
+// The decode kernel's equal-share plan (Params::dq_*), by one 256-thread block: per unit its tile
+// count (up to unit_kend, at most dq_max_tiles), the exclusive prefix sums S_u with S_units = W, the
+// share max(ceil(W / dq_blocks), dq_min_share), and per block g its first piece as one record
+// (unit u, S_u, S_(u+1), share): the unit holding tile g share is the u with
+// S_u <= g share < S_(u+1), so the blocks g in [ceil(S_u / share), ceil(S_(u+1) / share)) start in
+// unit u and each is written by that unit's thread. Blocks past W get u = units. Every entry the
+// decode kernel and the combine read is written here.
+__device__ void dq_plan_block(const Params& P) {
+    __shared__ int s_scan[2][256];
+    __shared__ int s_share;
+    const int tid = threadIdx.x, U = P.dq_units, G = P.dq_blocks;
+    int32_t* plan = P.dq_plan;
+    int32_t* Su = plan + 2;
+    int4* brec = (int4*)(plan + P.dq_rec_off);
+    const int per = (U + 255) / 256;
+    const int u0 = min(tid * per, U), u1 = min(u0 + per, U);
+    auto tiles = [&](int u) { return min((unit_kend(P, u / P.nrb, u % P.nrb) + 63) >> 6, P.dq_max_tiles); };
+    int sum = 0;
+    for (int u = u0; u < u1; ++u) sum += tiles(u);
+    // inclusive scan of the 256 chunk sums (Hillis-Steele, ping-pong)
+    int cur = 0;
+    s_scan[0][tid] = sum;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+        const int x = s_scan[cur][tid] + (tid >= o ? s_scan[cur][tid - o] : 0);
+        s_scan[cur ^ 1][tid] = x;
+        cur ^= 1;
+        __syncthreads();
+    }
+    const int W = s_scan[cur][255];
+    if (tid == 0) {
+        const int share = max(max((W + G - 1) / G, P.dq_min_share), 1);
+        s_share = share;
+        plan[0] = W;
+        plan[1] = share;
+        Su[U] = W;
+    }
+    __syncthreads();
+    const int share = s_share;
+    int run = s_scan[cur][tid] - sum;  // exclusive prefix of this thread's chunk
+    for (int u = u0; u < u1; ++u) {
+        const int t = tiles(u);
+        Su[u] = run;
+        for (int g = (run + share - 1) / share; g * share < run + t && g < G; ++g)
+            brec[g] = make_int4(u, run, run + t, share);
+        run += t;
+    }
+    const int nb = (W + share - 1) / share;  // blocks with a share: [0, nb)
+    for (int g = nb + tid; g < G; g += 256) brec[g] = make_int4(U, W, W, share);
+}
+
 __global__ void __launch_bounds__(256) ea_prep(Params P) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *P.wl_cnt = 0;
+    if (P.dq_stream && blockIdx.x == gridDim.x - 1) {
+        dq_plan_block(P);  // the extra last block
+        return;
+    }
     int lane = threadIdx.x & 63;
     int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= P.rows) return;
@@ -1073,10 +1128,17 @@ struct Plan {
     int nsplit, split_len, rb, nrb, r_seg, grp, nseg, pshift, dlog;
     int64_t rows;
     size_t off_q64, off_qinfo, off_qn, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
-    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr, off_pfpart;
+    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr, off_pfpart, off_dq;
     int t2_keys;
     int prefill, pf_ntiles, pf_nrb, pf_nsplit, pf_tps;
+    // the decode kernel's equal-share decomposition (Params::dq_*): dq = 1 when the geometry may
+    // take it (the pointer checks come at launch); nsplit_gen = the general kernel's uniform split
+    // count, nsplit = nsplit_gen + 1 partial slots per unit for the decode kernel's pieces
+    int dq, nsplit_gen, dq_units, dq_min_share, dq_max_tiles, dq_rec_off;
 };
+
+// most blocks the decode kernel's equal-share decomposition launches (the plan array's size)
+#define EA_DQ_MAX_BLOCKS 4096
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1122,6 +1184,20 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->split_len = sl;
     pl->nsplit = (maxlen + sl - 1) / sl;
     if (pl->nsplit < 1) pl->nsplit = 1;
+    pl->nsplit_gen = pl->nsplit;
+    // the d = 128 decode kernel may run this step (ea_launch_decode also checks the pointers):
+    // its pieces need nsplit + 1 partial slots per unit
+    const int64_t max_tiles = ((int64_t)maxlen + 63) / 64;
+    int pf_nt = 0, pf_nr = 0;
+    pl->dq = g->head_dim == 128 && g->head_dim_v == 128 && o->kernel != EA_KERNEL_GENERAL && !o->timers &&
+             !ea_prefill_eligible(*g, pl->grp, o->kernel, &pf_nt, &pf_nr) && pl->rows < ((int64_t)1 << 30) &&
+             (int64_t)maxlen + 64 < ((int64_t)1 << 30) &&
+             (int64_t)pl->nseg * pl->nrb * max_tiles < ((int64_t)1 << 30) &&
+             (int64_t)pl->nseg * pl->nrb < ((int64_t)1 << 24);
+    pl->dq_units = pl->nseg * pl->nrb;
+    pl->dq_max_tiles = (int)max_tiles;
+    pl->dq_min_share = (int)((max_tiles + pl->nsplit_gen - 1) / pl->nsplit_gen);
+    if (pl->dq) pl->nsplit = pl->nsplit_gen + 1;
     int64_t R = pl->rows;
     int dv = g->head_dim_v;
     size_t off = 0;
@@ -1135,6 +1211,9 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->off_pV = off; off = align_up(off + (size_t)pl->nsplit * pl->nseg * pl->nrb * dv * 4);
     pl->off_wl = off; off = align_up(off + (size_t)(R > 0 ? R : 1) * 4);
     pl->off_cnt = off; off = align_up(off + 4);
+    pl->off_dq = off;
+    pl->dq_rec_off = (3 + pl->dq_units + 3) & ~3;  // 16-byte aligned block records after S
+    if (pl->dq) off = align_up(off + (size_t)(pl->dq_rec_off + 4 * EA_DQ_MAX_BLOCKS) * 4);
     pl->t2_keys = maxlen + 64;
     pl->off_t2M = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 4);
     pl->off_t2E = off; off = align_up(off + (size_t)EA_T2_BLOCKS * pl->t2_keys * 8);
@@ -1227,7 +1306,7 @@ int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* byt
     int rc = make_plan(g, o, &pl);
     if (rc) return rc;
     if (bytes) *bytes = pl.total;
-    if (nsplit) *nsplit = pl.nsplit;
+    if (nsplit) *nsplit = pl.prefill ? pl.nsplit : pl.nsplit_gen;  // the decode kernel adds one partial slot
     return 0;
 }
 
@@ -1304,6 +1383,28 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.pf_part = (void*)(ws + pl.off_pfpart);
     hipStream_t st = (hipStream_t)stream;
     unsigned rb4 = (unsigned)((pl.rows + 3) / 4);
+    // the decode kernel with its equal-share plan, or the general kernel with uniform splits
+    P.dq_stream = 0;
+    bool use_decode = false;
+    if (!pl.prefill) {
+        P.nsplit = pl.nsplit_gen;
+        use_decode = pl.dq && pl.nseg > 0 && ea_decode_eligible(P);
+        int slots = 0;
+        if (use_decode && (rc = ea_decode_slots(P, &slots))) return rc;
+        // the equal-share plan when the uniform split grid would take more than one round of
+        // resident blocks (long or ragged contexts); otherwise one block per (unit, split)
+        if (use_decode && (int64_t)pl.dq_units * pl.nsplit_gen > slots) {
+            const int64_t nb = std::min<int64_t>(slots, EA_DQ_MAX_BLOCKS);
+            P.dq_stream = 1;
+            P.nsplit = pl.nsplit;
+            P.dq_units = pl.dq_units;
+            P.dq_blocks = (int32_t)(nb > 0 ? nb : 1);
+            P.dq_min_share = pl.dq_min_share;
+            P.dq_max_tiles = pl.dq_max_tiles;
+            P.dq_rec_off = pl.dq_rec_off;
+            P.dq_plan = (int32_t*)(ws + pl.off_dq);
+        }
+    }
     auto mark = [&](int i) -> int {
         return (o->events && o->events[i]) ? herr(hipEventRecord((hipEvent_t)o->events[i], st)) : 0;
     };
@@ -1325,7 +1426,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         }
         return mark(4);
     }
-    hipLaunchKernelGGL(ea_prep, dim3(rb4), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(ea_prep, dim3(rb4 + (P.dq_stream ? 1u : 0u)), dim3(256), 0, st, P);
     rc = herr(hipGetLastError());
     if (rc) return rc;
     if (pl.nseg > 0) {
@@ -1343,16 +1444,12 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         });
         rc = herr(attr_err);
         if (rc) return rc;
-        dim3 grid((unsigned)(pl.nseg * pl.nrb), (unsigned)pl.nsplit);
+        dim3 grid((unsigned)(pl.nseg * pl.nrb), (unsigned)pl.nsplit_gen);
         if ((rc = mark(1))) return rc;
         const dim3 blk(EA_THREADS);
         const size_t lds = sizeof(SplitSmem);
-        int dec = 0;
-        if (!o->timers && o->kernel != EA_KERNEL_GENERAL) {
-            dec = ea_launch_decode(P, pl.rb, grid, st);
-            if (dec < 0) return dec;
-        }
-        if (dec) {
+        if (use_decode) {
+            if ((rc = ea_launch_decode(P, st))) return rc;
         } else if (o->timers) {
             if (pl.rb == 1) hipLaunchKernelGGL((ea_split<1, true>), grid, blk, lds, st, P);
             else if (pl.rb == 2) hipLaunchKernelGGL((ea_split<2, true>), grid, blk, lds, st, P);

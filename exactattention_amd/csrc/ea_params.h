@@ -74,10 +74,47 @@ struct Params {
     int32_t pf_nsplit;          // key splits per (segment, row block); 1: rounding in ea_pf_main
     int32_t pf_tps;             // 64-key tiles per key split
     void* pf_part;              // pf_nsplit > 1: the splits' partials (PfPart, then PfEntry arrays)
+    // Equal-share decomposition of the d = 128 decode kernel (dq_stream = 1). The step's 64-key
+    // tiles, unit by unit (unit = (segment, row block), tiles up to its visible end), are cut into
+    // dq_blocks consecutive shares of `share` tiles; block g takes share g, which is one or more
+    // pieces (its intersections with units), and writes piece p of unit u in partial slot p,
+    // p = g - floor(S_u / share). dq_plan, written by the prep kernel's planner block: [0] W
+    // (tiles), [1] share, [2 + u] S_u for u = 0 .. dq_units (prefix sums, S_units = W), then
+    // at dq_rec_off (16-byte aligned) per block g its first piece (u, S_u, S_(u+1), share), u =
+    // dq_units for a block past the last tile. share >= dq_min_share keeps every unit within
+    // nsplit pieces.
+    int32_t dq_stream;
+    int32_t dq_units;
+    int32_t dq_blocks;
+    int32_t dq_min_share;
+    int32_t dq_max_tiles;
+    int32_t dq_rec_off;
+    int32_t* dq_plan;
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
     return (b * P.g.num_tokens + t) * P.g.num_q_heads + hq;
+}
+
+// The key range a decode unit (segment seg, row block rbk of P.rb rows) reads: keys below the
+// largest visible end of its rows (prefix kv_len, tree keys tree_base + i), clipped to seq_len.
+// The decode kernel and the planner of its equal-share decomposition both use it.
+__device__ inline int unit_kend(const Params& P, int seg, int rbk) {
+    const int Hkv = P.g.num_kv_heads;
+    const int b = seg / Hkv;
+    const int row0 = rbk * P.rb;
+    const int nrow = min(P.rb, P.r_seg - row0);
+    const int tb = P.tree_mask ? P.tree_base[b] : 0;
+    int kend = 0;
+    for (int r = 0; r < nrow; ++r) {
+        const int t = (row0 + r) / P.grp;
+        const int64_t tok = (int64_t)b * P.g.num_tokens + t;
+        int e = P.kv_len[tok];
+        const uint64_t m = P.tree_mask ? P.tree_mask[tok] : 0ull;
+        if (m) e = max(e, tb + 64 - (int)__clzll(m));
+        kend = max(kend, e);
+    }
+    return min(kend, (int)P.seq_len[b]);
 }
 
 // global element offset of key n of sequence b, kv head hk (K when isv = 0, V when 1)
@@ -175,9 +212,13 @@ __device__ __forceinline__ int wave_sum_i(int x) {
 }
 
 
-// Launches the d = dv = 128 decode kernel (ea_decode.hip) when the geometry allows it: returns 1
-// when launched, 0 when the caller must run the general split kernel, -100 - e on a HIP error.
-int ea_launch_decode(const Params& P, int rb, dim3 grid, hipStream_t st);
+// The d = dv = 128 decode kernel (ea_decode.hip). ea_decode_eligible: 1 when P's geometry and
+// pointers allow it (else the general split kernel runs). ea_decode_slots: blocks resident on the
+// current device at once. ea_launch_decode: P.dq_blocks blocks over the equal-share plan (0 or
+// -100 - e on a HIP error).
+int ea_decode_eligible(const Params& P);
+int ea_decode_slots(const Params& P, int* slots);
+int ea_launch_decode(const Params& P, hipStream_t st);
 
 // int8-MFMA prefill path (ea_prefill.hip). A tile holds 64 keys of one segment:
 //   [0, 32768)       K digit planes t = 0..3: [t][key 64][128 bytes], 16-byte chunk c of key k

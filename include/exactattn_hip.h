@@ -135,8 +135,11 @@ typedef struct ea_options {
 #define EA_KERNEL_GENERAL 3
 
 /* Bytes of device workspace ea_hip_attention needs for this geometry and options. Also reports
- * the split count it will use. Reference counterpart: none (the Triton launcher allocates its
- * partial buffers itself, src/exactattn/triton_kernels.py:1411-1448). */
+ * the split count it will use: the KV splits per (sequence, KV head), given or chosen; the d = 128
+ * decode kernel reads the same count as a bound and divides the step's key tiles into equal shares
+ * across the grid (at most nsplit + 1 pieces per segment and row block). Reference counterpart:
+ * none (the Triton launcher allocates its partial buffers itself,
+ * src/exactattn/triton_kernels.py:1411-1448). */
 int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* bytes, int32_t* nsplit);
 
 /* Whether ea_hip_attention with this geometry and these options reads o->kv_digits: *reads = 1
