@@ -70,6 +70,7 @@ __device__ void dq_plan_block(const Params& P) {
         plan[0] = W;
         plan[1] = share;
         Su[U] = W;
+        if (P.stats) atomicAdd((unsigned long long*)&P.stats[15], 1ull);
     }
     __syncthreads();
     const int share = s_share;

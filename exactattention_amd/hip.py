@@ -55,7 +55,7 @@ EA_PF_TILE_BYTES = 69632  # one 64-key digit tile (ea_params.h)
 STATS = ["rows", "tier1_flagged", "tier2_certified", "uncertified", "domain_errors", "uncertified_scores",
          "undecided_weights", "uncertified_final", "slow_path_scores",
          "decode_kernel_rows", "prefill_kernel_rows", "prefill_epoch_folds", "prefill_cold_waves",
-         "host_exact_rows", "host_exact_refused"]
+         "host_exact_rows", "host_exact_refused", "decode_equal_share_steps"]
 
 
 def available() -> bool:

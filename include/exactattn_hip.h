@@ -96,7 +96,8 @@ typedef struct ea_options {
                                tile (waves), [12] prefill waves that ran the exact
                                per-pair path, [13] rows certified by the host exact
                                tier (ea_hip_exact_rows), [14] rows it refused (spread
-                               limit, flag 2), [15] reserved */
+                               limit, flag 2), [15] steps whose decode kernel ran
+                               the equal-share plan */
     void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep (the
                                int8 path: q and K/V slicing), the tier-1 kernel, the combine (the
                                int8 path: the merge of its key splits, when it has any) and tier 2,

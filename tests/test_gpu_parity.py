@@ -865,3 +865,33 @@ def test_sequences_of_length_zero(gpu, kernel):
             assert np.array_equal(got, want), (name, splits)
             if kernel != "general":
                 assert st[f"{kernel}_kernel_rows"] > 0, (name, splits, st)
+
+
+@pytest.mark.parametrize("case", ["many_small_units", "ragged_long"])
+def test_decode_equal_share_plan(gpu, case):
+    """The decode kernel's equal-share plan (taken when the uniform split grid would need more
+    than one round of resident blocks): with 1,040 short units every block's share reaches several
+    units (the piece loop), and with a few long ragged sequences shares cut units at arbitrary
+    tiles. Bits equal the oracle's row by row and the same problem at one fixed split count."""
+    rng = np.random.default_rng(77 if case == "many_small_units" else 78)
+    ab = default_alpha_bits(128)
+    if case == "many_small_units":
+        B, S, Hq, Hkv, page = 130, 700, 16, 8, 16
+        lens = rng.integers(0, S + 1, size=B)
+        lens[:3] = [0, 1, S]
+    else:
+        B, S, Hq, Hkv, page = 5, 24000, 16, 8, 64
+        lens = rng.integers(2000, S + 1, size=B)
+    q = bf16(rng, (B, 1, Hq, 128))
+    k = bf16(rng, (B, Hkv, S, 128), "outlier")
+    v = bf16(rng, (B, Hkv, S, 128))
+    base = problem.contiguous(q, k, v, lens.reshape(B, 1), seq_len=lens)
+    prob = problem.to_paged(base, page, rng, "NHD")
+    got, flags, st = _run(prob, ab)
+    assert st["decode_kernel_rows"] > 0 and st["decode_equal_share_steps"] == 1, st
+    want, _ = _oracle(prob, ab)
+    assert not flags.any()
+    assert np.array_equal(got, want)
+    # one step with a split count the caller fixes (uniform splits when it fits one round)
+    got2, flags2, st2 = _run(prob, ab, splits=1)
+    assert np.array_equal(got2, want) and not flags2.any()
