@@ -439,6 +439,25 @@ def graph_steps(dp, ab: int, steps: int, warmup: int, kv_digits=None):
     return ms, dp.out.cpu().numpy().view(np.uint16)
 
 
+def baseline_split_line(prob: dict, ab: int, nsplit: int, steps: int, warmup: int, golden) -> dict:
+    """C2 at the split count BASELINE names (8) instead of the auto count: the graph-replayed step
+    and the decode kernel back to back, timed as the main line times them; the bits must equal the
+    golden hash (the certified output cannot depend on the split count)."""
+    import torch
+    from exactattention_amd.hip import DeviceProblem
+    dp = DeviceProblem(prob, "bf16", nsplit, "cuda:0")
+    ms_step, gout = graph_steps(dp, ab, steps, warmup)
+    b2b = back_to_back_ms(dp, ab, 128, steps)
+    nbytes = algorithmic_bytes(prob)
+    out = {"nsplit": dp.nsplit, "ms_per_step": round(ms_step, 5), "value": round(nbytes / (ms_step * 1e-3) / 1e9, 2),
+           "unit": "GB/s", "kernel_ms": round(b2b, 5) if b2b else None,
+           "kernel_frac": round(nbytes / (b2b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if b2b else None,
+           "bit_exact": (hashlib.sha256(gout.tobytes()).hexdigest() == golden) if golden else None}
+    del dp
+    torch.cuda.empty_cache()
+    return out
+
+
 def tree_line(steps: int, warmup: int) -> dict:
     """C4 speculative tree verification (8 sequences: an 8192-key prefix and a 16-node draft tree
     each, 16 query / 8 KV heads): 32 rows per (sequence, KV head) take the int8 prefill kernel
@@ -778,6 +797,8 @@ def main():
                                 "share": {k: round(tv[i] / tot, 4) for i, k in enumerate(TIMER_PHASES[:7])}}
     del r, dp
     torch.cuda.empty_cache()
+    if args.splits == 0:
+        line["baseline_nsplit"] = baseline_split_line(prob, ab, 8, args.steps, args.warmup, golden)
     if args.only is None and not args.no_prefill:
         line["prefill"] = prefill_line(max(5, min(args.steps, 20)), 2)
         line["tree_verify"] = tree_line(max(5, min(args.steps, 20)), 2)

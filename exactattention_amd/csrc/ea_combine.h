@@ -101,8 +101,12 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
         return 0;
     }
     const double up = 0x1p-53 * (1.0 + 0x1p-28);
+    // the rounding depth inside one partial: n + 4, capped at 16 T + 6 for the decode kernel's
+    // partials of at most T tiles (its lane chains hold 16 keys per tile)
+    int64_t dcap = INT64_MAX;
+    if (P.pv_tiles > 0) dcap = 16 * (int64_t)(P.dq_stream ? P.dq_plan[1] : P.pv_tiles) + 6;
     auto shift_of = [&](int n, int r) __attribute__((always_inline)) { return (n > 0 && R != INT_MIN) ? r - R : 0; };
-    // Z and the bound's weight A = sum_s 2^(R_s - R) Zhat_s (n_s + nsplit + 4)
+    // Z and the bound's weight A = sum_s 2^(R_s - R) Zhat_s (D_s + nsplit), D_s = min(n_s + 4, dcap)
     double Z = 0.0, A = 0.0;
     int nterm = 0, far = 0;
     auto add_z = [&](int n, int r, double z) __attribute__((always_inline)) {
@@ -110,7 +114,7 @@ __device__ inline int combine_row(const Params& P, int64_t row, int lane) {
         far |= (n > 0 && dsh < -900) ? 1 : 0;
         const double zs = n > 0 ? ldexp(z, max(dsh, -1000)) : 0.0;
         Z += zs;
-        A += zs * (double)(n + nsb + 4);
+        A += zs * (double)(min((int64_t)n + 4, dcap) + nsb);
         nterm += n > 0 ? n : 0;
     };
     add_z(n0, r0, z0);

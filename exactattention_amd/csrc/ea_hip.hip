@@ -87,7 +87,7 @@ __device__ void dq_plan_block(const Params& P) {
 }
 
 __global__ void __launch_bounds__(256) ea_prep(Params P) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) *P.wl_cnt = 0;
+    if (blockIdx.x == 0 && threadIdx.x <= EA_T2_BLOCKS) P.wl_cnt[threadIdx.x] = 0;
     if (P.dq_stream && blockIdx.x == gridDim.x - 1) {
         dq_plan_block(P);  // the extra last block
         return;
@@ -588,9 +588,16 @@ __global__ void __launch_bounds__(EA_THREADS, 2) ea_split(Params P) {
 // Kernel 3: combine. One wave per row. Merges the split partials in merge order, then the
 // certified rounding per channel. Rows not certified go to the tier-2 work list.
 // Error bound (u = 2^-53, relative weights w_j 2^-R of the split, n_s visible keys):
-//   |Zhat_s - Z_s| <= (n_s + 4) u' Z_s,  |Nhat_sc - N_sc| <= (n_s + 4) u' Vmax_sc Z_s
-// (any summation tree of FMA-fused exact products, depth <= n_s + 2, u' = u (1 + 2^-28));
-// merging adds depth nsplit, so with A = sum_s 2^(R_s - R) Zhat_s (n_s + nsplit + 4):
+//   |Zhat_s - Z_s| <= D_s u' Z_s,  |Nhat_sc - N_sc| <= D_s u' Vmax_sc Z_s
+// where D_s bounds the roundings on any term's path through the split's sums (FMA-fused exact
+// products, u' = u (1 + 2^-28)). Any summation tree of n_s nonzero terms has at most n_s - 1
+// rounding additions on a path (additions of exact zeros are exact), so D_s = n_s + 4 always
+// holds. The d = 128 decode kernel's sums are shallower (pv_tiles > 0): each lane's P.V chain
+// takes at most 16 keys of each of the partial's T tiles, then 2 additions merge the 4 key groups;
+// each lane's Z chain takes one key per tile, then a 6-level wave sum. There
+// D_s = min(n_s + 4, 16 T + 6), T the most tiles of one partial (split_len / 64, or the share of
+// the equal-share plan). Merging adds depth nsplit, so with A = sum_s 2^(R_s - R) Zhat_s
+// (D_s + nsplit):
 //   eZ = u' A + tiny,  eN_c = u' A max_s Vmax_sc + tiny.
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) ea_combine(Params P) {
@@ -674,32 +681,60 @@ __device__ int block_max_i64(T2Smem& S, int64_t x, int64_t* out) {
     return 0;
 }
 
+// One key chunk's share of a row that tier 2 splits over several blocks: the chunk's sums against
+// its own window bases (R_b - F for Z, nr_c - F for channel c), each as a floor with a count of
+// units lost to the floors.
+struct T2Part {
+    int64_t R;                 // max over the chunk's keys of E + 23 (INT64_MIN: no key)
+    int32_t flag;              // 0, 1 (a logit or weight not certified), 2 (domain error)
+    int32_t pad;
+    uint64_t zhi, zlo, ze;     // Z_b in units 2^(R - F) and its lost count
+    int64_t nr[EA_MAXDV];      // NR_c over the chunk (INT64_MIN: no nonzero V element)
+    uint64_t nhi[EA_MAXDV], nlo[EA_MAXDV], ner[EA_MAXDV];  // N_c,b in units 2^(nr_c - F), lost count
+};
+
+// Rows are split into C key chunks when fewer rows are listed than there are blocks (C = blocks /
+// rows, so one flagged row takes every block instead of one): block (row slot, chunk) computes the
+// chunk's logits and weights and its Z and N sums, writes them as a T2Part, and the row's last
+// chunk block to finish merges the C partials. Merging moves each floored partial to the row's
+// larger base by an arithmetic right shift: floor(a 2^-s) <= a 2^-s < floor(a 2^-s) + lost, so
+// the row's sums stay of the form [acc, acc + lost count] in units of the common base, the form
+// the final rounding takes. With C = 1 the block finishes the row itself.
 __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
     __shared__ T2Smem S;
+    __shared__ int s_last;
     const int tid = threadIdx.x;
-    if ((int)blockIdx.x >= *P.wl_cnt) return;  // no listed row for this block (the usual case)
+    const int cnt = *P.wl_cnt;
+    const int C = cnt >= (int)gridDim.x ? 1 : (int)gridDim.x / max(cnt, 1);
+    const int64_t items = (int64_t)cnt * C;
+    if ((int64_t)blockIdx.x >= items) return;  // no listed row for this block (the usual case)
     for (int i = tid; i < 256; i += EA_T2_THREADS) {
         S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
         S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
     }
     __syncthreads();
-    const int cnt = *P.wl_cnt;
     const int d = P.g.head_dim, dv = P.g.head_dim_v;
     const int Hq = P.g.num_q_heads, T = P.g.num_tokens;
     int32_t* Mw = P.t2M + (int64_t)blockIdx.x * P.t2_keys;
     int64_t* Ew = P.t2E + (int64_t)blockIdx.x * P.t2_keys;
-    for (int item = blockIdx.x; item < cnt; item += gridDim.x) {
-        const int64_t row = P.wl[item];
+    T2Part* parts = (T2Part*)P.t2part;
+    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const int slot = (int)(item / C), chunk = (int)(item % C);
+        const int64_t row = P.wl[slot];
         const int64_t b = row / ((int64_t)T * Hq);
         const int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
         const int hk = hq / P.grp;
         const int64_t tok = b * T + t;
-        // the row's visible keys (vis_prefix, vis_tree_bits: the set tier 1 attends)
+        // the row's visible keys (vis_prefix, vis_tree_bits: the set tier 1 attends); this block
+        // takes keys [jc0, jc1) of them
         const int64_t slen = P.seq_len[b];
         const int64_t L = vis_prefix(P.kv_len[tok], slen);
         const uint64_t mask =
             P.tree_mask ? vis_tree_bits(P.tree_mask[tok], (int64_t)P.tree_base[b], L, slen) : 0ull;
         const int64_t nkeys = L + __popcll(mask);
+        const int64_t csz = (nkeys + C - 1) / C;
+        const int64_t jc0 = min(nkeys, (int64_t)chunk * csz), jc1 = min(nkeys, jc0 + csz);
+        const int64_t nkc = jc1 - jc0;
         const int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
         if (tid == 0) S.flag = 0;
         const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
@@ -714,19 +749,16 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
         __syncthreads();
         int myflag = 0;
         if (nkeys > P.t2_keys) myflag = 1;  // workspace too small: not certified
-        // ---- scores, logits, weights. Wave wv takes keys wv, wv + 8, ... in batches of 64: for
-        // each key of the batch the wave reads the K row coalesced (lane ln: dims 2 ln, 2 ln + 1),
-        // finds the window base from the lead exponent (wave max) and sums the floor-shifted
-        // products in 128 bits (wave reduction); lane (key % 64) keeps the sum. Then every lane
-        // decides its key's logit and weight at once.
+        // ---- scores, logits, weights: one key per thread, its K row read coalesced in 16-dim
+        // chunks twice (the lead exponent, then the window sum in 128 bits)
         const int wv = tid >> 6, ln = tid & 63;
         uint64_t tq0 = __builtin_amdgcn_s_memtime();
         // phase clocks (P.timers set): slots 9..13 = scores, Z, N maxima, N sums, rounding
-        auto t2tick = [&](int slot) __attribute__((always_inline)) {
+        auto t2tick = [&](int ts) __attribute__((always_inline)) {
             if (P.timers) {
-                const uint64_t t = __builtin_amdgcn_s_memtime();
-                if (tid == 0) atomicAdd((unsigned long long*)&P.timers[slot], (unsigned long long)(t - tq0));
-                tq0 = t;
+                const uint64_t tn = __builtin_amdgcn_s_memtime();
+                if (tid == 0) atomicAdd((unsigned long long*)&P.timers[ts], (unsigned long long)(tn - tq0));
+                tq0 = tn;
             }
         };
         const int64_t tb = P.tree_mask ? P.tree_base[b] : 0;
@@ -740,10 +772,10 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
         // one key per thread, its K row in registers (16-byte loads when rows are aligned)
         const bool k16 = (((uintptr_t)P.k | (uintptr_t)(P.g.k_page_stride * 2) | (uintptr_t)(P.g.k_slot_stride * 2) |
                            (uintptr_t)(P.g.k_head_stride * 2)) & 15) == 0 && d == 128;
-        for (int64_t j = tid; j < nkeys && !myflag && S.flag < 2; j += EA_T2_THREADS) {
-            const uint16_t* kr = P.k + kv_off(P, b, key_n(j), hk, 0);
+        for (int64_t jr = tid; jr < nkc && !myflag && S.flag < 2; jr += EA_T2_THREADS) {
+            const uint16_t* kr = P.k + kv_off(P, b, key_n(jc0 + jr), hk, 0);
             // 16 dims (8 dwords) at a time, read twice: the lead exponent, then the window sum
-            auto chunk = [&](int c16, uint32_t (&kw)[8]) __attribute__((always_inline)) {
+            auto kchunk = [&](int c16, uint32_t (&kw)[8]) __attribute__((always_inline)) {
                 if (k16) {
                     const uint4 u0 = ((const uint4*)kr)[2 * c16], u1 = ((const uint4*)kr)[2 * c16 + 1];
                     kw[0] = u0.x; kw[1] = u0.y; kw[2] = u0.z; kw[3] = u0.w;
@@ -760,7 +792,7 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
             bool bad = false;
             for (int c16 = 0; c16 < EA_MAXD / 16; ++c16) {
                 uint32_t kw[8];
-                chunk(c16, kw);
+                kchunk(c16, kw);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int i = 16 * c16 + e;
@@ -784,7 +816,7 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
                 uint64_t err = 0;
                 for (int c16 = 0; c16 < EA_MAXD / 16; ++c16) {
                     uint32_t kw[8];
-                    chunk(c16, kw);
+                    kchunk(c16, kw);
 #pragma unroll
                     for (int e = 0; e < 16; ++e) {
                         const int i = 16 * c16 + e;
@@ -798,7 +830,7 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
                         err += (uint64_t)lost;
                     }
                 }
-            uint32_t tlo = 0, thi = 0;
+                uint32_t tlo = 0, thi = 0;
                 const int slo = rn32_prod(P.am, acc, P.ae + base, &tlo);
                 const int shi = err ? rn32_prod(P.am, acc + (i128)err, P.ae + base, &thi) : slo;
                 if (!err) thi = tlo;
@@ -820,8 +852,8 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
                     break;
                 }
             }
-            Mw[j] = M;
-            Ew[j] = E;
+            Mw[jr] = M;
+            Ew[jr] = E;
             emax = max(emax, E + 23);
         }
         if (myflag) atomicMax(&S.flag, 1);
@@ -830,29 +862,30 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
         block_max_i64(S, emax, &R);
         t2tick(9);
         int fl = S.flag;
-        if (fl == 0 && nkeys > 0) {
-            int key_log2 = 0;
-            while (((int64_t)1 << key_log2) < nkeys) ++key_log2;
-            const int F = 126 - key_log2;
+        // F: every chunk sums against windows of the row's key count, so the partials merge
+        int key_log2 = 0;
+        while (((int64_t)1 << key_log2) < nkeys) ++key_log2;
+        const int F = 126 - key_log2;
+        i128 z = 0;
+        uint64_t ze = 0;
+        if (fl == 0 && nkc > 0) {
             // Z
-            i128 z = 0;
-            uint64_t ze = 0;
-            for (int64_t j = tid; j < nkeys; j += EA_T2_THREADS) {
+            for (int64_t jr = tid; jr < nkc; jr += EA_T2_THREADS) {
                 int lost;
-                z += floor_shift128((i128)Mw[j], Ew[j] - (R - F), &lost);
+                z += floor_shift128((i128)Mw[jr], Ew[jr] - (R - F), &lost);
                 ze += (uint64_t)lost;
             }
             block_reduce_i128(S, &z, &ze);
             t2tick(10);
-            // N per channel, key-parallel: wave wv takes keys wv, wv + 8, ...; lane ln channels
-            // 2 ln and 2 ln + 1. Pass 1: NR_c = max_j (E_j + 24 + lead(v_jc)); pass 2: the
-            // 128-bit sums of floor(M_j v_jc 2^(E_j + e_jc - base_c)) and their lost counts,
-            // base_c = NR_c - F; partials reduced over the waves through LDS.
-            // batches of 64 keys per wave: lane ln finds key j0 + ln's V row, the row offsets are
+            // N per channel, key-parallel: wave wv takes keys wv, wv + 8, ... of the chunk; lane
+            // ln channels 2 ln and 2 ln + 1. Pass 1: NR_c = max_j (E_j + 24 + lead(v_jc)); pass
+            // 2: the 128-bit sums of floor(M_j v_jc 2^(E_j + e_jc - base_c)) and their lost
+            // counts, base_c = NR_c - F; partials reduced over the waves through LDS.
+            // batches of 16 keys per wave: lane ln finds key jb + ln's V row, the row offsets are
             // broadcast and the batch's V elements loaded together (independent loads in flight)
             uint32_t vx[16][2];
-            auto load_batch = [&](int64_t j0, int nk) __attribute__((always_inline)) {
-                const int64_t myoff = ln < nk ? kv_off(P, b, key_n(j0 + ln), hk, 1) : 0;
+            auto load_batch = [&](int64_t jb, int nk) __attribute__((always_inline)) {
+                const int64_t myoff = ln < nk ? kv_off(P, b, key_n(jc0 + jb + ln), hk, 1) : 0;
 #pragma unroll
                 for (int kk = 0; kk < 16; ++kk) {
                     const int64_t o = __shfl(myoff, kk, 64);
@@ -860,18 +893,18 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
                     for (int h = 0; h < 2; ++h) vx[kk][h] = (kk < nk && 2 * ln + h < dv) ? (uint32_t)P.v[o + 2 * ln + h] : 0u;
                 }
             };
-            const int64_t nvb = (nkeys + 16 * EA_T2_WAVES - 1) / (16 * EA_T2_WAVES);
+            const int64_t nvb = (nkc + 16 * EA_T2_WAVES - 1) / (16 * EA_T2_WAVES);
             int64_t nr[2] = {INT64_MIN, INT64_MIN};
             bool vbad = false;
             for (int64_t bt = 0; bt < nvb; ++bt) {
-                const int64_t j0 = (bt * EA_T2_WAVES + wv) * 16;
-                if (j0 >= nkeys) break;
-                const int nk = (int)min((int64_t)16, nkeys - j0);
-                load_batch(j0, nk);
+                const int64_t jb = (bt * EA_T2_WAVES + wv) * 16;
+                if (jb >= nkc) break;
+                const int nk = (int)min((int64_t)16, nkc - jb);
+                load_batch(jb, nk);
 #pragma unroll
                 for (int kk = 0; kk < 16; ++kk) {
                     if (kk >= nk) continue;
-                    const int64_t e = Ew[j0 + kk] + 24;
+                    const int64_t e = Ew[jb + kk] + 24;
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                     const uint32_t x = vx[kk][h];
@@ -898,15 +931,15 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
             i128 acc[2] = {0, 0};
             uint64_t err[2] = {0, 0};
             for (int64_t bt = 0; bt < nvb; ++bt) {
-                const int64_t j0 = (bt * EA_T2_WAVES + wv) * 16;
-                if (j0 >= nkeys) break;
-                const int nk = (int)min((int64_t)16, nkeys - j0);
-                load_batch(j0, nk);
+                const int64_t jb = (bt * EA_T2_WAVES + wv) * 16;
+                if (jb >= nkc) break;
+                const int nk = (int)min((int64_t)16, nkc - jb);
+                load_batch(jb, nk);
 #pragma unroll
                 for (int kk = 0; kk < 16; ++kk) {
                     if (kk >= nk) continue;
-                    const int64_t Ej = Ew[j0 + kk];
-                    const int64_t Mj = Mw[j0 + kk];
+                    const int64_t Ej = Ew[jb + kk];
+                    const int64_t Mj = Mw[jb + kk];
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const uint32_t x = vx[kk][h];
@@ -931,50 +964,150 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
             }
             __syncthreads();
             t2tick(12);
-            bool ok = true;
-            for (int c = tid; c < dv; c += EA_T2_THREADS) {
-                int64_t NR = INT64_MIN;
-                for (int q = 0; q < EA_T2_WAVES; ++q) NR = max(NR, S.nrw[q][c]);
-                uint32_t bits = 0;
-                if (NR != INT64_MIN) {
-                    const int64_t base = NR - F;
-                    u128 accu = 0;
-                    uint64_t err = 0;
-                    for (int q = 0; q < EA_T2_WAVES; ++q) {
-                        accu += ((u128)S.ahi[q][c] << 64) | S.alo[q][c];
-                        err += S.aer[q][c];
-                    }
-                    // N_c in [acc, acc + err] 2^base over Z in [z, z + ze] 2^(R - F)
-                    const i128 acc = (i128)accu;
-                    if (!certify_quotient(acc, acc + (i128)err, z, z + (i128)ze, base - (R - F), P.out_fp32, &bits))
-                        ok = false;
-                }
-                if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = bits;
-                else ((uint16_t*)P.out)[obase + c] = (uint16_t)bits;
-            }
-            if (!ok) atomicMax(&S.flag, 1);
-            __syncthreads();
-            t2tick(13);
             fl = S.flag;
-        } else if (fl == 0) {
-            for (int c = tid; c < dv; c += EA_T2_THREADS) {
-                if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
-                else ((uint16_t*)P.out)[obase + c] = 0;
-            }
         }
-        if (fl != 0) {
-            for (int c = tid; c < dv; c += EA_T2_THREADS) {
-                if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
-                else ((uint16_t*)P.out)[obase + c] = 0;
+        // the chunk's channel sums (over the waves: one base per channel, exact 128-bit adds)
+        auto channel_sum = [&](int c, int64_t* NR, i128* acc, uint64_t* err) __attribute__((always_inline)) {
+            *NR = INT64_MIN;
+            u128 accu = 0;
+            uint64_t e = 0;
+            for (int q = 0; q < EA_T2_WAVES; ++q) {
+                *NR = max(*NR, S.nrw[q][c]);
+                accu += ((u128)S.ahi[q][c] << 64) | S.alo[q][c];
+                e += S.aer[q][c];
             }
+            *acc = (i128)accu;
+            *err = e;
+        };
+        // certified RN(N_c / Z) into the output, N_c in [acc, acc + err] 2^(NR - F), Z in
+        // [zz, zz + zze] 2^(RR - F); false when the interval straddles a rounding boundary
+        auto round_out = [&](int c, int64_t NR, i128 acc, uint64_t err, i128 zz, uint64_t zze, int64_t RR) {
+            uint32_t bits = 0;
+            bool ok = true;
+            if (NR != INT64_MIN)
+                ok = certify_quotient(acc, acc + (i128)err, zz, zz + (i128)zze, NR - RR, P.out_fp32, &bits);
+            if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = bits;
+            else ((uint16_t*)P.out)[obase + c] = (uint16_t)bits;
+            return ok;
+        };
+        // flags, zero output for a flagged row, stats: once per row
+        auto finish_row = [&](int f) __attribute__((always_inline)) {
+            if (f != 0) {
+                for (int c = tid; c < dv; c += EA_T2_THREADS) {
+                    if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
+                    else ((uint16_t*)P.out)[obase + c] = 0;
+                }
+            }
+            if (tid == 0) {
+                P.flags[row] = (uint8_t)f;
+                if (P.stats) {
+                    if (f == 0) atomicAdd((unsigned long long*)&P.stats[2], 1ull);
+                    if (f == 1) atomicAdd((unsigned long long*)&P.stats[3], 1ull);
+                    if (f == 2) atomicAdd((unsigned long long*)&P.stats[4], 1ull);
+                }
+            }
+        };
+        if (C == 1) {
+            if (fl == 0 && nkeys > 0) {
+                bool ok = true;
+                for (int c = tid; c < dv; c += EA_T2_THREADS) {
+                    int64_t NR;
+                    i128 acc;
+                    uint64_t err;
+                    channel_sum(c, &NR, &acc, &err);
+                    if (!round_out(c, NR, acc, err, z, ze, R)) ok = false;
+                }
+                if (!ok) atomicMax(&S.flag, 1);
+                __syncthreads();
+                t2tick(13);
+                fl = S.flag;
+            } else if (fl == 0) {
+                for (int c = tid; c < dv; c += EA_T2_THREADS) {
+                    if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
+                    else ((uint16_t*)P.out)[obase + c] = 0;
+                }
+            }
+            finish_row(fl);
+            __syncthreads();
+            continue;
         }
+        // ---- C > 1: this chunk's partial (item < gridDim.x slots), then the row's last chunk
+        // block merges. Release: every thread's partial stores are visible at device scope (other
+        // XCDs included) before the count moves; acquire: the merging block reads the others'
+        // partials only after it has seen the full count.
+        T2Part& pt = parts[item];
+        const bool have = fl == 0 && nkc > 0;
         if (tid == 0) {
-            P.flags[row] = (uint8_t)fl;
-            if (P.stats) {
-                if (fl == 0) atomicAdd((unsigned long long*)&P.stats[2], 1ull);
-                if (fl == 1) atomicAdd((unsigned long long*)&P.stats[3], 1ull);
-                if (fl == 2) atomicAdd((unsigned long long*)&P.stats[4], 1ull);
+            pt.R = have ? R : INT64_MIN;
+            pt.flag = fl;
+            pt.zhi = have ? (uint64_t)((u128)z >> 64) : 0;
+            pt.zlo = have ? (uint64_t)(u128)z : 0;
+            pt.ze = have ? ze : 0;
+        }
+        for (int c = tid; c < dv; c += EA_T2_THREADS) {
+            int64_t NR = INT64_MIN;
+            i128 acc = 0;
+            uint64_t err = 0;
+            if (have) channel_sum(c, &NR, &acc, &err);
+            pt.nr[c] = NR;
+            pt.nhi[c] = (uint64_t)((u128)acc >> 64);
+            pt.nlo[c] = (uint64_t)(u128)acc;
+            pt.ner[c] = err;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(&P.wl_cnt[1 + slot], 1) == C - 1;
+        __syncthreads();
+        if (s_last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            const T2Part* rp = parts + (int64_t)slot * C;
+            int rf = 0;
+            int64_t RR = INT64_MIN;
+            for (int k = 0; k < C; ++k) {
+                rf = max(rf, rp[k].flag);
+                RR = max(RR, rp[k].R);
             }
+            if (rf == 0 && RR != INT64_MIN) {
+                // Z over the chunks, each moved to base RR - F (thread k takes chunk k)
+                i128 zz = 0;
+                uint64_t zze = 0;
+                for (int k = tid; k < C; k += EA_T2_THREADS) {
+                    if (rp[k].R == INT64_MIN) continue;
+                    const i128 zb = (i128)(((u128)rp[k].zhi << 64) | rp[k].zlo);
+                    int lost;
+                    zz += floor_shift128(zb, rp[k].R - RR, &lost);
+                    zze += rp[k].ze + (uint64_t)lost;
+                }
+                block_reduce_i128(S, &zz, &zze);
+                bool ok = true;
+                for (int c = tid; c < dv; c += EA_T2_THREADS) {
+                    int64_t NR = INT64_MIN;
+                    for (int k = 0; k < C; ++k) NR = max(NR, rp[k].nr[c]);
+                    i128 acc = 0;
+                    uint64_t err = 0;
+                    if (NR != INT64_MIN)
+                        for (int k = 0; k < C; ++k) {
+                            if (rp[k].nr[c] == INT64_MIN) continue;
+                            const i128 nb = (i128)(((u128)rp[k].nhi[c] << 64) | rp[k].nlo[c]);
+                            int lost;
+                            acc += floor_shift128(nb, rp[k].nr[c] - NR, &lost);
+                            err += rp[k].ner[c] + (uint64_t)lost;
+                        }
+                    if (!round_out(c, NR, acc, err, zz, zze, RR)) ok = false;
+                }
+                if (tid == 0) S.flag = 0;
+                __syncthreads();
+                if (!ok) atomicMax(&S.flag, 1);
+                __syncthreads();
+                rf = S.flag;
+            } else if (rf == 0) {
+                for (int c = tid; c < dv; c += EA_T2_THREADS) {
+                    if (P.out_fp32) ((uint32_t*)P.out)[obase + c] = 0;
+                    else ((uint16_t*)P.out)[obase + c] = 0;
+                }
+            }
+            finish_row(rf);
+            if (tid == 0) P.wl_cnt[1 + slot] = 0;  // the row's count, ready for the next launch
         }
         __syncthreads();
     }
@@ -1129,7 +1262,7 @@ struct Plan {
     int nsplit, split_len, rb, nrb, r_seg, grp, nseg, pshift, dlog;
     int64_t rows;
     size_t off_q64, off_qinfo, off_qn, off_pR, off_pn, off_pZ, off_pN, off_pV, off_wl, off_cnt, off_t2M, off_t2E, total;
-    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr, off_pfpart, off_dq;
+    size_t off_pfq, off_pfqm, off_pfkv, off_pfscr, off_pfpart, off_dq, off_t2part;
     int t2_keys;
     int prefill, pf_ntiles, pf_nrb, pf_nsplit, pf_tps;
     // the decode kernel's equal-share decomposition (Params::dq_*): dq = 1 when the geometry may
@@ -1211,7 +1344,8 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     pl->off_pN = off; off = align_up(off + (size_t)pl->nsplit * R * dv * 8);
     pl->off_pV = off; off = align_up(off + (size_t)pl->nsplit * pl->nseg * pl->nrb * dv * 4);
     pl->off_wl = off; off = align_up(off + (size_t)(R > 0 ? R : 1) * 4);
-    pl->off_cnt = off; off = align_up(off + 4);
+    pl->off_cnt = off; off = align_up(off + 4 * (1 + EA_T2_BLOCKS));
+    pl->off_t2part = off; off = align_up(off + EA_T2_BLOCKS * sizeof(T2Part));
     pl->off_dq = off;
     pl->dq_rec_off = (3 + pl->dq_units + 3) & ~3;  // 16-byte aligned block records after S
     if (pl->dq) off = align_up(off + (size_t)(pl->dq_rec_off + 4 * EA_DQ_MAX_BLOCKS) * 4);
@@ -1364,6 +1498,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     P.pV = (float*)(ws + pl.off_pV);
     P.wl = (int32_t*)(ws + pl.off_wl);
     P.wl_cnt = (int32_t*)(ws + pl.off_cnt);
+    P.t2part = (void*)(ws + pl.off_t2part);
     P.t2M = (int32_t*)(ws + pl.off_t2M);
     P.t2E = (int64_t*)(ws + pl.off_t2E);
     P.t2_keys = pl.t2_keys;
@@ -1394,6 +1529,7 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         if (use_decode && (rc = ea_decode_slots(P, &slots))) return rc;
         // the equal-share plan when the uniform split grid would take more than one round of
         // resident blocks (long or ragged contexts); otherwise one block per (unit, split)
+        if (use_decode) P.pv_tiles = pl.split_len / EA_TILE;
         if (use_decode && (int64_t)pl.dq_units * pl.nsplit_gen > slots) {
             const int64_t nb = std::min<int64_t>(slots, EA_DQ_MAX_BLOCKS);
             P.dq_stream = 1;

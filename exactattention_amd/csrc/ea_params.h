@@ -52,7 +52,8 @@ struct Params {
     double* pN;       // nsplit * rows * dv
     float* pV;        // nsplit * nseg * nrb * dv : max |v| per channel over the block's keys
     int32_t* wl;      // rows
-    int32_t* wl_cnt;  // 1
+    int32_t* wl_cnt;  // 1 + EA_T2_BLOCKS: the work list's length, then tier 2's per-row chunk counts
+    void* t2part;     // EA_T2_BLOCKS tier-2 chunk partials (T2Part, ea_hip.hip)
     int32_t* t2M;     // EA_T2_BLOCKS * max_keys
     int64_t* t2E;     // EA_T2_BLOCKS * max_keys
     int32_t t2_keys;
@@ -90,6 +91,10 @@ struct Params {
     int32_t dq_max_tiles;
     int32_t dq_rec_off;
     int32_t* dq_plan;
+    // Most 64-key tiles in one partial of the d = 128 decode kernel (split_len / 64, or the share
+    // of its equal-share plan); 0 when another kernel wrote the partials. The combine's error bound
+    // uses it: the kernel's lane chains hold at most 16 keys of each tile.
+    int32_t pv_tiles;
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {

@@ -240,7 +240,7 @@ __device__ __forceinline__ void slice32(const uint16_t* src, bool valid, Slice32
 // work-list counter (this is the step's first kernel on the prefill path).
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) ea_pf_qslice(Params P) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) *P.wl_cnt = 0;
+    if (blockIdx.x == 0 && threadIdx.x <= EA_T2_BLOCKS) P.wl_cnt[threadIdx.x] = 0;
     const int q16 = threadIdx.x & 15;
     const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     if (row >= P.rows) return;  // whole 16-lane groups leave together
@@ -1299,7 +1299,15 @@ int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int kernel, int* ntil
     // Rows of one (sequence, KV head) that fill a 32-row block (64 tokens, or fewer tokens with a
     // wider GQA group: speculative trees, chunked prefill) read each K/V tile once here, against
     // once per 1-4 rows in the decode kernel (C4: 0.82 ms here, 2.57 ms there)
-    if (!force && g.num_tokens < 64 && r_seg < PF_RPB) return 0;
+    // Segments of 16-31 rows (verification of 8-15 draft tokens) come here too when there is
+    // enough work: measured on MI355X (contiguous K/V, graph replays), the int8 kernel beats the
+    // decode kernel's 4-row blocks by 9-14% at 16 rows with 64+ segments of 4K+ keys or 32+ of
+    // 8K+, and by 6-38% at 24 rows with 8K+ keys; with fewer or shorter segments the decode
+    // kernel is faster (up to 1.6x at 2K keys).
+    const int64_t nseg = (int64_t)g.num_seqs * g.num_kv_heads;
+    const bool mid = r_seg >= 16 && ((nseg >= 64 && g.max_seq_len >= 4096) || (nseg >= 32 && g.max_seq_len >= 8192) ||
+                                     (r_seg >= 24 && g.max_seq_len >= 8192));
+    if (!force && g.num_tokens < 64 && r_seg < PF_RPB && !mid) return 0;
     if (r_seg >= (1 << 30) || (int64_t)g.max_seq_len + 64 >= (1 << 30)) return 0;
     const int rpb = PF_RPB;
     *ntiles = (g.max_seq_len + 63) / 64;

@@ -73,6 +73,28 @@ def _rows(prob):
     return prob["q"].shape[0] * prob["q"].shape[1] * prob["q"].shape[2]
 
 
+@pytest.mark.parametrize("nrows,kind", [(1, "normal"), (3, "wide"), (7, "outlier"), (2, "subnormal")])
+def test_forced_tier2_splits_few_long_rows(gpu, nrows, kind):
+    """Fewer listed rows than tier 2's 32 blocks: each row's keys are split over 32 // rows blocks
+    (1 row: 32 chunks, 3: 10, 7: 4, 2: 16) whose partials the row's last block merges. Ragged key
+    counts (some rows shorter than their chunk count would need) and every input kind; bits equal
+    the oracle's, every row certified by tier 2."""
+    rng = np.random.default_rng(900 + nrows)
+    d = dv = 128
+    S = 2500
+    q = bf16(rng, (nrows, 1, 1, d), kind)
+    k = bf16(rng, (nrows, 1, S, d), kind)
+    v = bf16(rng, (nrows, 1, S, dv), "wide" if kind == "normal" else "normal")
+    seq = np.array([S, 17, 1, 900, 2049, 31, 2500][:nrows], dtype=np.int32)
+    prob = problem.contiguous(q, k, v, seq.reshape(nrows, 1), seq_len=seq)
+    ab = default_alpha_bits(d)
+    want, _ = _oracle(prob, ab)
+    for kernel in ("decode", "general"):
+        got, flags, st = _run(prob, ab, kernel=kernel, force_tier2=True)
+        assert st["tier2_certified"] == nrows and not flags.any(), st
+        assert np.array_equal(got, want)
+
+
 def _qwen_rows(d=128):
     z = np.load(os.path.join(GOLD, "qwen3_0.6b_heads.npz"))
     q, k, v = z["q_27_11"], z["k_27_11"], z["v_27_11"]
