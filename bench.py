@@ -493,6 +493,48 @@ def tree_line(steps: int, warmup: int) -> dict:
     return line
 
 
+def exact_tier_line(reps: int = 3) -> dict:
+    """What a row that tier 1 leaves costs on the device tier 2: ea_options.force_tier2 lists every
+    row, on one row of 32,768 keys (tier 2 splits its keys over its 32 blocks) and on 32 such rows
+    (one block each), bf16 N(0,1) data drawn on the device (torch, seed 7), contiguous K/V. The
+    time is the events around tier 2 in the step (min of `reps`); the bits must equal tier 1's."""
+    import torch
+    from exactattention_amd import configs, problem
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    ab = configs.alpha_bits()
+    d, n = 128, 32768
+    out = []
+    for rows in (1, 32):
+        gen = torch.Generator(device="cuda:0").manual_seed(7)
+        q = torch.randn((1, 1, rows, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        k = torch.randn((1, rows, n, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        v = torch.randn((1, rows, n, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        g = problem._geom(1, 1, rows, rows, d, d, (rows * d, rows * d, d), (rows * d, rows * d, d),
+                          (rows * n * d, d, n * d), (rows * n * d, d, n * d), 1, 0, n)
+        prob = dict(geom=g, q=q, k=k, v=v, seq_len=np.full(1, n, np.int32), kv_len=np.full(1, n, np.int32),
+                    block_table=None, block_table_offset=None, tree_mask=None, tree_base=None,
+                    out_shape=(1, 1, rows, d))
+        dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+        launch_hip(dp, ab)
+        torch.cuda.synchronize()
+        want = dp.out.cpu().numpy().copy()
+        ev = HipEvents(5)
+        times = []
+        for _ in range(reps):
+            dp.stats.zero_()
+            launch_hip(dp, ab, events=ctypes.cast(ev.slot(0), ctypes.POINTER(ctypes.c_void_p)), force_tier2=True)
+            torch.cuda.synchronize()
+            times.append(ev.ms(3, 4))
+        ev.close()
+        st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+        out.append({"rows": rows, "keys_per_row": n, "tier2_ms": round(min(times), 4),
+                    "blocks_per_row": 32 // rows, "tier2_certified": st["tier2_certified"],
+                    "bits_equal_tier1": bool(np.array_equal(dp.out.cpu().numpy(), want))})
+        del dp, prob, q, k, v
+        torch.cuda.empty_cache()
+    return {"basis": "force_tier2, HIP events around the work-list and tier-2 launches, min of 3", "cases": out}
+
+
 def long_context_line(steps: int, warmup: int) -> dict:
     """C5 ragged long-context decode (16 sequences of 8K-131K keys, outlier channels in k, page 16)
     on the fp64 decode kernel: HBM roofline over the algorithmic bytes, bits against the golden
@@ -705,7 +747,7 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill measurement")
-    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving", "shapes", "drop_in"), default=None,
+    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving", "shapes", "drop_in", "exact_tier"), default=None,
                     help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
                     help="after the timed steps, run 5 steps of the phase-clock build and report it")
@@ -737,6 +779,9 @@ def main():
         return
     if args.only == "C5":
         print(json.dumps({"long_context": long_context_line(args.steps, args.warmup)}), flush=True)
+        return
+    if args.only == "exact_tier":
+        print(json.dumps({"exact_tier": exact_tier_line()}), flush=True)
         return
     if args.only == "shapes":
         print(json.dumps({"published_shapes": published_shapes_line(args.steps, args.warmup)}), flush=True)
@@ -806,6 +851,7 @@ def main():
     if args.only is None:
         line["serving"] = serving_line(prob, ab, max(5, min(args.steps, 20)))
         line["published_shapes"] = published_shapes_line(max(5, min(args.steps, 20)), 2)
+        line["exact_tier"] = exact_tier_line()
     if args.only is None and not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         csr = c2_csr(prob)
