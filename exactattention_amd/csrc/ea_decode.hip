@@ -65,6 +65,7 @@ __device__ __forceinline__ float absf(float x) { return __builtin_fabsf(x); }
 
 template <int RB, int PGL, bool STREAM>
 __device__ __forceinline__ void decode_body(Params P) {
+    static_assert(RB == 1 || RB == 2, "1- or 2-row blocks (two waves per SIMD)");
     extern __shared__ __align__(16) unsigned char smem_raw[];
     DecodeSmem<RB>& S = *reinterpret_cast<DecodeSmem<RB>*>(smem_raw);
 
@@ -324,15 +325,10 @@ __device__ __forceinline__ void decode_body(Params P) {
                 auto gate = [&](dptr (&o)[RB]) __attribute__((always_inline)) {
                     if constexpr (RB == 1) {
                         asm volatile("s_mov_b64 %0, %1" : "=&s"(o[0]) : "s"(qrow[0]), "v"(a0[0]), "v"(a1[0]));
-                    } else if constexpr (RB == 2) {
+                    } else {
                         asm volatile("s_mov_b64 %0, %2\n\ts_mov_b64 %1, %3"
                                      : "=&s"(o[0]), "=&s"(o[1])
                                      : "s"(qrow[0]), "s"(qrow[1]), "v"(a0[0]), "v"(a1[0]), "v"(a0[1]), "v"(a1[1]));
-                    } else {
-                        asm volatile("s_mov_b64 %0, %4\n\ts_mov_b64 %1, %5\n\ts_mov_b64 %2, %6\n\ts_mov_b64 %3, %7"
-                                     : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
-                                     : "s"(qrow[0]), "s"(qrow[1]), "s"(qrow[2]), "s"(qrow[3]), "v"(a0[0]), "v"(a1[0]),
-                                       "v"(a0[1]), "v"(a1[1]), "v"(a0[2]), "v"(a1[2]), "v"(a0[3]), "v"(a1[3]));
                     }
                 };
                 auto qload = [&](int h, double (&qv)[RB][4]) __attribute__((always_inline)) {
@@ -613,7 +609,7 @@ __device__ __forceinline__ void decode_body(Params P) {
 namespace {
 // Uniform splits: one block per (unit, split). Two waves per SIMD for the 1- and 2-row blocks.
 template <int RB, int PGL>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(RB < 4 ? 2 : 1, 2))) ea_decode(Params P) {
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) ea_decode(Params P) {
     decode_body<RB, PGL, false>(P);
 }
 
@@ -621,7 +617,7 @@ __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(RB < 4
 // loop adds a few live registers; two waves per SIMD are kept for the 1- and 2-row blocks (the
 // rare exact paths then reload a few values from scratch).
 template <int RB, int PGL>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(RB < 4 ? 2 : 1, 2)))
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ea_decode_stream(Params P) {
     decode_body<RB, PGL, true>(P);
 }
@@ -644,7 +640,7 @@ int ea::ea_decode_eligible(const Params& P) {
     const ea_geometry& g = P.g;
     if (g.head_dim != 128 || g.head_dim_v != 128) return 0;
     if (P.bt && P.pshift < 2) return 0;
-    if (P.rb != 1 && P.rb != 2 && P.rb != 4) return 0;
+    if (P.rb != 1 && P.rb != 2) return 0;
     // 16-byte alignment of every K/V row start (dwordx4 loads)
     if (((uintptr_t)P.k | (uintptr_t)P.v) & 15) return 0;
     if ((g.k_page_stride | g.k_slot_stride | g.k_head_stride | g.v_page_stride | g.v_slot_stride | g.v_head_stride) & 7)
@@ -661,24 +657,20 @@ namespace {
 // page lookups every PGL keys, PGL <= page size (one lookup per 64-key tile without a table)
 const void* decode_fn_for(const Params& P, bool stream) {
     const int pgl = !P.bt ? 64 : (P.pshift >= 6 ? 64 : (P.pshift >= 4 ? 16 : 4));
-    if (stream) return P.rb == 1 ? decode_fn<1, true>(pgl) : (P.rb == 2 ? decode_fn<2, true>(pgl) : decode_fn<4, true>(pgl));
-    return P.rb == 1 ? decode_fn<1, false>(pgl) : (P.rb == 2 ? decode_fn<2, false>(pgl) : decode_fn<4, false>(pgl));
+    if (stream) return P.rb == 1 ? decode_fn<1, true>(pgl) : decode_fn<2, true>(pgl);
+    return P.rb == 1 ? decode_fn<1, false>(pgl) : decode_fn<2, false>(pgl);
 }
-size_t decode_lds(int rb) {
-    return rb == 1 ? sizeof(DecodeSmem<1>) : (rb == 2 ? sizeof(DecodeSmem<2>) : sizeof(DecodeSmem<4>));
-}
+size_t decode_lds(int rb) { return rb == 1 ? sizeof(DecodeSmem<1>) : sizeof(DecodeSmem<2>); }
 hipError_t decode_attrs() {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [] {
-        const void* fns[18] = {decode_fn<1, false>(4), decode_fn<1, false>(16), decode_fn<1, false>(64),
+        const void* fns[12] = {decode_fn<1, false>(4), decode_fn<1, false>(16), decode_fn<1, false>(64),
                                decode_fn<2, false>(4), decode_fn<2, false>(16), decode_fn<2, false>(64),
-                               decode_fn<4, false>(4), decode_fn<4, false>(16), decode_fn<4, false>(64),
                                decode_fn<1, true>(4),  decode_fn<1, true>(16),  decode_fn<1, true>(64),
-                               decode_fn<2, true>(4),  decode_fn<2, true>(16),  decode_fn<2, true>(64),
-                               decode_fn<4, true>(4),  decode_fn<4, true>(16),  decode_fn<4, true>(64)};
+                               decode_fn<2, true>(4),  decode_fn<2, true>(16),  decode_fn<2, true>(64)};
         for (const void* f : fns) {
-            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem<4>));
+            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DecodeSmem<2>));
             if (e != hipSuccess) attr_err = e;
         }
     });
@@ -690,12 +682,12 @@ int ea::ea_decode_slots(const Params& P, int* slots) {
     // blocks of the decode kernel resident on the current device at once (CUs x blocks per CU),
     // cached per device and row-block size
     static std::mutex mu;
-    static int cache[64][3] = {};
+    static int cache[64][2] = {};
     hipError_t e = decode_attrs();
     if (e != hipSuccess) return -100 - (int)e;
     int dev = 0;
     if ((e = hipGetDevice(&dev)) != hipSuccess) return -100 - (int)e;
-    const int ri = P.rb == 1 ? 0 : (P.rb == 2 ? 1 : 2);
+    const int ri = P.rb == 1 ? 0 : 1;
     std::lock_guard<std::mutex> lk(mu);
     if (dev < 0 || dev >= 64) return -1;
     if (!cache[dev][ri]) {

@@ -1289,7 +1289,12 @@ int make_plan(const ea_geometry* g, const ea_options* o, Plan* pl) {
     if (o->prefill_waves != 0 && o->prefill_waves != 4 && o->prefill_waves != 8) return -2;
     pl->grp = g->num_q_heads / g->num_kv_heads;
     pl->r_seg = g->num_tokens * pl->grp;
-    pl->rb = pl->r_seg >= 3 ? 4 : pl->r_seg;  // kernels exist for 1, 2 and 4 rows per block
+    // rows per block: the d = 128 decode kernel takes 1- or 2-row blocks (two waves per SIMD; a
+    // 4-row block needs more than 256 VGPRs, runs at one wave per SIMD and measured 4-14% slower
+    // on every multi-row shape: GQA 4 and 8 decode, 4-16 query tokens), the general split kernel
+    // 1, 2 or 4
+    const bool dec_rows = g->head_dim == 128 && g->head_dim_v == 128 && o->kernel != EA_KERNEL_GENERAL && !o->timers;
+    pl->rb = dec_rows ? std::min(pl->r_seg, 2) : (pl->r_seg >= 3 ? 4 : pl->r_seg);
     pl->nrb = (pl->r_seg + pl->rb - 1) / pl->rb;
     pl->nseg = g->num_seqs * g->num_kv_heads;
     pl->rows = (int64_t)g->num_seqs * g->num_tokens * g->num_q_heads;

@@ -1300,13 +1300,13 @@ int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int kernel, int* ntil
     // wider GQA group: speculative trees, chunked prefill) read each K/V tile once here, against
     // once per 1-4 rows in the decode kernel (C4: 0.82 ms here, 2.57 ms there)
     // Segments of 16-31 rows (verification of 8-15 draft tokens) come here too when there is
-    // enough work: measured on MI355X (contiguous K/V, graph replays), the int8 kernel beats the
-    // decode kernel's 4-row blocks by 9-14% at 16 rows with 64+ segments of 4K+ keys or 32+ of
-    // 8K+, and by 6-38% at 24 rows with 8K+ keys; with fewer or shorter segments the decode
-    // kernel is faster (up to 1.6x at 2K keys).
+    // enough work: measured on MI355X against the decode kernel's 2-row blocks (contiguous K/V,
+    // graph replays), the int8 kernel is 5-10% faster at 16 rows with 128+ segments or 64+ of
+    // 32K+ keys, and 20-47% faster at 24 rows with 8K+ keys on 16+ segments or 32K+ keys on any;
+    // with fewer or shorter segments the decode kernel is as fast or faster (up to 1.8x at 2K keys).
     const int64_t nseg = (int64_t)g.num_seqs * g.num_kv_heads;
-    const bool mid = r_seg >= 16 && ((nseg >= 64 && g.max_seq_len >= 4096) || (nseg >= 32 && g.max_seq_len >= 8192) ||
-                                     (r_seg >= 24 && g.max_seq_len >= 8192));
+    const bool mid = (r_seg >= 24 && g.max_seq_len >= 8192 && (nseg >= 16 || g.max_seq_len >= 32768)) ||
+                     (r_seg >= 16 && ((nseg >= 128 && g.max_seq_len >= 2048) || (nseg >= 64 && g.max_seq_len >= 32768)));
     if (!force && g.num_tokens < 64 && r_seg < PF_RPB && !mid) return 0;
     if (r_seg >= (1 << 30) || (int64_t)g.max_seq_len + 64 >= (1 << 30)) return 0;
     const int rpb = PF_RPB;
