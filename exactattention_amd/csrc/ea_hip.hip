@@ -736,7 +736,9 @@ __global__ void __launch_bounds__(EA_T2_THREADS) ea_tier2(Params P) {
         const int64_t jc0 = min(nkeys, (int64_t)chunk * csz), jc1 = min(nkeys, jc0 + csz);
         const int64_t nkc = jc1 - jc0;
         const int64_t obase = b * P.g.o_seq_stride + (int64_t)t * P.g.o_tok_stride + (int64_t)hq * P.g.o_head_stride;
+        // the flag starts at 0 before any wave can raise it (a NaN/inf q element below)
         if (tid == 0) S.flag = 0;
+        __syncthreads();
         const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
         for (int i = tid; i < d; i += EA_T2_THREADS) {
             uint32_t x = qr[i];
