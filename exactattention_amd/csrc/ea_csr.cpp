@@ -206,10 +206,14 @@ int attention_csr(const uint16_t* q, int64_t rows, int d, const uint16_t* k, con
     int rc = ea_hip_workspace_size(&g, &o, &ws_bytes, &ns);
     if (rc) return rc;
 
-    // q rows in token order (padding tokens zero)
+    // q rows in token order (padding tokens zero), and the host side of the results: every host
+    // buffer a copy reads or writes exists before the first copy is enqueued
     std::vector<uint16_t> qh((size_t)(BT * d), 0);
     for (int64_t i = 0; i < BT; ++i)
         if (L.tok_row[(size_t)i] >= 0) memcpy(&qh[(size_t)(i * d)], q + L.tok_row[(size_t)i] * d, (size_t)d * 2);
+    std::vector<unsigned char> oh((size_t)BT * dv * osz);
+    std::vector<uint8_t> fh((size_t)BT);
+    int64_t hs[16] = {};
 
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -241,6 +245,16 @@ int attention_csr(const uint16_t* q, int64_t rows, int d, const uint16_t* k, con
     }
     char* base = (char*)A.base;
     const hipStream_t st = A.stream;
+    // every way out after this point, an error or an exception included, first waits for the
+    // stream: no copy may still read or write a host buffer of this call, and no work may still use
+    // the arena when a later call regrows it
+    struct SyncOnExit {
+        hipStream_t s;
+        bool armed;
+        ~SyncOnExit() {
+            if (armed) (void)hipStreamSynchronize(s);
+        }
+    } guard{st, true};
 #define EA_TRY(x)                            \
     do {                                     \
         if ((e = (x)) != hipSuccess) return hip_rc(e); \
@@ -270,12 +284,10 @@ int attention_csr(const uint16_t* q, int64_t rows, int d, const uint16_t* k, con
     bf.flags = (uint8_t*)(base + o_fl);
     o.stats = (int64_t*)(base + o_st);
     if ((rc = ea_hip_attention(&g, &bf, &o, base + o_ws, ws_bytes, (ea_stream_t)st))) return rc;
-    std::vector<unsigned char> oh((size_t)BT * dv * osz);
-    std::vector<uint8_t> fh((size_t)BT);
-    int64_t hs[16];
     EA_TRY(hipMemcpyAsync(oh.data(), base + o_out, oh.size(), hipMemcpyDeviceToHost, st));
     EA_TRY(hipMemcpyAsync(fh.data(), base + o_fl, fh.size(), hipMemcpyDeviceToHost, st));
     EA_TRY(hipMemcpyAsync(hs, base + o_st, sizeof(hs), hipMemcpyDeviceToHost, st));
+    guard.armed = false;
     EA_TRY(hipStreamSynchronize(st));
 #undef EA_TRY
     for (int64_t i = 0; i < BT; ++i) {

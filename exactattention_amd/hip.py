@@ -303,10 +303,20 @@ def ea_attention_hip(q, k, v, alpha, row_ptr, key_idx, out="bf16", splits=8, acc
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
+    if q.ndim != 2 or k.ndim != 2 or v.ndim != 2:
+        raise ValueError("q, k and v must be 2-D arrays (rows x d, keys x d, keys x dv)")
     rows, d = q.shape
     n, dv = v.shape
+    if k.shape != (n, d):
+        raise ValueError(f"k has shape {k.shape}; q and v need ({n}, {d})")
     rp = np.ascontiguousarray(row_ptr, dtype=np.int64)
     ki = np.ascontiguousarray(key_idx, dtype=np.int64)
+    # the C entry point takes bare pointers: it reads row_ptr[0 .. rows] and the key_idx entries
+    # those delimit, so the lengths are checked here
+    if rp.shape != (rows + 1,):
+        raise ValueError(f"row_ptr must have rows + 1 = {rows + 1} entries, got shape {rp.shape}")
+    if ki.ndim != 1 or (rows > 0 and (rp[0] < 0 or rp[-1] > ki.shape[0])):
+        raise ValueError("key_idx must be 1-D and hold every entry row_ptr delimits")
     fp32 = out == "fp32"
     res = np.zeros((rows, dv), dtype=np.uint32 if fp32 else np.uint16)
     flags = np.zeros(rows, dtype=np.uint8)

@@ -379,3 +379,22 @@ def test_csr_layout_rejects_bad_lists():
         hip.csr_layout(np.array([0, 2, 1]), np.array([0, 1]), 5)       # decreasing row_ptr
     lay = hip.csr_layout(np.array([0, 0, 0]), np.zeros(0, np.int64), 5, arrays=True)
     assert lay["num_seqs"] == 0
+
+
+def test_drop_in_wrapper_checks_array_shapes():
+    """The C drop-in reads row_ptr[0 .. rows] and key_idx through bare pointers: the Python wrapper
+    refuses arrays whose lengths or shapes would make it read past them (before any device call)."""
+    from exactattention_amd import hip
+    _lib()
+    q = np.zeros((2, 8), np.uint16)
+    k = np.zeros((5, 8), np.uint16)
+    v = np.zeros((5, 4), np.uint16)
+    ki = np.array([0, 1, 2], np.int64)
+    with pytest.raises(ValueError):
+        hip.ea_attention_hip(q, k, v, 1.0, np.array([0, 3]), ki)        # row_ptr of 1 row for 2
+    with pytest.raises(ValueError):
+        hip.ea_attention_hip(q, k, v, 1.0, np.array([0, 1, 4]), ki)     # past the end of key_idx
+    with pytest.raises(ValueError):
+        hip.ea_attention_hip(q, k[:4], v, 1.0, np.array([0, 1, 3]), ki)  # k and v key counts differ
+    with pytest.raises(ValueError):
+        hip.ea_attention_hip(q.reshape(-1), k, v, 1.0, np.array([0, 1, 3]), ki)  # q not 2-D
