@@ -1676,9 +1676,9 @@ static int exact_rows_impl(const ea_geometry* g, const ea_buffers* bf, const ea_
         maxk = nk[i] > maxk ? nk[i] : maxk;
     }
     const size_t cap = (size_t)(d + maxk * (int64_t)(d + dv));
+    std::vector<uint16_t> host(cap);  // before the device buffer: a throw here leaks nothing
     uint16_t* stage = nullptr;
     if ((e = hipMalloc(&stage, cap * 2)) != hipSuccess) return herr(e);
-    std::vector<uint16_t> host(cap);
     const size_t osz = o->out_fp32 ? 4 : 2;
     int64_t fixed = 0, refused = 0, dom = 0;
     for (size_t i = 0; i < todo.size() && e == hipSuccess; ++i) {
