@@ -69,10 +69,9 @@ __device__ __forceinline__ void decode_body(Params P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     DecodeSmem<RB>& S = *reinterpret_cast<DecodeSmem<RB>*>(smem_raw);
 
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-        S.T1[i] = u64_as_f64(EA_T1_BITS[i]);
-        S.T2[i] = u64_as_f64(EA_T2_BITS[i]);
-    }
+    // the exp2 tables go to LDS from wave A, their global loads issued just before its first K
+    // DMA and their LDS writes after it (the two latencies overlap); first piece only
+    bool tables_due = true;
     // the decode kernel takes every row of the problem: one add for the whole grid
     if constexpr (STREAM)
         if (threadIdx.x == 0 && P.stats && blockIdx.x == 0) atomicAdd((unsigned long long*)&P.stats[9], (unsigned long long)P.rows);
@@ -288,7 +287,23 @@ __device__ __forceinline__ void decode_body(Params P) {
 
     if (role == 0) {
         // ============ wave A: K tiles, scores, certified logits and weights of rows [0, RA)
-        if (ntiles > 0) issue_k(k0, 0);
+        if (tables_due) {
+            uint64_t tb1[4], tb2[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                tb1[h] = EA_T1_BITS[lane + 64 * h];
+                tb2[h] = EA_T2_BITS[lane + 64 * h];
+            }
+            if (ntiles > 0) issue_k(k0, 0);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                S.T1[lane + 64 * h] = u64_as_f64(tb1[h]);
+                S.T2[lane + 64 * h] = u64_as_f64(tb2[h]);
+            }
+            tables_due = false;
+        } else if (ntiles > 0) {
+            issue_k(k0, 0);
+        }
         __syncthreads();  // tables visible
         for (int it = 0; it <= ntiles; ++it) {
             if (it < ntiles) {
