@@ -582,16 +582,33 @@ __device__ __forceinline__ void decode_body(Params P) {
 
     if constexpr (!STREAM) {
         // uniform splits: block (unit, split) takes keys [split split_len, (split + 1) split_len)
+        // The hardware deals consecutive workgroups to the 8 XCDs in turn, and each XCD has its own
+        // L2. A segment's row blocks (units seg * nrb .. seg * nrb + nrb - 1) read the same K/V
+        // tiles, so they are placed 8 block indices apart, all on one XCD and dispatched close
+        // together: block x runs unit ((x / 8) / nrb * 8 + x % 8) * nrb + (x / 8) % nrb (a
+        // permutation of the units when nseg % 8 == 0; units % 8 == 0 keeps the split rows
+        // aligned). Measured on GQA 4 and 8 decode and 4-token steps: 5-17% faster, same bits.
         const int k0 = (int)blockIdx.y * P.split_len;
-        piece((int)blockIdx.x, (int)blockIdx.y, k0, k0 + P.split_len);
+        int item = (int)blockIdx.x;
+        if (P.nrb > 1 && (P.nseg & 7) == 0) {
+            const int lo = item & 7, hi = item >> 3;
+            item = ((hi / P.nrb) * 8 + lo) * P.nrb + hi % P.nrb;
+        }
+        piece(item, (int)blockIdx.y, k0, k0 + P.split_len);
         return;
     }
     // Block g's share of the step's tiles (the plan the prep kernel's planner block wrote): its
     // intersections with the units, in unit order, one piece each. The first comes from the
     // block's record (unit, S_u, S_(u+1), share) in one load.
-    const int4 rec = ((const int4*)(P.dq_plan + P.dq_rec_off))[blockIdx.x];
+    // Each XCD takes a contiguous eighth of the shares (share g runs on workgroup (g % (G/8)) * 8 +
+    // g / (G/8)) when units span fewer than 8 shares on average: a segment's row-block units are
+    // then neighbours on one XCD's L2. Units of 8 or more shares already put the same tiles of
+    // neighbouring units 8 workgroups apart, on one XCD, and measured 3-5% slower remapped.
+    int gb = (int)blockIdx.x;
+    if (P.nrb > 1 && (P.dq_blocks & 7) == 0 && (int64_t)P.dq_units * 8 > P.dq_blocks)
+        gb = (gb & 7) * (P.dq_blocks >> 3) + (gb >> 3);
+    const int4 rec = ((const int4*)(P.dq_plan + P.dq_rec_off))[gb];
     const int W = P.dq_plan[0];
-    const int gb = blockIdx.x;
     int u = rec.x;
     const int share = rec.w;
     if (u >= P.dq_units || share <= 0) return;  // past the last share: no tile

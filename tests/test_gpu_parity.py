@@ -895,3 +895,34 @@ def test_decode_equal_share_plan(gpu, case):
     # one step with a split count the caller fixes (uniform splits when it fits one round)
     got2, flags2, st2 = _run(prob, ab, splits=1)
     assert np.array_equal(got2, want) and not flags2.any()
+
+
+@pytest.mark.parametrize("case", ["uniform", "equal_share"])
+def test_decode_xcd_placement(gpu, case):
+    """GQA 4 decode (2-row blocks, 2 units per segment, segments a multiple of 8): the decode
+    kernel places a segment's row blocks on one XCD, on the uniform split grid and, with more
+    units than an eighth of the equal-share plan's blocks, by a permutation of the shares. The
+    work moves between workgroups only: bits equal the general split kernel's on the same problem
+    (ragged lengths, paged NHD) and, on the uniform case, the oracle's."""
+    rng = np.random.default_rng(91 if case == "uniform" else 92)
+    ab = default_alpha_bits(128)
+    if case == "uniform":
+        B, S, page = 4, 1500, 16          # 32 segments x 2 row blocks, uniform splits
+    else:
+        B, S, page = 16, 9500, 64         # 128 segments x 2 row blocks, 8 splits: equal-share plan
+    Hq, Hkv = 32, 8
+    lens = rng.integers(S // 3, S + 1, size=B)
+    q = bf16(rng, (B, 1, Hq, 128))
+    k = bf16(rng, (B, Hkv, S, 128), "outlier")
+    v = bf16(rng, (B, Hkv, S, 128))
+    base = problem.contiguous(q, k, v, lens.reshape(B, 1), seq_len=lens)
+    prob = problem.to_paged(base, page, rng, "NHD")
+    got, flags, st = _run(prob, ab)
+    assert st["decode_kernel_rows"] > 0 and not flags.any(), st
+    assert st["decode_equal_share_steps"] == (1 if case == "equal_share" else 0), st
+    ref, flags2, st2 = _run(prob, ab, kernel="general")
+    assert st2["decode_kernel_rows"] == 0 and not flags2.any()
+    assert np.array_equal(got, ref)
+    if case == "uniform":
+        want, _ = _oracle(prob, ab)
+        assert np.array_equal(got, want)
