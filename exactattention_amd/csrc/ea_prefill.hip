@@ -1298,15 +1298,15 @@ int ea::ea_prefill_eligible(const ea_geometry& g, int grp, int kernel, int* ntil
     const int64_t r_seg = (int64_t)g.num_tokens * grp;
     // Rows of one (sequence, KV head) that fill a 32-row block (64 tokens, or fewer tokens with a
     // wider GQA group: speculative trees, chunked prefill) read each K/V tile once here, against
-    // once per 1-4 rows in the decode kernel (C4: 0.82 ms here, 2.57 ms there)
-    // Segments of 16-31 rows (verification of 8-15 draft tokens) come here too when there is
-    // enough work: measured on MI355X against the decode kernel's 2-row blocks (contiguous K/V,
-    // graph replays), the int8 kernel is 5-10% faster at 16 rows with 128+ segments or 64+ of
-    // 32K+ keys, and 20-47% faster at 24 rows with 8K+ keys on 16+ segments or 32K+ keys on any;
-    // with fewer or shorter segments the decode kernel is as fast or faster (up to 1.8x at 2K keys).
+    // once per 1-2 rows in the decode kernel (C4: 0.82 ms here, 2.57 ms there with 4-row blocks)
+    // Segments of 24-31 rows (verification of 12-15 draft tokens at GQA 2) come here too when
+    // there is enough work: measured on MI355X against the decode kernel (2-row blocks, a
+    // segment's row blocks on one XCD; contiguous K/V, graph replays), the int8 kernel is 14-45%
+    // faster at 24 rows with 8K+ keys on 16+ segments or 32K+ keys on any; at 16 rows the decode
+    // kernel is as fast or faster everywhere measured (up to 1.9x at 2K keys, within 3% at 64
+    // segments of 32K keys).
     const int64_t nseg = (int64_t)g.num_seqs * g.num_kv_heads;
-    const bool mid = (r_seg >= 24 && g.max_seq_len >= 8192 && (nseg >= 16 || g.max_seq_len >= 32768)) ||
-                     (r_seg >= 16 && ((nseg >= 128 && g.max_seq_len >= 2048) || (nseg >= 64 && g.max_seq_len >= 32768)));
+    const bool mid = r_seg >= 24 && g.max_seq_len >= 8192 && (nseg >= 16 || g.max_seq_len >= 32768);
     if (!force && g.num_tokens < 64 && r_seg < PF_RPB && !mid) return 0;
     if (r_seg >= (1 << 30) || (int64_t)g.max_seq_len + 64 >= (1 << 30)) return 0;
     const int rpb = PF_RPB;
