@@ -493,6 +493,48 @@ def tree_line(steps: int, warmup: int) -> dict:
     return line
 
 
+GQA_SHAPES = [(32, 8, 8, 4096), (32, 8, 32, 16384), (64, 8, 4, 8192), (64, 8, 32, 4096)]  # (Hq, Hkv, B, n)
+
+
+def gqa_line(steps: int, warmup: int) -> dict:
+    """Decode at GQA 4 and 8 (32 or 64 query heads on 8 KV heads, one token per sequence: the
+    decode kernel in 2-row blocks, a segment's 2 or 4 row blocks on one XCD), bf16 N(0,1) data
+    drawn on the device (torch, seed 2024), contiguous K/V, the step as a HIP-graph replay. GB/s
+    over the bf16 K+V bytes; the bits must equal a one-split run's."""
+    import torch
+    from exactattention_amd import configs, problem
+    from exactattention_amd.hip import STATS, DeviceProblem, launch_hip
+    ab = configs.alpha_bits()
+    d = 128
+    out = []
+    for Hq, Hkv, B, n in GQA_SHAPES:
+        gen = torch.Generator(device="cuda:0").manual_seed(2024)
+        q = torch.randn((B, 1, Hq, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        k = torch.randn((B, Hkv, n, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        v = torch.randn((B, Hkv, n, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+        g = problem._geom(B, 1, Hq, Hkv, d, d, (Hq * d, Hq * d, d), (Hq * d, Hq * d, d),
+                          (Hkv * n * d, d, n * d), (Hkv * n * d, d, n * d), 1, 0, n)
+        prob = dict(geom=g, q=q, k=k, v=v, seq_len=np.full(B, n, np.int32), kv_len=np.full(B, n, np.int32),
+                    block_table=None, block_table_offset=None, tree_mask=None, tree_base=None,
+                    out_shape=(B, 1, Hq, d))
+        one = DeviceProblem(prob, "bf16", 1, "cuda:0")
+        launch_hip(one, ab)
+        torch.cuda.synchronize()
+        want = one.out.cpu().numpy().view(np.uint16)
+        del one
+        dp = DeviceProblem(prob, "bf16", 0, "cuda:0")
+        ms, got = graph_steps(dp, ab, steps, warmup)
+        st = dict(zip(STATS, dp.stats.cpu().numpy().tolist()))
+        kv_bytes = 2 * B * Hkv * n * d * 2
+        out.append({"shape": f"GQA {Hq // Hkv} ({Hq}/{Hkv} heads) B={B} n={n}", "ms": round(ms, 5),
+                    "kv_gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1), "nsplit": dp.nsplit,
+                    "equal_share_plan": bool(st["decode_equal_share_steps"]),
+                    "bits_equal_one_split": bool(np.array_equal(got, want)), "rows_flagged": int(st["tier1_flagged"])})
+        del dp, prob, q, k, v
+        torch.cuda.empty_cache()
+    return {"basis": "HIP-graph replays (events around them); bf16 K+V bytes only", "shapes": out}
+
+
 def exact_tier_line(reps: int = 3) -> dict:
     """What a row that tier 1 leaves costs on the device tier 2: ea_options.force_tier2 lists every
     row, on one row of 32,768 keys (tier 2 splits its keys over its 32 blocks) and on 32 such rows
@@ -747,7 +789,8 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill measurement")
-    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving", "shapes", "drop_in", "exact_tier"), default=None,
+    ap.add_argument("--only", choices=("C2", "C3", "C4", "C5", "serving", "shapes", "drop_in", "exact_tier", "gqa"),
+                    default=None,
                     help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
                     help="after the timed steps, run 5 steps of the phase-clock build and report it")
@@ -779,6 +822,9 @@ def main():
         return
     if args.only == "C5":
         print(json.dumps({"long_context": long_context_line(args.steps, args.warmup)}), flush=True)
+        return
+    if args.only == "gqa":
+        print(json.dumps({"gqa": gqa_line(args.steps, args.warmup)}), flush=True)
         return
     if args.only == "exact_tier":
         print(json.dumps({"exact_tier": exact_tier_line()}), flush=True)
@@ -852,6 +898,7 @@ def main():
         line["serving"] = serving_line(prob, ab, max(5, min(args.steps, 20)))
         line["published_shapes"] = published_shapes_line(max(5, min(args.steps, 20)), 2)
         line["exact_tier"] = exact_tier_line()
+        line["gqa"] = gqa_line(max(5, min(args.steps, 20)), 2)
     if args.only is None and not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         csr = c2_csr(prob)
