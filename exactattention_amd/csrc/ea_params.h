@@ -63,7 +63,7 @@ struct Params {
     uint8_t* pfkv;    // nseg * pf_ntiles * EA_PF_TILE_BYTES: K/V digit tiles and tile metadata
     double* pfscr;    // nseg * pf_nrb * 512 lanes * 32: per-lane sums of completed epochs
     int32_t pf_ntiles;  // 64-key tiles per segment
-    int32_t pf_nrb;     // 64-row blocks per segment
+    int32_t pf_nrb;     // 32-row blocks per segment
     // digit-tile cache (ea_hip_kv_digits_update): with kvd_begin set, ea_pf_kvslice re-slices the
     // tiles that hold keys [kvd_begin[b], kvd_end[b]) of each sequence, kvd_span tiles per segment
     const int32_t* kvd_begin;

@@ -1,5 +1,5 @@
-// Device helpers shared by the int8-MFMA prefill kernels (ea_prefill.hip: 32-row blocks,
-// ea_prefill64.hip: 64-row blocks): tile DMA and barrier primitives, the score MFMAs and
+// Device helpers of the int8-MFMA prefill kernel (ea_prefill.hip, 32-row blocks): tile DMA and
+// barrier primitives, the score MFMAs and
 // their fp64 fold, the branch-free certified logit and weight, and the exact per-pair path.
 #pragma once
 #include <hip/hip_runtime.h>

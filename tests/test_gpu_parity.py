@@ -485,7 +485,7 @@ def test_decode_kernel_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
 
 
 # ---------------------------------------------------------------------------------------------
-# the int8-MFMA prefill kernel (64 rows per block, balanced radix-256 digits)
+# the int8-MFMA prefill kernel (32 rows per block, balanced radix-256 digits)
 # ---------------------------------------------------------------------------------------------
 
 def _rows(prob):
