@@ -1,6 +1,6 @@
 // Device helpers of the int8-MFMA prefill kernel (ea_prefill.hip, 32-row blocks): tile DMA and
-// barrier primitives, the score MFMAs and
-// their fp64 fold, the branch-free certified logit and weight, and the exact per-pair path.
+// barrier primitives, the score MFMAs and their fp64 fold, the branch-free certified logit and
+// weight, and the exact per-pair path.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
