@@ -398,3 +398,23 @@ def test_drop_in_wrapper_checks_array_shapes():
         hip.ea_attention_hip(q, k[:4], v, 1.0, np.array([0, 1, 3]), ki)  # k and v key counts differ
     with pytest.raises(ValueError):
         hip.ea_attention_hip(q.reshape(-1), k, v, 1.0, np.array([0, 1, 3]), ki)  # q not 2-D
+
+
+def test_kernel_choice_for_verification_segments():
+    """The int8 kernel takes segments of 24-31 rows (12-15 draft tokens at GQA 2) with 8K+ keys on
+    16+ segments, or 32K+ keys on any; 16-23 rows stay on the decode kernel at any length, and so do
+    24-row segments with fewer keys (host logic of the kernel choice, seen through the digit-cache
+    query)."""
+    fake = 4096
+
+    def geom(tokens, seqs, keys):
+        return _c2_geom(num_tokens=tokens, num_seqs=seqs, max_seq_len=keys, q_tok_stride=16 * 128,
+                        q_seq_stride=tokens * 16 * 128, o_tok_stride=16 * 128, o_seq_stride=tokens * 16 * 128)
+
+    assert _reads_digits(geom(12, 32, 8192), fake) == (0, 1)     # 24 rows, 256 segments, 8K keys
+    assert _reads_digits(geom(12, 2, 8192), fake) == (0, 1)      # 16 segments
+    assert _reads_digits(geom(12, 32, 4096), fake) == (0, 0)     # 24 rows, 4K keys: decode
+    assert _reads_digits(geom(12, 1, 16384), fake) == (0, 0)     # 8 segments, 16K keys: decode
+    assert _reads_digits(geom(12, 1, 32768), fake) == (0, 1)     # 8 segments, 32K keys
+    assert _reads_digits(geom(8, 32, 65536), fake) == (0, 0)     # 16 rows: decode at any length
+    assert _reads_digits(geom(16, 1, 1024), fake) == (0, 1)      # 32 rows: always the int8 kernel
