@@ -926,3 +926,31 @@ def test_decode_xcd_placement(gpu, case):
     if case == "uniform":
         want, _ = _oracle(prob, ab)
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", [301, 302, 303, 304, 305, 306])
+def test_decode_placement_random_many_segments(gpu, seed):
+    """Seeded geometries with 128-256 segments (8 KV heads) and 2-8 row blocks per segment, ragged
+    lengths, pages of 16 or 64 keys, 1 or 2 tokens: the decode kernel, its row blocks placed by
+    XCD on the uniform grid or the equal-share plan (whichever the step takes), gives the general
+    split kernel's bits, every row certified."""
+    rng = np.random.default_rng(seed)
+    ab = default_alpha_bits(128)
+    Hkv = 8
+    grp = int(rng.choice([2, 4, 8]))
+    T = int(rng.choice([1, 2]))
+    B = int(rng.choice([16, 24, 32]))
+    S = int(rng.integers(1500, 9001))
+    lens = rng.integers(S // 4, S + 1, size=B)
+    kv = np.stack([np.clip(lens[b] - T + 1 + np.arange(T), 0, None) for b in range(B)])
+    q = bf16(rng, (B, T, Hkv * grp, 128))
+    k = bf16(rng, (B, Hkv, S, 128), str(rng.choice(["normal", "outlier", "wide"])))
+    v = bf16(rng, (B, Hkv, S, 128))
+    base = problem.contiguous(q, k, v, kv, seq_len=lens)
+    prob = problem.to_paged(base, int(rng.choice([16, 64])), rng, "NHD")
+    got, flags, st = _run(prob, ab)
+    desc = f"seed {seed}: B={B} T={T} grp={grp} S={S} {st}"
+    assert st["decode_kernel_rows"] > 0 and not flags.any(), desc
+    ref, flags2, st2 = _run(prob, ab, kernel="general")
+    assert not flags2.any(), desc
+    assert np.array_equal(got, ref), desc
