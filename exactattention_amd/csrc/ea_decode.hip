@@ -9,7 +9,9 @@
 //           round trip), 16-byte chunks XOR-swizzled by key so per-key reads are conflict-free;
 //           double-buffered, tile i+1 in flight while tile i is processed.
 //   S       lane = key: two fp64 FMA chains per row over the 128 dims, q as SGPR operands
-//           (scalar loads of the prep kernel's fp64 q). Rounding error of the chains is bounded
+//           (scalar loads of the fp64 q: on uniform splits wave A converts the block's bf16 q
+//           rows itself before the first barrier, which takes the prep kernel off the step;
+//           the stream plan keeps the prep kernel). Rounding error of the chains is bounded
 //           by 66 u sum_b |q_b|_1 |k_b|_inf over four 32-dim blocks (|k_b|_inf from v_max3_f32
 //           on the fp32 patterns the conversion makes anyway).
 //   B       lane = key, every row: certified t = RN32(alpha s) from the interval, RN24(2^t)
@@ -46,6 +48,7 @@ struct DecodeSmem {
     double2 sb[2][DT][RBB];  // (score, error bound) of wave B's rows; wave B overwrites .x with the weight
     double sc[2][RA];        // rescale of wave A's rows' running P.V sums before that tile
     double T1[256], T2[256];
+    int qbad[RB];  // uniform splits: the NaN/inf flag of each row's q, computed by wave A
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -94,6 +97,10 @@ __device__ __forceinline__ void decode_body(Params P) {
     cint_t* kvl4 = (cint_t*)P.kv_len;
     cint_t* qinfo4 = (cint_t*)P.qinfo;
     cdouble_t* qn4 = (cdouble_t*)P.qn;
+    // the fp64 q rows (written in this kernel on uniform splits): every read goes through this
+    // base, which is handed out again by an empty asm after the barrier that follows the writes,
+    // so no load through it can be scheduled before them
+    cdouble_t* q64b = (cdouble_t*)P.q64;
     // rows of the block (a short block repeats its last row; repeats are never written). Key
     // positions, lengths and row indices fit 31 bits (checked by the launcher).
     int grow[RB];
@@ -114,7 +121,8 @@ __device__ __forceinline__ void decode_body(Params P) {
         int e = kvl[r];
         if (tmk[r]) e = max(e, tb + 64 - (int)__clzll(tmk[r]));
         kend = max(kend, e);
-        rflag[r] = qinfo4[grow[r] * 5 + 4] ? 1 : 0;
+        if constexpr (STREAM) rflag[r] = qinfo4[grow[r] * 5 + 4] ? 1 : 0;
+        else rflag[r] = 0;  // set once wave A has converted the rows' q
     }
     const int slen = ((cint_t*)P.seq_len)[b];
     if (kend > slen) kend = slen;
@@ -266,8 +274,8 @@ __device__ __forceinline__ void decode_body(Params P) {
         *fout = f;
         return om;
     };
-    // q row r's fp64 values (prep kernel), for the exact path
-    auto qrow64 = [&](int r) __attribute__((always_inline)) { return (cdouble_t*)P.q64 + (int64_t)grow[r] * EA_MAXD; };
+    // q row r's fp64 values (the prep kernel's, or on uniform splits wave A's), for the exact path
+    auto qrow64 = [&](int r) __attribute__((always_inline)) { return q64b + (int64_t)grow[r] * EA_MAXD; };
 
     // R, Z and the visible count (-1: flagged) of rows [r0, r1) into the split partial
     auto publish_rows = [&](int r0, int r1) __attribute__((always_inline)) {
@@ -287,6 +295,20 @@ __device__ __forceinline__ void decode_body(Params P) {
 
     if (role == 0) {
         // ============ wave A: K tiles, scores, certified logits and weights of rows [0, RA)
+        // uniform splits: this block converts its rows' q (the prep kernel's work for these rows;
+        // every split's block stores the same values), the loads issued before the first K DMA
+        uint32_t qx[RB][2];
+        if constexpr (!STREAM) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const int64_t row = grow[r];
+                const int64_t bb = row / ((int64_t)P.g.num_tokens * P.g.num_q_heads);
+                const int tt = (int)((row / P.g.num_q_heads) % P.g.num_tokens), hq = (int)(row % P.g.num_q_heads);
+                const uint16_t* qr = P.q + bb * P.g.q_seq_stride + (int64_t)tt * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
+                qx[r][0] = qr[2 * lane];
+                qx[r][1] = qr[2 * lane + 1];
+            }
+        }
         if (tables_due) {
             uint64_t tb1[4], tb2[4];
 #pragma unroll
@@ -304,7 +326,23 @@ __device__ __forceinline__ void decode_body(Params P) {
         } else if (ntiles > 0) {
             issue_k(k0, 0);
         }
+        if constexpr (!STREAM) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                if (r >= nrow) {  // a repeat of the last row: its flag
+                    rflag[r] = rflag[r - 1];
+                    continue;
+                }
+                const int bad = prep_row_store(P, grow[r], lane, qx[r][0], qx[r][1]);
+                rflag[r] = bad;
+                if (lane == 0) S.qbad[r] = bad;
+            }
+            // the step's first kernel on this path clears the tier-2 work list and chunk counts
+            if (item == 0 && split == 0 && lane <= EA_T2_BLOCKS) P.wl_cnt[lane] = 0;
+            wait_vm<0>();  // the q stores are complete before the barrier
+        }
         __syncthreads();  // tables visible
+        asm volatile("" : "+s"(q64b), "+s"(qn4));
         for (int it = 0; it <= ntiles; ++it) {
             if (it < ntiles) {
                 const int buf = it & 1;
@@ -335,7 +373,7 @@ __device__ __forceinline__ void decode_body(Params P) {
                 typedef const double* dptr;
                 dptr qrow[RB];
     #pragma unroll
-                for (int r = 0; r < RB; ++r) qrow[r] = P.q64 + (int64_t)grow[r] * EA_MAXD;
+                for (int r = 0; r < RB; ++r) qrow[r] = (const double*)q64b + (int64_t)grow[r] * EA_MAXD;
                 // hands out copies of the row pointers that the compiler cannot see through
                 auto gate = [&](dptr (&o)[RB]) __attribute__((always_inline)) {
                     if constexpr (RB == 1) {
@@ -538,6 +576,10 @@ __device__ __forceinline__ void decode_body(Params P) {
         // each tile (its weights are published by then) and one after the last. Straight-line
         // pairs keep vA and vB free of merges (no register copies).
         __syncthreads();  // prologue barrier (tables visible)
+        asm volatile("" : "+s"(q64b), "+s"(qn4));
+        if constexpr (!STREAM)
+#pragma unroll
+            for (int r = RA; r < RB; ++r) rflag[r] = S.qbad[min(r, nrow - 1)];
         int t = 0;
         for (; t + 1 < ntiles; t += 2) {
             __syncthreads();

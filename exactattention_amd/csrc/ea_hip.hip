@@ -1,7 +1,8 @@
 // Certified split-KV ExactAttention for AMD Instinct MI355X (gfx950): kernels and C ABI.
 //
 // One step is four launches on the caller's stream, with fixed grids and no memsets:
-//   ea_prep      q rows -> fp64 + exponent ranges; clears the tier-2 work counter
+//   ea_prep      q rows -> fp64 + exponent ranges; clears the tier-2 work counter (the decode
+//                kernel on uniform splits does both itself, and the step is three launches)
 //   ea_split     tier 1: per (segment, row block, KV split) an fp64 pass over 64-key tiles:
 //                exact scores (checked), certified logits and weights, P.V partials with
 //                rigorous error bounds. Writes one partial per (split, row).
@@ -29,10 +30,9 @@
 using namespace ea;
 
 // ------------------------------------------------------------------------------------------------
-// Kernel 1: q rows to fp64 plus per-32-dim-block exponent ranges. One wave per row.
-// qinfo[row*5 + blk] = (FQmax << 16) | FQmin' over the nonzero elements of dims [32 blk, 32 blk+32)
-// (FQmin' = max(field, 1): a subnormal's lsb is that of field 1), 0x80000000 for an all-zero block;
-// qinfo[row*5 + 4] = 1 when the row holds a NaN/inf.
+// Kernel 1: q rows to fp64 plus per-32-dim-block exponent ranges and |q| sums (prep_row_store),
+// one wave per row; block 0 clears the tier-2 work list, and on the decode kernel's stream plan an
+// extra last block writes that plan.
 // ------------------------------------------------------------------------------------------------
 // The decode kernel's equal-share plan (Params::dq_*), by one 256-thread block: per unit its tile
 // count (up to unit_kend, at most dq_max_tiles), the exclusive prefix sums S_u with S_units = W, the
@@ -99,44 +99,9 @@ __global__ void __launch_bounds__(256) ea_prep(Params P) {
     int64_t b = row / ((int64_t)T * Hq);
     int t = (int)((row / Hq) % T), hq = (int)(row % Hq);
     const uint16_t* qr = P.q + b * P.g.q_seq_stride + (int64_t)t * P.g.q_tok_stride + (int64_t)hq * P.g.q_head_stride;
-    // the four 32-dim blocks at once: lanes 16 blk .. 16 blk + 15 take dims 32 blk + 2 (lane & 15)
-    // and the next one, and each 16-lane group reduces its block
-    const int blk = lane >> 4;
-    int bad = 0, fmax = 0, fmin = 0x1FF;
-    double aq = 0.0;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = blk * 32 + 2 * (lane & 15) + h;
-        if (i < d) {
-            const uint32_t x = qr[i];
-            const double qv = (double)__uint_as_float(x << 16);
-            P.q64[row * EA_MAXD + i] = qv;
-            aq += fabs(qv);
-            const int f = (x >> 7) & 0xFF;
-            if (f == 0xFF) bad = 1;
-            if (x & 0x7FFF) {
-                fmax = max(fmax, f);
-                fmin = min(fmin, max(f, 1));
-            }
-        } else {
-            P.q64[row * EA_MAXD + i] = 0.0;
-        }
-    }
-    // sum |q_i| over the block: <= 32 roundings of relative size 2^-53 each in any order, so
-    // scaling the fp64 sum by (1 + 2^-40) gives an upper bound (NaN/inf propagate; the row is
-    // flagged)
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        fmax = max(fmax, __shfl_xor(fmax, o, 64));
-        fmin = min(fmin, __shfl_xor(fmin, o, 64));
-        aq += __shfl_xor(aq, o, 64);
-    }
-    if ((lane & 15) == 0) {
-        P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
-        P.qn[row * 4 + blk] = aq * (1.0 + 0x1p-40);
-    }
-    bad = wave_max_i(bad);
-    if (lane == 0) P.qinfo[row * 5 + 4] = bad;
+    // dims past d enter as +0 (stored as 0.0, no exponent, no flag)
+    const uint32_t x0 = 2 * lane < d ? qr[2 * lane] : 0u, x1 = 2 * lane + 1 < d ? qr[2 * lane + 1] : 0u;
+    (void)prep_row_store(P, row, lane, x0, x1);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1570,9 +1535,12 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
         }
         return mark(4);
     }
-    hipLaunchKernelGGL(ea_prep, dim3(rb4 + (P.dq_stream ? 1u : 0u)), dim3(256), 0, st, P);
-    rc = herr(hipGetLastError());
-    if (rc) return rc;
+    // the decode kernel on uniform splits prepares its own rows' q (and clears the work list)
+    if (!(use_decode && !P.dq_stream)) {
+        hipLaunchKernelGGL(ea_prep, dim3(rb4 + (P.dq_stream ? 1u : 0u)), dim3(256), 0, st, P);
+        rc = herr(hipGetLastError());
+        if (rc) return rc;
+    }
     if (pl.nseg > 0) {
         static std::once_flag once;
         static hipError_t attr_err = hipSuccess;

@@ -277,4 +277,44 @@ int ea_launch_kv_digits(const Params& P, hipStream_t st);
 typedef const double __attribute__((address_space(4))) cdouble_t;
 typedef const int32_t __attribute__((address_space(4))) cint_t;
 
+// q row `row` prepared by one wave from its bf16 elements x[h] = q[2 lane + h] (dims past the head
+// dimension passed as +0): the fp64 row, per 32-dim block (lanes 16 blk .. 16 blk + 15, each
+// 16-lane group reduces its block) qinfo[row*5 + blk] = (FQmax << 16) | FQmin' over the nonzero
+// elements (FQmin' = max(field, 1): a subnormal's lsb is that of field 1), 0x80000000 for an
+// all-zero block, and qn[row*4 + blk] = an upper bound of sum |q_i| (the fp64 sum has at most 32
+// roundings of relative size 2^-53 in any order, so times 1 + 2^-40 bounds it; NaN/inf propagate),
+// and qinfo[row*5 + 4] = the NaN/inf flag, which it also returns (the same in every lane).
+__device__ __forceinline__ int prep_row_store(const Params& P, int64_t row, int lane, uint32_t x0, uint32_t x1) {
+    const int blk = lane >> 4;
+    const uint32_t x[2] = {x0, x1};
+    int bad = 0, fmax = 0, fmin = 0x1FF;
+    double aq = 0.0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = 2 * lane + h;
+        const double qv = (double)__uint_as_float(x[h] << 16);
+        P.q64[row * EA_MAXD + i] = qv;
+        aq += fabs(qv);
+        const int f = (x[h] >> 7) & 0xFF;
+        if (f == 0xFF) bad = 1;
+        if (x[h] & 0x7FFF) {
+            fmax = max(fmax, f);
+            fmin = min(fmin, max(f, 1));
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        fmax = max(fmax, __shfl_xor(fmax, o, 64));
+        fmin = min(fmin, __shfl_xor(fmin, o, 64));
+        aq += __shfl_xor(aq, o, 64);
+    }
+    if ((lane & 15) == 0) {
+        P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
+        P.qn[row * 4 + blk] = aq * (1.0 + 0x1p-40);
+    }
+    bad = wave_max_i(bad);
+    if (lane == 0) P.qinfo[row * 5 + 4] = bad;
+    return bad;
+}
+
 }  // namespace ea
