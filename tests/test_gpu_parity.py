@@ -484,6 +484,42 @@ def test_decode_kernel_nonfinite_flags_exactly_the_rows_that_see_them(gpu):
                 assert np.array_equal(got[0, t, h], want[0, t, h]), (t, h)
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_decode_kernel_converts_q_rows_itself(gpu, splits):
+    """On the uniform grid the decode kernel converts its blocks' q rows (no prep launch): a NaN q
+    row alone in the last, partial 2-row block of a segment (3 rows per segment), a -inf element
+    in the first row of another block, and a q row of zeros, with 1, 2 and 4 splits writing the
+    same converted rows. Exactly the non-finite rows are flag 2 and every other row equals the
+    oracle; the clean q on the same geometry then leaves no flag."""
+    rng = np.random.default_rng(4242 + splits)
+    B, T, H, S = 2, 3, 2, 300
+    prob = _rand_problem(rng, "normal", "normal", B=B, T=T, Hq=H, Hkv=H, S=S, d=128, dv=128)
+    prob["q"][0, 2, 1, 7] = 0x7FC0     # NaN: segment (0, 1), row 2 (the partial block's only row)
+    prob["q"][1, 0, 0, 100] = 0xFF80   # -inf: segment (1, 0), row 0
+    prob["q"][1, 1, 1, :] = 0          # zeros: uniform weights
+    bad = {(0, 2, 1), (1, 0, 0)}
+    clean = {**prob, "q": prob["q"].copy()}
+    for b, t, h in bad:
+        clean["q"][b, t, h, :] = 0
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(clean, ab)
+    got, flags, st = _run(prob, ab, splits=splits)
+    assert st["decode_kernel_rows"] > 0 and st["decode_equal_share_steps"] == 0, st
+    fl = flags.reshape(B, T, H)
+    for b in range(B):
+        for t in range(T):
+            for h in range(H):
+                if (b, t, h) in bad:
+                    assert fl[b, t, h] == 2, (b, t, h, flags)
+                else:
+                    assert fl[b, t, h] == 0, (b, t, h, flags)
+                    assert np.array_equal(got[b, t, h], want[b, t, h]), (b, t, h)
+    # the clean problem on the same geometry: no flag survives from the previous q rows
+    got2, flags2, _ = _run(clean, ab, splits=splits)
+    assert not np.any(flags2)
+    assert np.array_equal(got2, want)
+
+
 # ---------------------------------------------------------------------------------------------
 # the int8-MFMA prefill kernel (32 rows per block, balanced radix-256 digits)
 # ---------------------------------------------------------------------------------------------
