@@ -48,7 +48,11 @@ struct DecodeSmem {
     double2 sb[2][DT][RBB];  // (score, error bound) of wave B's rows; wave B overwrites .x with the weight
     double sc[2][RA];        // rescale of wave A's rows' running P.V sums before that tile
     double T1[256], T2[256];
-    int qbad[RB];  // uniform splits: the NaN/inf flag of each row's q, computed by wave A
+    // uniform splits, computed by wave A: each row's q NaN/inf flag and its per-32-dim-block
+    // |q| bounds (the score bound reads them here: two rows share a line of the qn array, and a
+    // scalar load of it could hold another block's row from before that block stored it)
+    double qnb[RB][4];
+    int qbad[RB];
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -327,22 +331,23 @@ __device__ __forceinline__ void decode_body(Params P) {
             issue_k(k0, 0);
         }
         if constexpr (!STREAM) {
+            double qb = 0.0;
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
-                if (r >= nrow) {  // a repeat of the last row: its flag
+                if (r >= nrow) {  // a repeat of the last row: its flag and bounds
                     rflag[r] = rflag[r - 1];
-                    continue;
+                } else {
+                    rflag[r] = prep_row_store(P, grow[r], lane, qx[r][0], qx[r][1], &qb);
+                    if (lane == 0) S.qbad[r] = rflag[r];
                 }
-                const int bad = prep_row_store(P, grow[r], lane, qx[r][0], qx[r][1]);
-                rflag[r] = bad;
-                if (lane == 0) S.qbad[r] = bad;
+                if ((lane & 15) == 0) S.qnb[r][lane >> 4] = qb;
             }
             // the step's first kernel on this path clears the tier-2 work list and chunk counts
             if (item == 0 && split == 0 && lane <= EA_T2_BLOCKS) P.wl_cnt[lane] = 0;
             wait_vm<0>();  // the q stores are complete before the barrier
         }
         __syncthreads();  // tables visible
-        asm volatile("" : "+s"(q64b), "+s"(qn4));
+        asm volatile("" : "+s"(q64b));
         for (int it = 0; it <= ntiles; ++it) {
             if (it < ntiles) {
                 const int buf = it & 1;
@@ -452,9 +457,11 @@ __device__ __forceinline__ void decode_body(Params P) {
             for (int r = 0; r < RB; ++r) {
                 __builtin_amdgcn_sched_barrier(0);  // one row at a time (bounded live temporaries)
                 const double s = a0[r] + a1[r];
-                const double bnd = __fma_rn(qn4[grow[r] * 4 + 0], (double)km[0],
-                                    __fma_rn(qn4[grow[r] * 4 + 1], (double)km[1],
-                                    __fma_rn(qn4[grow[r] * 4 + 2], (double)km[2], qn4[grow[r] * 4 + 3] * (double)km[3])));
+                double qn_[4];
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) qn_[i] = STREAM ? qn4[grow[r] * 4 + i] : S.qnb[r][i];
+                const double bnd = __fma_rn(qn_[0], (double)km[0],
+                                    __fma_rn(qn_[1], (double)km[1], __fma_rn(qn_[2], (double)km[2], qn_[3] * (double)km[3])));
                 const double del = gam * bnd * (1.0 + 0x1p-40) + 0x1p-1060;
                 if (r >= RA) {
                     S.sb[buf][lane][r - RA] = make_double2(s, del);
@@ -576,7 +583,7 @@ __device__ __forceinline__ void decode_body(Params P) {
         // each tile (its weights are published by then) and one after the last. Straight-line
         // pairs keep vA and vB free of merges (no register copies).
         __syncthreads();  // prologue barrier (tables visible)
-        asm volatile("" : "+s"(q64b), "+s"(qn4));
+        asm volatile("" : "+s"(q64b));
         if constexpr (!STREAM)
 #pragma unroll
             for (int r = RA; r < RB; ++r) rflag[r] = S.qbad[min(r, nrow - 1)];

@@ -284,7 +284,9 @@ typedef const int32_t __attribute__((address_space(4))) cint_t;
 // all-zero block, and qn[row*4 + blk] = an upper bound of sum |q_i| (the fp64 sum has at most 32
 // roundings of relative size 2^-53 in any order, so times 1 + 2^-40 bounds it; NaN/inf propagate),
 // and qinfo[row*5 + 4] = the NaN/inf flag, which it also returns (the same in every lane).
-__device__ __forceinline__ int prep_row_store(const Params& P, int64_t row, int lane, uint32_t x0, uint32_t x1) {
+// *qn_blk receives the stored bound of the lane's own block (lane >> 4).
+__device__ __forceinline__ int prep_row_store(const Params& P, int64_t row, int lane, uint32_t x0, uint32_t x1,
+                                              double* qn_blk = nullptr) {
     const int blk = lane >> 4;
     const uint32_t x[2] = {x0, x1};
     int bad = 0, fmax = 0, fmin = 0x1FF;
@@ -308,10 +310,12 @@ __device__ __forceinline__ int prep_row_store(const Params& P, int64_t row, int 
         fmin = min(fmin, __shfl_xor(fmin, o, 64));
         aq += __shfl_xor(aq, o, 64);
     }
+    const double qb = aq * (1.0 + 0x1p-40);
     if ((lane & 15) == 0) {
         P.qinfo[row * 5 + blk] = (fmin == 0x1FF) ? (int32_t)0x80000000 : ((fmax << 16) | fmin);
-        P.qn[row * 4 + blk] = aq * (1.0 + 0x1p-40);
+        P.qn[row * 4 + blk] = qb;
     }
+    if (qn_blk) *qn_blk = qb;
     bad = wave_max_i(bad);
     if (lane == 0) P.qinfo[row * 5 + 4] = bad;
     return bad;
