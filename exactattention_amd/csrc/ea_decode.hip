@@ -297,6 +297,28 @@ __device__ __forceinline__ void decode_body(Params P) {
         }
     };
 
+    // exact products of q row r and key n, the key read from the cache (its LDS tile is being
+    // refilled by then: wave B's pairs, and wave A's with the equal-share plan); only pairs the
+    // fp64 interval cannot decide come here
+    auto exact_global = [&](int r, int n, double& ss, double& es, double& ea) __attribute__((always_inline)) {
+        const int64_t pg = P.bt ? (int64_t)btb[n >> pshift] : (int64_t)b;
+        const int sl = P.bt ? (n & pmask) : n;
+        const uint4* kp = (const uint4*)(kh + pg * kps2 + (int64_t)sl * kss2);
+        cdouble_t* qr = qrow64(r);
+        for (int c = 0; c < 16; ++c) {
+            const uint4 kv = kp[c];
+            const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                double e0, e1;
+                ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
+                ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
+                es += e0 + e1;
+                ea += fabs(e0) + fabs(e1);
+            }
+        }
+    };
+
     if (role == 0) {
         // ============ wave A: K tiles, scores, certified logits and weights of rows [0, RA)
         // uniform splits: this block converts its rows' q (the prep kernel's work for these rows;
@@ -352,11 +374,15 @@ __device__ __forceinline__ void decode_body(Params P) {
             if (it < ntiles) {
                 const int buf = it & 1;
                 const int n0 = k0 + it * DT;
-                const bool more = it + 1 < ntiles;
-                // K(it+1) into the buffer S(it-1) read; K(it) has landed once only K(it+1)'s 16
-                // instructions may be outstanding
-                if (more) {
-                    issue_k(n0 + DT, buf ^ 1);
+                // K(it+1) into the buffer S(it-1) read (with the equal-share plan it was issued right
+                // after the scores of tile it-1, K(1) here); K(it) has landed once only K(it+1)'s
+                // 16 instructions may be outstanding
+                if constexpr (STREAM) {
+                    if (it == 0 && ntiles > 1) issue_k(k0 + DT, 1);
+                } else {
+                    if (it + 1 < ntiles) issue_k(n0 + DT, buf ^ 1);
+                }
+                if (it + 1 < ntiles) {
                     wait_vm<16>();
                 } else {
                     wait_vm<0>();
@@ -433,11 +459,20 @@ __device__ __forceinline__ void decode_body(Params P) {
                 }
             }
 
+            // ---- equal-share plan: K(it+2) into the buffer the scores just read (their LDS reads
+            // are complete), so it loads during this tile's certification. Measured: C5 decode
+            // kernel -2.5%; the uniform grid (C2) +1%, so it keeps the issue at the next iteration.
+            if constexpr (STREAM) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                if (it + 2 < ntiles) issue_k(n0 + 2 * DT, buf);
+            }
             // ---- B: lane = key; rows [0, RA) certified here, the scores and bounds of rows
             // [RA, RB) handed to wave B
             __builtin_amdgcn_sched_barrier(0);
             const int n = n0 + lane;
-            // exact products of q row r and this lane's key, from the K tile in LDS
+            // exact products of q row r and this lane's key, from the K tile in LDS (the uniform
+            // grid: the buffer is not refilled before the next iteration)
             auto exact_lds = [&](int r, int, double& ss, double& es, double& ea) __attribute__((always_inline)) {
                 cdouble_t* qr = qrow64(r);
                 for (int c = 0; c < 16; ++c) {
@@ -468,7 +503,9 @@ __device__ __forceinline__ void decode_body(Params P) {
                     continue;
                 }
                 double f;
-                const double om = certify(r, n, s, del, exact_lds, &f);
+                double om;
+                if constexpr (STREAM) om = certify(r, n, s, del, exact_global, &f);
+                else om = certify(r, n, s, del, exact_lds, &f);
                 if (lane == 0) S.sc[buf][r] = f;
                 S.w[buf][lane][r] = om;
             }
@@ -495,26 +532,6 @@ __device__ __forceinline__ void decode_body(Params P) {
             issue_v(k0 + DT, vB, 0.0, 0.0);
         }
         // P of tile t with its V in vr; then V(t+2) into vr
-        // exact products of q row r and key n, the key read from the cache (its LDS tile is being
-        // refilled by then); only pairs the fp64 interval cannot decide come here
-        auto exact_global = [&](int r, int n, double& ss, double& es, double& ea) __attribute__((always_inline)) {
-            const int64_t pg = P.bt ? (int64_t)btb[n >> pshift] : (int64_t)b;
-            const int sl = P.bt ? (n & pmask) : n;
-            const uint4* kp = (const uint4*)(kh + pg * kps2 + (int64_t)sl * kss2);
-            cdouble_t* qr = qrow64(r);
-            for (int c = 0; c < 16; ++c) {
-                const uint4 kv = kp[c];
-                const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    double e0, e1;
-                    ss = two_sum(ss, qr[8 * c + 2 * j] * bf16lo_f64(wd[j]), &e0);
-                    ss = two_sum(ss, qr[8 * c + 2 * j + 1] * bf16hi_f64(wd[j]), &e1);
-                    es += e0 + e1;
-                    ea += fabs(e0) + fabs(e1);
-                }
-            }
-        };
         auto pv = [&](int t, u32x4 (&vr)[16]) __attribute__((always_inline)) {
             const int buf = t & 1;
             // rows [RA, RB) of tile t: certified here (lane = key) while V(t) is still landing;
