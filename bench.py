@@ -458,7 +458,7 @@ def baseline_split_line(prob: dict, ab: int, nsplit: int, steps: int, warmup: in
     return out
 
 
-def tree_line(steps: int, warmup: int) -> dict:
+def tree_line(steps: int, warmup: int, timers: bool = False) -> dict:
     """C4 speculative tree verification (8 sequences: an 8192-key prefix and a 16-node draft tree
     each, 16 query / 8 KV heads): 32 rows per (sequence, KV head) take the int8 prefill kernel
     with key splits, reading the K/V digit tiles from the cache the KV write path keeps (sliced
@@ -488,6 +488,8 @@ def tree_line(steps: int, warmup: int) -> dict:
             "kv_digits_slice_ms_all_keys": round(r["slice_ms"], 3),
             "bit_exact": r["bit_exact"], "fallback_rows_pct": round(100.0 * st["tier1_flagged"] / max(1, st["rows"]), 4),
             "input_gen_s": round(r["gen_s"], 1)}
+    if timers:
+        line["phase_clocks"] = prefill_timers(r)
     del r
     torch.cuda.empty_cache()
     return line
@@ -611,7 +613,7 @@ def prefill_timers(r: dict, reps: int = 3) -> dict:
     from exactattention_amd.hip import launch_hip
     tm = torch.zeros(16, dtype=torch.int64, device="cuda:0")
     for _ in range(reps):
-        launch_hip(r["dp"], r["ab"], timers=tm)
+        launch_hip(r["dp"], r["ab"], timers=tm, kv_digits=r["cache"])
     torch.cuda.synchronize()
     tv = tm.cpu().numpy().astype(float)
     tiles = max(1.0, tv[8])  # tiles counted once per wave
@@ -793,7 +795,7 @@ def main():
                     default=None,
                     help="run one workload only, no CPU baseline (for profiler runs)")
     ap.add_argument("--timers", action="store_true",
-                    help="after the timed steps, run 5 steps of the phase-clock build and report it")
+                    help="after the timed steps, run steps of the phase-clock build and report them (C2, C3, C4)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (scales rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -818,7 +820,7 @@ def main():
         print(json.dumps({"prefill": prefill_line(args.steps, args.warmup, args.timers)}), flush=True)
         return
     if args.only == "C4":
-        print(json.dumps({"tree_verify": tree_line(args.steps, args.warmup)}), flush=True)
+        print(json.dumps({"tree_verify": tree_line(args.steps, args.warmup, args.timers)}), flush=True)
         return
     if args.only == "C5":
         print(json.dumps({"long_context": long_context_line(args.steps, args.warmup)}), flush=True)

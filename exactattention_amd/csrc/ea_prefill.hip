@@ -427,6 +427,15 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
             tprev = t;
         }
     };
+    // the clocks into P.timers, once per wave (slot 8 counts the wave's tiles)
+    auto flush_timers = [&](int ntile) __attribute__((always_inline)) {
+        if (TIMERS && (threadIdx.x & 63) == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (i != 8) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
+            atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)ntile);
+        }
+    };
     constexpr int SPLIT = NWB / 2;         // waves per row group of 16 rows
     constexpr int RPB = 16 * NWB / SPLIT;  // rows per block (32)
     constexpr int NKT = 4 / SPLIT;         // key groups of 16 per wave
@@ -1034,6 +1043,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
                 }
             }
         }
+        flush_timers(nt);  // loop phases, prologue, drain and row totals (no final rounding here)
         return;
     }
     // ---- the last epoch plus the earlier ones, then RN(N/Z) per (row, channel), certified:
@@ -1120,13 +1130,7 @@ __global__ void __launch_bounds__(64 * NWB, 1) ea_pf_main(Params P) {
         }
     }
     tick(13);
-    if (TIMERS && lane == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
-#pragma unroll
-        for (int i = 9; i < 16; ++i) atomicAdd((unsigned long long*)&P.timers[i], (unsigned long long)tclk[i]);
-        atomicAdd((unsigned long long*)&P.timers[8], (unsigned long long)nt);
-    }
+    flush_timers(nt);
     if (P.stats) {
         const int st5 = wave_sum_i(nunc_s), st6 = wave_sum_i(nunc_w), st8 = wave_sum_i(nslow);
         if (lane == 0) {
