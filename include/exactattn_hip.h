@@ -99,7 +99,8 @@ typedef struct ea_options {
                                limit, flag 2), [15] steps whose decode kernel ran
                                the equal-share plan */
     void* const* events;    /* optional: 5 hipEvent_t recorded on `stream` before prep (the
-                               int8 path: q and K/V slicing), the tier-1 kernel, the combine (the
+                               int8 path: q and K/V slicing; none on the decode kernel's uniform
+                               grid, whose kernel converts q), the tier-1 kernel, the combine (the
                                int8 path: the merge of its key splits, when it has any) and tier 2,
                                and after tier 2 (per-kernel timing); a null entry is skipped (each
                                record is one more packet in the stream) */
@@ -151,7 +152,8 @@ int ea_hip_workspace_size(const ea_geometry* g, const ea_options* o, size_t* byt
  * every launch, src/exactattn/triton_kernels.py:1255-1280). */
 int ea_hip_reads_kv_digits(const ea_geometry* g, const ea_options* o, int32_t* reads);
 
-/* Enqueue one certified attention step on `stream`: q prep, tier-1 split kernel, combine with
+/* Enqueue one certified attention step on `stream`: q prep (inside the tier-1 kernel on the d =
+ * 128 decode kernel's uniform grid), tier-1 split kernel, combine with
  * certified rounding, device tier 2 for rows tier 1 could not certify. No host transfer, no
  * synchronisation, fixed grids: capturable in a hipGraph. The caller owns every buffer; the
  * library retains nothing after the work completes.
