@@ -21,8 +21,9 @@ from gen import KINDS, bf16
 
 pytestmark = pytest.mark.gpu
 
-# 1024 cases take about 10 s on an MI355X; EA_SWEEP_CASES=N runs N (20,000 pass in about 130 s),
-# starting at case EA_SWEEP_FIRST (default 0), so a longer run can cover indices not run before
+# 1024 cases take about 19 s on an MI355X; EA_SWEEP_CASES=N runs N (20,000 pass in about 350 s:
+# run those with pytest -s, which prints every case as it starts), starting at case
+# EA_SWEEP_FIRST (default 0), so a longer run can cover indices not run before
 NCASES = int(os.environ.get("EA_SWEEP_CASES", "1024"))
 FIRST = int(os.environ.get("EA_SWEEP_FIRST", "0"))
 
