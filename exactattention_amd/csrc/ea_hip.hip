@@ -1497,11 +1497,20 @@ int ea_hip_attention(const ea_geometry* g, const ea_buffers* bf, const ea_option
     if (!pl.prefill) {
         P.nsplit = pl.nsplit_gen;
         use_decode = pl.dq && pl.nseg > 0 && ea_decode_eligible(P);
-        int slots = 0;
-        if (use_decode && (rc = ea_decode_slots(P, &slots))) return rc;
+        int slots = 0, cus = 0;
+        if (use_decode && (rc = ea_decode_slots(P, &slots, &cus))) return rc;
         // the equal-share plan when the uniform split grid would take more than one round of
         // resident blocks (long or ragged contexts); otherwise one block per (unit, split)
+        P.dq_lead = 0;
         if (use_decode) P.pv_tiles = pl.split_len / EA_TILE;
+        if (use_decode && pl.nsplit_gen >= 2 && (int64_t)pl.dq_units * pl.nsplit_gen == slots && slots > cus) {
+            // exactly one round: the first wave's splits are weighted 5 against 4 (the decode
+            // kernel's uniform path); the longest is at most 5 / (5 + 4 (n - 1)) of the unit's
+            // tiles, plus one for the rounding
+            const int64_t tt = (int64_t)pl.nsplit_gen * (pl.split_len / EA_TILE), den = 5 + 4 * (int64_t)(pl.nsplit_gen - 1);
+            P.dq_lead = cus;
+            P.pv_tiles = (int32_t)((5 * tt + den - 1) / den + 1);
+        }
         if (use_decode && (int64_t)pl.dq_units * pl.nsplit_gen > slots) {
             const int64_t nb = std::min<int64_t>(slots, EA_DQ_MAX_BLOCKS);
             P.dq_stream = 1;

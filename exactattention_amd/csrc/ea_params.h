@@ -91,10 +91,16 @@ struct Params {
     int32_t dq_max_tiles;
     int32_t dq_rec_off;
     int32_t* dq_plan;
-    // Most 64-key tiles in one partial of the d = 128 decode kernel (split_len / 64, or the share
-    // of its equal-share plan); 0 when another kernel wrote the partials. The combine's error bound
-    // uses it: the kernel's lane chains hold at most 16 keys of each tile.
+    // Most 64-key tiles in one partial of the d = 128 decode kernel (split_len / 64, the longest
+    // weighted split, or the share of its equal-share plan); 0 when another kernel wrote the
+    // partials. The combine's error bound uses it: the kernel's lane chains hold at most 16 keys of
+    // each tile.
     int32_t pv_tiles;
+    // Uniform decode grid of exactly one round of resident blocks: the first dq_lead blocks in
+    // dispatch order (one per CU) run ahead of the rest (about 1.2x), so a unit's key range
+    // [0, nsplit split_len) is cut in whole tiles in proportion to weights 5 for its splits among
+    // them and 4 for the others. 0: equal splits of split_len.
+    int32_t dq_lead;
 };
 
 __device__ __forceinline__ int64_t row_index(const Params& P, int64_t b, int t, int hq) {
@@ -222,7 +228,7 @@ __device__ __forceinline__ int wave_sum_i(int x) {
 // current device at once. ea_launch_decode: P.dq_blocks blocks over the equal-share plan (0 or
 // -100 - e on a HIP error).
 int ea_decode_eligible(const Params& P);
-int ea_decode_slots(const Params& P, int* slots);
+int ea_decode_slots(const Params& P, int* slots, int* cus = nullptr);
 int ea_launch_decode(const Params& P, hipStream_t st);
 
 // int8-MFMA prefill path (ea_prefill.hip). A tile holds 64 keys of one segment:

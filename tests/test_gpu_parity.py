@@ -520,6 +520,25 @@ def test_decode_kernel_converts_q_rows_itself(gpu, splits):
     assert np.array_equal(got2, want)
 
 
+@pytest.mark.parametrize("B,S", [(64, 600), (16, 2048), (32, 1100)])
+def test_decode_lead_wave_splits(gpu, B, S):
+    """Uniform decode grids of exactly one round of resident blocks (MI355X: 1,024 = 512 units x
+    2 splits, 128 x 8, 256 x 4): the first wave's splits take weighted key ranges, so units see
+    1, 2 or no lead splits and cut their keys differently; ragged lengths leave some splits short
+    or empty. Bits equal the oracle, every row certified."""
+    rng = np.random.default_rng(7000 + B)
+    prob = _rand_problem(rng, "normal", "normal", B=B, T=1, Hq=16, Hkv=8, S=S, d=128, dv=128, causal=False)
+    prob["seq_len"][:] = rng.integers(S // 3, S + 1, size=B)
+    prob["seq_len"][0] = S
+    prob["kv_len"][:] = prob["seq_len"]  # one token per sequence
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    got, flags, st = _run(prob, ab)
+    assert st["decode_kernel_rows"] > 0 and st["decode_equal_share_steps"] == 0, st
+    assert not np.any(flags), st
+    assert np.array_equal(got, want)
+
+
 # ---------------------------------------------------------------------------------------------
 # the int8-MFMA prefill kernel (32 rows per block, balanced radix-256 digits)
 # ---------------------------------------------------------------------------------------------
