@@ -539,6 +539,40 @@ def test_decode_lead_wave_splits(gpu, B, S):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("seed", range(401, 409))
+def test_decode_lead_wave_random_grids(gpu, seed):
+    """Seeded random uniform decode grids of exactly 1,024 blocks (the weighted first wave on
+    MI355X): GQA group 1-4 (2-row blocks, several per segment, the XCD permutation when the
+    segment count is a multiple of 8), 1-2 tokens, ragged lengths, contiguous or paged NHD caches.
+    Bits equal the oracle and a one-split run, every row certified."""
+    rng = np.random.default_rng(seed)
+    while True:
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        grp = int(rng.choice([1, 2, 4]))
+        T = int(rng.choice([1, 2]))
+        B = int(rng.choice([4, 8, 16, 32, 64]))
+        nrb = (T * grp + 1) // 2
+        items = B * Hkv * nrb
+        if items in (64, 128, 256, 512) and B * T * Hkv * grp <= 2048:
+            break
+    ns = 1024 // items
+    S = ns * 64 * int(rng.integers(4, 9))
+    prob = _rand_problem(rng, "normal", "normal", B=B, T=T, Hq=Hkv * grp, Hkv=Hkv, S=S, d=128, dv=128)
+    prob["seq_len"][0] = S
+    prob["kv_len"][:] = np.clip(prob["seq_len"][:, None] - T + 1 + np.arange(T), 1, None).reshape(prob["kv_len"].shape)
+    if rng.random() < 0.5:
+        prob = problem.to_paged(prob, int(rng.choice([16, 64])), np.random.default_rng(seed), "NHD")
+    ab = default_alpha_bits(128)
+    want, _ = _oracle(prob, ab)
+    got, flags, st = _run(prob, ab)
+    assert st["decode_kernel_rows"] > 0 and st["decode_equal_share_steps"] == 0, (seed, st)
+    assert st["nsplit"] == ns, (seed, ns, st)
+    assert not np.any(flags), (seed, st)
+    assert np.array_equal(got, want), seed
+    got1, _, _ = _run(prob, ab, splits=1)
+    assert np.array_equal(got1, want), seed
+
+
 # ---------------------------------------------------------------------------------------------
 # the int8-MFMA prefill kernel (32 rows per block, balanced radix-256 digits)
 # ---------------------------------------------------------------------------------------------
