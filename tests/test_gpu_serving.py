@@ -233,11 +233,13 @@ def test_random_serving_sessions_match_oracle(gpu, seed):
 
 
 @pytest.mark.parametrize("B,H,Hkv,ql,kl,transposed", [(2, 4, 2, 5, 70, False), (1, 4, 2, 96, 96, True),
-                                                    (1, 2, 2, 1, 300, False), (3, 4, 1, 64, 130, True)])
+                                                    (1, 2, 2, 1, 300, False), (3, 4, 1, 64, 130, True),
+                                                    (2, 4, 2, 5, 70, True), (4, 8, 2, 1, 700, True)])
 def test_hf_attention_matches_oracle(gpu, B, H, Hkv, ql, kl, transposed):
     """serving.hf_attention (the transformers attention-function drop-in) against the oracle:
     queries at the end of the key range, GQA, decode (ql = 1), the int8 prefill path (ql >= 64),
-    and queries given as the transposed (B, ql, H, D) -> (B, H, ql, D) views transformers makes."""
+    and queries given as the transposed (B, ql, H, D) -> (B, H, ql, D) views transformers makes,
+    on both the prefill kernel and the decode kernel (which converts its strided q rows itself)."""
     import torch
     from exactattention_amd.formats import alpha_bits_for
     from exactattention_amd.serving import hf_attention
